@@ -1,0 +1,353 @@
+// extern "C" boundary (include/speculate_hip.h) over Model / Decoder.
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "../../include/speculate_hip.h"
+#include "sd_model.hpp"
+#include "sd_common.hpp"
+
+struct sd_model {
+    std::unique_ptr<sd::Model> model;
+    std::unique_ptr<sd::Decoder> dec;
+};
+
+static thread_local std::string g_err;
+
+template <typename F> static sd_status guard(F &&f) {
+    try {
+        f();
+        return SD_OK;
+    } catch (const sd::SamplingError &e) {
+        g_err = e.what();
+        return SD_ERR_SAMPLING;
+    } catch (const sd::RollbackError &e) {
+        g_err = e.what();
+        return SD_ERR_ROLLBACK;
+    } catch (const sd::ArgError &e) {
+        g_err = e.what();
+        return SD_ERR_ARG;
+    } catch (const sd::UnsupportedError &e) {
+        g_err = e.what();
+        return SD_ERR_UNSUPPORTED;
+    } catch (const sd::BackendError &e) {
+        g_err = e.what();
+        return SD_ERR_BACKEND;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return SD_ERR_BACKEND;
+    }
+}
+
+static void need(const sd_model *m) {
+    if (!m || !m->model) throw sd::ArgError("null model handle");
+}
+static void need_weights(const sd_model *m) {
+    need(m);
+    if (!m->model->weights_ready()) throw sd::ArgError("model weights are not fully set");
+}
+static void setdev(sd_model *m) { SD_HIP_CHECK(hipSetDevice(m->model->cfg.device)); }
+
+extern "C" {
+
+const char *sd_last_error(void) { return g_err.c_str(); }
+
+sd_status sd_model_create(const sd_config *cfg, sd_model **out) {
+    return guard([&] {
+        if (!cfg || !out) throw sd::ArgError("null argument");
+        *out = nullptr;
+        sd::ModelCfg c;
+        c.arch = cfg->arch;
+        if (c.arch != SD_ARCH_LLAMA && c.arch != SD_ARCH_QWEN2) throw sd::ArgError("unknown arch");
+        c.n_layers = cfg->n_layers;
+        c.hidden = cfg->hidden;
+        c.n_heads = cfg->n_heads;
+        c.n_kv_heads = cfg->n_kv_heads;
+        c.head_dim = cfg->head_dim;
+        c.ffn = cfg->ffn;
+        c.vocab = cfg->vocab;
+        c.rope_theta = cfg->rope_theta;
+        c.rms_eps = cfg->rms_eps;
+        c.ctx_len = cfg->ctx_len;
+        c.max_batch = cfg->max_batch;
+        c.tied_output = cfg->tied_output;
+        c.device = cfg->device;
+        if (c.hidden != c.n_heads * c.head_dim) throw sd::UnsupportedError("hidden must equal n_heads * head_dim");
+        auto h = std::make_unique<sd_model>();
+        h->model = std::make_unique<sd::Model>(c);
+        h->dec = std::make_unique<sd::Decoder>(h->model.get());
+        *out = h.release();
+    });
+}
+
+void sd_model_destroy(sd_model *m) { delete m; }
+
+sd_status sd_model_set_tensor(sd_model *m, int32_t layer, int32_t kind, int32_t fmt, const void *data, size_t bytes) {
+    return guard([&] {
+        need(m);
+        if (!data) throw sd::ArgError("null data");
+        m->model->set_tensor(layer, kind, fmt, data, bytes);
+        m->dec->last_valid = false;
+    });
+}
+
+sd_status sd_model_get_tensor(sd_model *m, int32_t layer, int32_t kind, void *out, size_t bytes) {
+    return guard([&] {
+        need(m);
+        if (!out) throw sd::ArgError("null output");
+        m->model->get_tensor(layer, kind, out, bytes);
+    });
+}
+
+sd_status sd_model_tensor_info(sd_model *m, int32_t layer, int32_t kind, int32_t *fmt, int32_t *rows, int32_t *cols,
+                               size_t *gguf_bytes) {
+    return guard([&] {
+        need(m);
+        int f, r, k;
+        size_t b;
+        m->model->tensor_info(layer, kind, &f, &r, &k, &b);
+        if (fmt) *fmt = f;
+        if (rows) *rows = r;
+        if (cols) *cols = k;
+        if (gguf_bytes) *gguf_bytes = b;
+    });
+}
+
+sd_status sd_model_synthesize(sd_model *m, int32_t mix, uint64_t seed, float stdv) {
+    return guard([&] {
+        need(m);
+        m->model->synthesize(mix, seed, stdv);
+        m->dec->last_valid = false;
+    });
+}
+
+sd_status sd_model_dequant_tensor(sd_model *m, int32_t layer, int32_t kind, float *out) {
+    return guard([&] {
+        need(m);
+        if (!out) throw sd::ArgError("null output");
+        m->model->dequant_tensor(layer, kind, out);
+    });
+}
+
+sd_status sd_model_qmatmul(sd_model *m, int32_t layer, int32_t kind, const float *x, size_t rows, float *y) {
+    return guard([&] {
+        need(m);
+        if (!x || !y) throw sd::ArgError("null argument");
+        m->model->qmatmul(layer, kind, x, (int)rows, y);
+    });
+}
+
+size_t sd_vocab_size(const sd_model *m) { return m && m->model ? (size_t)m->model->cfg.vocab : 0; }
+size_t sd_history_len(const sd_model *m) { return m && m->dec ? m->dec->history.size() : 0; }
+size_t sd_history(const sd_model *m, uint32_t *out, size_t cap) {
+    if (!m || !m->dec) return 0;
+    const size_t n = std::min(cap, m->dec->history.size());
+    if (out && n) std::memcpy(out, m->dec->history.data(), n * 4);
+    return n;
+}
+void sd_reset(sd_model *m) {
+    if (m && m->dec) m->dec->reset();
+}
+size_t sd_num_hidden_layers(const sd_model *m) { return m && m->model ? (size_t)m->model->cfg.n_layers : 0; }
+size_t sd_hidden_size(const sd_model *m) { return m && m->model ? (size_t)m->model->cfg.hidden : 0; }
+
+sd_status sd_observe(sd_model *m, const uint32_t *ids, size_t n) {
+    return guard([&] {
+        need_weights(m);
+        if (n && !ids) throw sd::ArgError("null ids");
+        setdev(m);
+        m->dec->observe(ids, n);
+    });
+}
+
+sd_status sd_next_logits(sd_model *m, float *out) {
+    return guard([&] {
+        need_weights(m);
+        setdev(m);
+        m->dec->next_logits(out);
+    });
+}
+
+sd_status sd_batched_logits(sd_model *m, const uint32_t *drafts, size_t k, float *out) {
+    return guard([&] {
+        need_weights(m);
+        if (k && !drafts) throw sd::ArgError("null drafts");
+        setdev(m);
+        m->dec->batched_logits(drafts, k, out);
+    });
+}
+
+sd_status sd_rollback_to(sd_model *m, size_t len) {
+    return guard([&] {
+        need(m);
+        m->dec->rollback_to(len);
+    });
+}
+
+sd_status sd_set_eos_token_ids(sd_model *m, const uint32_t *ids, size_t n) {
+    return guard([&] {
+        need(m);
+        if (n && !ids) throw sd::ArgError("null ids");
+        m->dec->eos.assign(ids, ids + n);
+    });
+}
+
+size_t sd_eos_token_ids(const sd_model *m, uint32_t *out, size_t cap) {
+    if (!m || !m->dec) return 0;
+    const size_t n = std::min(cap, m->dec->eos.size());
+    if (out && n) std::memcpy(out, m->dec->eos.data(), n * 4);
+    return m->dec->eos.size();
+}
+
+sd_status sd_tree_logits_keep_kv(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                 float *out_logits, float *out_hidden) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents) throw sd::ArgError("null tree");
+        setdev(m);
+        m->dec->tree_logits_keep_kv(tokens, parents, n, out_logits, out_hidden);
+    });
+}
+
+sd_status sd_tree_logits(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents) throw sd::ArgError("null tree");
+        setdev(m);
+        m->dec->tree_logits(tokens, parents, n, out_logits);
+    });
+}
+
+sd_status sd_commit_tree_path(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                              const uint32_t *accepted, size_t n_accepted) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents || (n_accepted && !accepted)) throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->commit_tree_path(tokens, parents, n, accepted, n_accepted);
+    });
+}
+
+sd_status sd_last_hidden_state(sd_model *m, float *out) {
+    return guard([&] {
+        need_weights(m);
+        setdev(m);
+        m->dec->last_hidden_state(out);
+    });
+}
+
+sd_status sd_observe_returning_last_hidden(sd_model *m, const uint32_t *ids, size_t n, float *out) {
+    return guard([&] {
+        need_weights(m);
+        if (n && !ids) throw sd::ArgError("null ids");
+        setdev(m);
+        m->dec->observe_returning_last_hidden(ids, n, out);
+    });
+}
+
+sd_status sd_last_hidden_states_multi(sd_model *m, const uint32_t *layers, size_t n_layers, float *out_final,
+                                      float *out_layers) {
+    return guard([&] {
+        need_weights(m);
+        if (n_layers && !layers) throw sd::ArgError("null layers");
+        setdev(m);
+        m->dec->last_hidden_states_multi(layers, n_layers, out_final, out_layers);
+    });
+}
+
+sd_status sd_apply_lm_head(sd_model *m, const float *hidden, size_t rows, float *out) {
+    return guard([&] {
+        need_weights(m);
+        if (!hidden || !out) throw sd::ArgError("null argument");
+        setdev(m);
+        m->model->lm_head_rows(hidden, (int)rows, out);
+    });
+}
+
+sd_status sd_embed_tokens(sd_model *m, const uint32_t *ids, size_t n, float *out) {
+    return guard([&] {
+        need_weights(m);
+        if (!ids || !out) throw sd::ArgError("null argument");
+        setdev(m);
+        std::vector<int> v(ids, ids + n);
+        for (size_t i = 0; i < n; i++)
+            if (ids[i] >= (uint32_t)m->model->cfg.vocab) throw sd::ArgError("token id out of range");
+        m->model->embed_rows(v.data(), (int)n, out);
+    });
+}
+
+sd_status sd_verify_greedy_linear(sd_model *m, const uint32_t *drafts, size_t k, uint32_t *commits,
+                                  size_t *n_commit, size_t *n_accepted) {
+    return guard([&] {
+        need_weights(m);
+        if ((k && !drafts) || !commits || !n_commit || !n_accepted) throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_greedy_linear(drafts, k, commits, n_commit, n_accepted);
+    });
+}
+
+sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                int32_t strict, uint32_t *path, size_t *path_len, uint32_t *bonus,
+                                int32_t *bonus_node) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents || !path || !path_len || !bonus || !bonus_node) throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_greedy_tree(tokens, parents, n, strict, path, path_len, bonus, bonus_node);
+    });
+}
+
+sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n) {
+    return guard([&] {
+        need(m);
+        if (!out) throw sd::ArgError("null output");
+        setdev(m);
+        m->dec->argmax_rows(out, n);
+    });
+}
+
+sd_status sd_prime_synthetic(sd_model *m, const uint32_t *ids, size_t n, uint64_t kv_seed) {
+    return guard([&] {
+        need(m);
+        if (!ids) throw sd::ArgError("null ids");
+        setdev(m);
+        m->dec->prime_synthetic(ids, n, kv_seed);
+    });
+}
+
+sd_status sd_profile_enable(sd_model *m, int32_t on) {
+    return guard([&] {
+        need(m);
+        m->model->prof_on = on != 0;
+    });
+}
+
+size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap) {
+    if (!m || !m->model) return 0;
+    auto &P = m->model->prof;
+    (void)hipSetDevice(m->model->cfg.device);
+    (void)hipStreamSynchronize(m->model->st);
+    size_t n = 0;
+    for (auto &e : P) {
+        if (n >= cap) break;
+        int c = e.name == "qkv" ? 0 : e.name == "wo" ? 1 : e.name == "gate_up" ? 2 : e.name == "down" ? 3 : 4;
+        float t = 0.f;
+        (void)hipEventElapsedTime(&t, e.a, e.b);
+        if (cls) cls[n] = c;
+        if (bytes) bytes[n] = e.bytes;
+        if (ms) ms[n] = t;
+        n++;
+    }
+    m->model->prof_reset();
+    return n;
+}
+
+sd_status sd_synchronize(sd_model *m) {
+    return guard([&] {
+        need(m);
+        setdev(m);
+        SD_HIP_CHECK(hipStreamSynchronize(m->model->st));
+    });
+}
+
+}  // extern "C"

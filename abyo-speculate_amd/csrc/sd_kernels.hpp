@@ -1,0 +1,61 @@
+// Host-side launchers of the HIP kernels (one translation unit per kernel family).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdexcept>
+#include <string>
+
+namespace sd {
+
+struct BackendError : std::runtime_error {
+    explicit BackendError(const std::string &m) : std::runtime_error(m) {}
+};
+
+// ---- sd_synth.hip ----
+void launch_synth_quant(int fmt, uint8_t *out, int64_t rows, int64_t K, uint64_t seed, float mult, hipStream_t st);
+void launch_synth_f32(float *out, int64_t n, uint64_t seed, float mult, hipStream_t st);
+void launch_fill_f32(float *out, int64_t n, float v, hipStream_t st);
+void launch_fill_kv(uint16_t *kv, int L, int n_kv, int64_t cap, int hd, int P, uint64_t seed, float mult,
+                    hipStream_t st);
+// GGUF block bytes -> f32, exact (input must be in GGUF layout)
+void launch_dequant(int fmt, const uint8_t *w, int64_t n_elems, float *y, hipStream_t st);
+
+// ---- sd_layout.hip: GGUF rows <-> device rows (Q6_K / Q8_0 regrouped into planes) ----
+void launch_gguf_to_dev(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st);
+void launch_dev_to_gguf(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st);
+
+// ---- sd_qgemm.hip: fused dequant-matmul on MFMA ----
+enum GemmMode : int { GM_STORE = 0, GM_RESID = 1, GM_SWIGLU = 2, GM_LOGITS = 3 };
+
+struct GemmSeg {
+    const uint8_t *w;  // device layout rows, stride dev_row_stride(fmt, K)
+    int fmt;
+    int rows;          // multiple of 16
+    int tile0;         // first 16-row tile of this segment in the launch
+    float *out;        // GM_STORE/GM_RESID/GM_LOGITS: out[m*ldo + col0 + n]
+    int ldo;
+    int col0;
+    const float *bias; // optional per-row bias (GM_STORE)
+};
+
+struct GemmParams {
+    GemmSeg seg[4];
+    int nseg;
+    int ntiles;              // total 16-row tiles (sum over segments)
+    const uint16_t *xp;      // fp16 activations, fragment layout, [Mpad][K]
+    int K;
+    int M;
+    int mode;
+    uint16_t *act;           // GM_SWIGLU: fp16 fragment-layout output [Mpad][act_ld]
+    int act_ld;
+    float *amax_v;           // GM_LOGITS: per (token, workgroup) argmax partials
+    int *amax_i;
+    int amax_ld;             // = number of workgroups
+};
+
+// Launches y = x . W^T over all segments.  Chooses the tile shape from M.
+// Returns the number of workgroups launched (GM_LOGITS partial count).
+int launch_qgemm(const GemmParams &p, hipStream_t st);
+int qgemm_workgroups(const GemmParams &p);
+
+}  // namespace sd

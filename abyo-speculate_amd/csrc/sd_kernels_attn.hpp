@@ -1,0 +1,39 @@
+// Parameter blocks and launchers of the attention kernels (sd_attn.hip).
+#pragma once
+#include "sd_kernels.hpp"
+
+namespace sd {
+
+struct RopeKvParams {
+    const float *qkv;   // [M][ld_qkv] f32: q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)
+    int ld_qkv;
+    const int *pos;     // [M] absolute positions
+    const float *cos_t, *sin_t;  // [ctx][hd/2]
+    uint16_t *q16;      // [n_heads][M][hd] fp16 (rotated q)
+    uint16_t *kc, *vc;  // this layer's cache [n_kv][cap][hd]
+    int64_t cap;
+    int P, M, n_heads, n_kv, hd;
+    int interleaved;    // 1: rope_i pairs (2i, 2i+1) (Llama); 0: rope pairs (i, i+hd/2) (Qwen2)
+};
+
+struct AttnParams {
+    const uint16_t *q16;
+    const uint16_t *kc, *vc;
+    int64_t cap;
+    const uint64_t *mask;  // [M][mask_words]
+    int mask_words;
+    int P, M, n_heads, n_kv, n_rep, hd;
+    int cps;               // 64-key chunks per split (a function of P only)
+    float scale;           // 1/sqrt(hd)
+    float *part_o;         // [nsplit][n_heads][M][hd]
+    float *part_ml;        // [nsplit][n_heads][M][2]
+    uint16_t *out16;       // [M][out_ld] fp16 fragment layout (input of wo)
+    int out_ld;
+};
+
+void launch_rope_kv(const RopeKvParams &p, hipStream_t st);
+int attn_chunks_per_split(int P, int n_kv);
+int attn_num_splits(int P, int M, int cps);
+void launch_attention(const AttnParams &p, hipStream_t st);
+
+}  // namespace sd

@@ -1,0 +1,18 @@
+// Launchers of the element-wise / reduction kernels (sd_elem.hip).
+#pragma once
+#include "sd_kernels.hpp"
+
+namespace sd {
+
+// exact f32 dequantisation of device-layout rows
+void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y, hipStream_t st);
+void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st);
+void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
+                    hipStream_t st);
+void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st);
+void launch_argmax_reduce(const float *pv, const int *pi, int nwg, int M, int *out, hipStream_t st);
+void launch_argmax_rows(const float *x, int64_t ld, int n, int M, int *out, hipStream_t st);
+void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int hd, int P, const int *src, int n,
+                         hipStream_t st);
+
+}  // namespace sd

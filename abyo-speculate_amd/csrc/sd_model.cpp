@@ -1,0 +1,973 @@
+// Host runtime of the target-verify path.  See sd_model.hpp.
+#include "sd_model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "sd_common.hpp"
+
+namespace sd {
+
+static const bool kIsF32Kind[K_NUM] = {false, false, true, false, false, false, false,
+                                       false, false, false, true, true, true, true, true};
+
+static void shape_of(const ModelCfg &c, int kind, int &rows, int &K) {
+    const int H = c.hidden, F = c.ffn;
+    switch (kind) {
+    case K_TOK_EMBD: case K_OUTPUT: rows = c.vocab; K = H; break;
+    case K_OUTPUT_NORM: case K_ATTN_NORM: case K_FFN_NORM: rows = 1; K = H; break;
+    case K_ATTN_Q: rows = c.q_dim(); K = H; break;
+    case K_ATTN_K: case K_ATTN_V: rows = c.kv_dim(); K = H; break;
+    case K_ATTN_O: rows = H; K = c.q_dim(); break;
+    case K_FFN_GATE: case K_FFN_UP: rows = F; K = H; break;
+    case K_FFN_DOWN: rows = H; K = F; break;
+    case K_BQ: rows = 1; K = c.q_dim(); break;
+    case K_BK: case K_BV: rows = 1; K = c.kv_dim(); break;
+    default: throw ArgError("unknown tensor kind");
+    }
+}
+
+static int64_t gguf_row_bytes(int fmt, int64_t K) {
+    if (fmt == F32) return 4 * K;
+    return K / fmt_block_elems(fmt) * fmt_block_bytes(fmt);
+}
+
+template <typename T> static T *dalloc(size_t n) {
+    void *p = nullptr;
+    SD_HIP_CHECK(hipMalloc(&p, n * sizeof(T) + 256));
+    SD_HIP_CHECK(hipMemset(p, 0, n * sizeof(T) + 256));
+    return (T *)p;
+}
+
+Model::Model(const ModelCfg &c) : cfg(c) {
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn <= 0 ||
+        c.vocab <= 0 || c.ctx_len <= 0)
+        throw ArgError("config: all sizes must be positive");
+    if (c.n_heads % c.n_kv_heads) throw ArgError("config: n_heads must be a multiple of n_kv_heads");
+    if (c.head_dim != 64 && c.head_dim != 128) throw UnsupportedError("config: head_dim must be 64 or 128");
+    if (c.hidden % 256 || c.ffn % 256 || c.q_dim() % 256) throw UnsupportedError("config: hidden/ffn/q_dim must be multiples of 256");
+    if (c.kv_dim() % 32 || c.vocab % 32) throw UnsupportedError("config: kv_dim and vocab must be multiples of 32");
+    if (c.max_batch < 1 || c.max_batch > 128) throw ArgError("config: max_batch must be in [1, 128]");
+    SD_HIP_CHECK(hipSetDevice(c.device));
+    SD_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    lw.resize(c.n_layers);
+    alloc_buffers();
+}
+
+Model::~Model() {
+    hipSetDevice(cfg.device);
+    if (st) hipStreamSynchronize(st);
+    auto F = [](void *p) {
+        if (p) hipFree(p);
+    };
+    for (auto &L : lw)
+        for (auto &t : L) F(t.d);
+    for (auto &t : gw) F(t.d);
+    for (void *p : {(void *)kv, (void *)cos_t, (void *)sin_t, (void *)h, (void *)qkv, (void *)logits,
+                    (void *)hidden_out, (void *)last_row, (void *)part_o, (void *)part_ml, (void *)amax_v,
+                    (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids, (void *)d_pos,
+                    (void *)d_src, (void *)d_mask, (void *)xp, (void *)ap, (void *)act, (void *)q16})
+        F(p);
+    if (h_stage) hipHostFree(h_stage);
+    if (stage_ev) hipEventDestroy(stage_ev);
+    for (auto &e : prof) {
+        hipEventDestroy(e.a);
+        hipEventDestroy(e.b);
+    }
+    if (st) hipStreamDestroy(st);
+}
+
+void Model::alloc_buffers() {
+    const ModelCfg &c = cfg;
+    const int Mx = c.max_batch, Mp = 128 + 16;  // padded rows (16-token MFMA tiles + last-row slack)
+    cap = (int64_t)c.ctx_len + 128;
+    kv = dalloc<uint16_t>((size_t)c.n_layers * 2 * c.n_kv_heads * cap * c.head_dim);
+    // RoPE tables (quantized_llama_local.rs:189-205): host f32 powf/cosf/sinf
+    {
+        const int half = c.head_dim / 2;
+        std::vector<float> theta(half), ct((size_t)cap * half), stt((size_t)cap * half);
+        for (int i = 0; i < half; i++) theta[i] = 1.0f / powf(c.rope_theta, (float)(2 * i) / (float)c.head_dim);
+        for (int64_t t = 0; t < cap; t++)
+            for (int i = 0; i < half; i++) {
+                const float a = (float)t * theta[i];
+                ct[t * half + i] = cosf(a);
+                stt[t * half + i] = sinf(a);
+            }
+        cos_t = dalloc<float>(ct.size());
+        sin_t = dalloc<float>(stt.size());
+        SD_HIP_CHECK(hipMemcpy(cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));
+        SD_HIP_CHECK(hipMemcpy(sin_t, stt.data(), stt.size() * 4, hipMemcpyHostToDevice));
+    }
+    const int qkvd = c.q_dim() + 2 * c.kv_dim();
+    xp_ld = std::max(c.hidden, c.q_dim());
+    ap_ld = c.q_dim();
+    act_ld = c.ffn;
+    h = dalloc<float>((size_t)Mx * c.hidden);
+    qkv = dalloc<float>((size_t)Mx * qkvd);
+    xp = dalloc<uint16_t>((size_t)Mp * xp_ld);
+    ap = dalloc<uint16_t>((size_t)Mp * ap_ld);
+    act = dalloc<uint16_t>((size_t)Mp * act_ld);
+    q16 = dalloc<uint16_t>((size_t)c.n_heads * Mx * c.head_dim);
+    nsplit_max = 256 / c.n_kv_heads + (Mx + 63) / 64 + 2;
+    part_o = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * c.head_dim);
+    part_ml = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * 2);
+    logits = dalloc<float>((size_t)Mx * c.vocab);
+    hidden_out = dalloc<float>((size_t)Mx * c.hidden);
+    last_row = dalloc<float>((size_t)c.vocab);
+    amax_ld = c.vocab / 16;
+    amax_v = dalloc<float>((size_t)Mx * amax_ld);
+    amax_i = dalloc<int>((size_t)Mx * amax_ld);
+    argmax = dalloc<int>(Mx);
+    collect_buf = dalloc<float>((size_t)c.n_layers * c.hidden);
+    d_ids = dalloc<int>(Mx);
+    d_pos = dalloc<int>(Mx);
+    d_src = dalloc<int>(Mx);
+    d_mask = dalloc<uint64_t>((size_t)Mx * 2);
+    h_stage_bytes = (size_t)Mx * (3 * sizeof(int) + 2 * sizeof(uint64_t)) + 256;
+    SD_HIP_CHECK(hipHostMalloc((void **)&h_stage, h_stage_bytes, hipHostMallocDefault));
+    SD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev, hipEventDisableTiming));
+}
+
+void Model::stage_wait() { SD_HIP_CHECK(hipEventSynchronize(stage_ev)); }
+void Model::stage_done() { SD_HIP_CHECK(hipEventRecord(stage_ev, st)); }
+
+bool Model::weights_ready() const {
+    static const int need[] = {K_ATTN_Q, K_ATTN_K, K_ATTN_V, K_ATTN_O, K_FFN_GATE, K_FFN_UP, K_FFN_DOWN,
+                               K_ATTN_NORM, K_FFN_NORM};
+    if (!gw[K_TOK_EMBD].set() || !gw[K_OUTPUT_NORM].set()) return false;
+    if (!cfg.tied_output && !gw[K_OUTPUT].set()) return false;
+    for (auto &L : lw) {
+        for (int k : need)
+            if (!L[k].set()) return false;
+        if (cfg.arch == 1 && (!L[K_BQ].set() || !L[K_BK].set() || !L[K_BV].set())) return false;
+    }
+    return true;
+}
+
+static void check_fmt(int kind, int fmt, int K) {
+    if (kIsF32Kind[kind]) {
+        if (fmt != F32) throw ArgError("norm/bias tensors must be F32");
+        return;
+    }
+    if (fmt != Q4_K && fmt != Q5_K && fmt != Q6_K && fmt != Q8_0)
+        throw UnsupportedError("matrix tensors must be Q4_K, Q5_K, Q6_K or Q8_0");
+    if (K % 256) throw UnsupportedError("K must be a multiple of 256");
+}
+
+static DevTensor &slot(Model &m, int layer, int kind) {
+    if (kind < 0 || kind >= K_NUM) throw ArgError("unknown tensor kind");
+    if (layer < -1 || layer >= m.cfg.n_layers) throw ArgError("layer out of range");
+    const bool global = kind <= K_OUTPUT_NORM;
+    if (global != (layer == -1)) throw ArgError("global tensors use layer -1, per-layer tensors 0..n_layers-1");
+    if (kind >= K_BQ && m.cfg.arch != 1) throw ArgError("QKV bias tensors exist only for qwen2");
+    return global ? m.gw[kind] : m.lw[layer][kind];
+}
+
+void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t bytes) {
+    DevTensor &t = slot(*this, layer, kind);
+    int rows, K;
+    shape_of(cfg, kind, rows, K);
+    check_fmt(kind, fmt, K);
+    const size_t want = (size_t)rows * gguf_row_bytes(fmt, K);
+    if (bytes != want) throw ArgError("tensor byte size does not match its shape and format");
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    if (t.d) {
+        SD_HIP_CHECK(hipFree(t.d));
+        t.d = nullptr;
+    }
+    t.fmt = fmt;
+    t.rows = rows;
+    t.K = K;
+    t.bytes = (size_t)rows * dev_row_stride(fmt, K);
+    t.d = dalloc<uint8_t>(t.bytes);
+    if (fmt == F32 || fmt == Q4_K || fmt == Q5_K) {
+        // identical layout (row strides are already 16-byte multiples)
+        SD_HIP_CHECK(hipMemcpy(t.d, host, bytes, hipMemcpyHostToDevice));
+    } else {
+        uint8_t *tmp = dalloc<uint8_t>(bytes);
+        SD_HIP_CHECK(hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice));
+        launch_gguf_to_dev(fmt, tmp, t.d, rows, K, st);
+        SD_HIP_CHECK(hipStreamSynchronize(st));
+        SD_HIP_CHECK(hipFree(tmp));
+    }
+}
+
+void Model::tensor_info(int layer, int kind, int *fmt, int *rows, int *K, size_t *gbytes) {
+    DevTensor &t = slot(*this, layer, kind);
+    if (!t.set()) throw ArgError("tensor not set");
+    *fmt = t.fmt;
+    *rows = t.rows;
+    *K = t.K;
+    *gbytes = (size_t)t.rows * gguf_row_bytes(t.fmt, t.K);
+}
+
+void Model::get_tensor(int layer, int kind, void *host, size_t bytes) {
+    DevTensor &t = slot(*this, layer, kind);
+    if (!t.set()) throw ArgError("tensor not set");
+    const size_t g = (size_t)t.rows * gguf_row_bytes(t.fmt, t.K);
+    if (bytes != g) throw ArgError("buffer size does not match the tensor");
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    if (t.fmt == F32 || t.fmt == Q4_K || t.fmt == Q5_K) {
+        SD_HIP_CHECK(hipMemcpy(host, t.d, g, hipMemcpyDeviceToHost));
+    } else {
+        uint8_t *tmp = dalloc<uint8_t>(g);
+        launch_dev_to_gguf(t.fmt, t.d, tmp, t.rows, t.K, st);
+        SD_HIP_CHECK(hipStreamSynchronize(st));
+        SD_HIP_CHECK(hipMemcpy(host, tmp, g, hipMemcpyDeviceToHost));
+        SD_HIP_CHECK(hipFree(tmp));
+    }
+}
+
+void Model::dequant_tensor(int layer, int kind, float *host) {
+    DevTensor &t = slot(*this, layer, kind);
+    if (!t.set()) throw ArgError("tensor not set");
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    const size_t n = (size_t)t.rows * t.K;
+    float *y = dalloc<float>(n);
+    launch_dequant_dev(t.fmt, t.d, t.rows, t.K, y, st);
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+    SD_HIP_CHECK(hipMemcpy(host, y, n * 4, hipMemcpyDeviceToHost));
+    SD_HIP_CHECK(hipFree(y));
+}
+
+// Q4_K_M mix (llama.cpp's use_more_bits rule for attn_v / ffn_down) and the others
+static int mix_fmt(int mix, int n_layers, int layer, int kind) {
+    if (kIsF32Kind[kind]) return F32;
+    if (mix == 0) return Q4_K;
+    if (mix == 1) {
+        const int n = n_layers, i = layer;
+        const bool more = i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2;
+        if ((kind == K_ATTN_V || kind == K_FFN_DOWN) && more) return Q6_K;
+        return Q4_K;
+    }
+    if (mix == 2) {
+        if (kind == K_ATTN_Q || kind == K_ATTN_K || kind == K_ATTN_V || kind == K_ATTN_O) return Q5_K;
+        return Q8_0;
+    }
+    if (mix == 3) return Q6_K;
+    if (mix == 4) return Q5_K;
+    if (mix == 5) return Q8_0;
+    throw ArgError("unknown quantisation mix");
+}
+
+void Model::synthesize(int mix, uint64_t seed, float stdv) {
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    const float mult = (float)((double)stdv * std::sqrt(3.0) / 65536.0);
+    auto make = [&](int layer, int kind) {
+        DevTensor &t = slot(*this, layer, kind);
+        int rows, K;
+        shape_of(cfg, kind, rows, K);
+        const int fmt = mix_fmt(mix, cfg.n_layers, layer, kind);
+        if (t.d) SD_HIP_CHECK(hipFree(t.d));
+        t.fmt = fmt;
+        t.rows = rows;
+        t.K = K;
+        t.bytes = (size_t)rows * dev_row_stride(fmt, K);
+        t.d = dalloc<uint8_t>(t.bytes);
+        const uint64_t ts = tensor_seed(seed, layer, kind);
+        if (kind == K_OUTPUT_NORM || kind == K_ATTN_NORM || kind == K_FFN_NORM) {
+            launch_fill_f32((float *)t.d, (int64_t)rows * K, 1.0f, st);
+        } else if (fmt == F32) {
+            launch_synth_f32((float *)t.d, (int64_t)rows * K, ts, mult, st);
+        } else if (fmt == Q4_K || fmt == Q5_K) {
+            launch_synth_quant(fmt, t.d, rows, K, ts, mult, st);
+        } else {
+            const size_t g = (size_t)rows * gguf_row_bytes(fmt, K);
+            uint8_t *tmp = dalloc<uint8_t>(g);
+            launch_synth_quant(fmt, tmp, rows, K, ts, mult, st);
+            launch_gguf_to_dev(fmt, tmp, t.d, rows, K, st);
+            SD_HIP_CHECK(hipStreamSynchronize(st));
+            SD_HIP_CHECK(hipFree(tmp));
+        }
+    };
+    make(-1, K_TOK_EMBD);
+    make(-1, K_OUTPUT_NORM);
+    if (!cfg.tied_output) make(-1, K_OUTPUT);
+    for (int l = 0; l < cfg.n_layers; l++) {
+        for (int k = K_ATTN_Q; k <= K_FFN_NORM; k++) make(l, k);
+        if (cfg.arch == 1)
+            for (int k = K_BQ; k <= K_BV; k++) make(l, k);
+    }
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Model::fill_kv_synthetic(int P, uint64_t seed) {
+    if (P < 0 || P > cfg.ctx_len) throw ArgError("prefix longer than the KV capacity");
+    const float mult = (float)(std::sqrt(3.0) / 65536.0);
+    launch_fill_kv(kv, cfg.n_layers, cfg.n_kv_heads, cap, cfg.head_dim, P, seed, mult, st);
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Model::prof_reset() {
+    for (auto &e : prof) {
+        hipEventDestroy(e.a);
+        hipEventDestroy(e.b);
+    }
+    prof.clear();
+}
+
+void Model::run_gemm(GemmParams &p, const char *name, double bytes) {
+    if (prof_on) {
+        ProfEntry e;
+        e.name = name;
+        e.bytes = bytes;
+        SD_HIP_CHECK(hipEventCreate(&e.a));
+        SD_HIP_CHECK(hipEventCreate(&e.b));
+        SD_HIP_CHECK(hipEventRecord(e.a, st));
+        launch_qgemm(p, st);
+        SD_HIP_CHECK(hipEventRecord(e.b, st));
+        prof.push_back(e);
+    } else {
+        launch_qgemm(p, st);
+    }
+}
+
+static double wbytes(const DevTensor &t) { return (double)t.rows * gguf_row_bytes(t.fmt, t.K); }
+
+static GemmSeg seg_of(const DevTensor &t, int tile0, float *out, int ldo, int col0, const float *bias) {
+    GemmSeg s;
+    s.w = t.d;
+    s.fmt = t.fmt;
+    s.rows = t.rows;
+    s.tile0 = tile0;
+    s.out = out;
+    s.ldo = ldo;
+    s.col0 = col0;
+    s.bias = bias;
+    return s;
+}
+
+void Model::qmatmul(int layer, int kind, const float *x, int M, float *y) {
+    DevTensor &t = slot(*this, layer, kind);
+    if (!t.set() || t.fmt == F32) throw ArgError("qmatmul needs a quantised matrix tensor");
+    if (M < 1 || M > cfg.max_batch) throw ArgError("M out of range");
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    float *dx = dalloc<float>((size_t)M * t.K);
+    float *dy = dalloc<float>((size_t)M * t.rows);
+    uint16_t *dxp = dalloc<uint16_t>((size_t)(128 + 16) * t.K);
+    SD_HIP_CHECK(hipMemcpy(dx, x, (size_t)M * t.K * 4, hipMemcpyHostToDevice));
+    launch_to_frag16(dx, M, t.K, dxp, t.K, st);
+    GemmParams p{};
+    p.seg[0] = seg_of(t, 0, dy, t.rows, 0, nullptr);
+    p.nseg = 1;
+    p.ntiles = t.rows / 16;
+    p.xp = dxp;
+    p.K = t.K;
+    p.M = M;
+    p.mode = GM_STORE;
+    launch_qgemm(p, st);
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+    SD_HIP_CHECK(hipMemcpy(y, dy, (size_t)M * t.rows * 4, hipMemcpyDeviceToHost));
+    hipFree(dx);
+    hipFree(dy);
+    hipFree(dxp);
+}
+
+void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P,
+                    int logits_mode, bool want_hidden, const std::vector<int> &collect, float *collect_out) {
+    const ModelCfg &c = cfg;
+    if (M < 1 || M > c.max_batch) throw ArgError("forward: M out of range");
+    if (P + M > c.ctx_len) throw ArgError("forward: KV capacity exceeded");
+    if (mask_words < 1 || mask_words > 2) throw ArgError("forward: mask words");
+    SD_HIP_CHECK(hipSetDevice(c.device));
+    // stage ids | pos | mask in pinned memory, one H2D copy each
+    stage_wait();
+    std::memcpy(h_stage, ids, M * sizeof(int));
+    std::memcpy(h_stage + c.max_batch, pos, M * sizeof(int));
+    uint64_t *hm = (uint64_t *)(h_stage + 3 * c.max_batch + (c.max_batch & 1));
+    std::memcpy(hm, mask, (size_t)M * mask_words * sizeof(uint64_t));
+    SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, M * sizeof(int), hipMemcpyHostToDevice, st));
+    SD_HIP_CHECK(hipMemcpyAsync(d_pos, h_stage + c.max_batch, M * sizeof(int), hipMemcpyHostToDevice, st));
+    SD_HIP_CHECK(hipMemcpyAsync(d_mask, hm, (size_t)M * mask_words * sizeof(uint64_t), hipMemcpyHostToDevice, st));
+    stage_done();
+
+    const int H = c.hidden, QD = c.q_dim(), KVD = c.kv_dim(), QKVD = QD + 2 * KVD;
+    launch_embed(gw[K_TOK_EMBD].fmt, gw[K_TOK_EMBD].d, H, d_ids, M, h, st);
+    const int cps = attn_chunks_per_split(P, c.n_kv_heads);
+    if (attn_num_splits(P, M, cps) > nsplit_max) throw BackendError("attention split count exceeds workspace");
+    for (int l = 0; l < c.n_layers; l++) {
+        auto &L = lw[l];
+        launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
+        {
+            GemmParams p{};
+            const bool bias = c.arch == 1;
+            int t0 = 0;
+            p.seg[0] = seg_of(L[K_ATTN_Q], t0, qkv, QKVD, 0, bias ? (const float *)L[K_BQ].d : nullptr);
+            t0 += L[K_ATTN_Q].rows / 16;
+            p.seg[1] = seg_of(L[K_ATTN_K], t0, qkv, QKVD, QD, bias ? (const float *)L[K_BK].d : nullptr);
+            t0 += L[K_ATTN_K].rows / 16;
+            p.seg[2] = seg_of(L[K_ATTN_V], t0, qkv, QKVD, QD + KVD, bias ? (const float *)L[K_BV].d : nullptr);
+            t0 += L[K_ATTN_V].rows / 16;
+            p.nseg = 3;
+            p.ntiles = t0;
+            p.xp = xp;
+            p.K = H;
+            p.M = M;
+            p.mode = GM_STORE;
+            run_gemm(p, "qkv", wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
+        }
+        {
+            RopeKvParams r{};
+            r.qkv = qkv;
+            r.ld_qkv = QKVD;
+            r.pos = d_pos;
+            r.cos_t = cos_t;
+            r.sin_t = sin_t;
+            r.q16 = q16;
+            r.kc = kc(l);
+            r.vc = vc(l);
+            r.cap = cap;
+            r.P = P;
+            r.M = M;
+            r.n_heads = c.n_heads;
+            r.n_kv = c.n_kv_heads;
+            r.hd = c.head_dim;
+            r.interleaved = c.arch == 0;
+            launch_rope_kv(r, st);
+            AttnParams a{};
+            a.q16 = q16;
+            a.kc = kc(l);
+            a.vc = vc(l);
+            a.cap = cap;
+            a.mask = d_mask;
+            a.mask_words = mask_words;
+            a.P = P;
+            a.M = M;
+            a.n_heads = c.n_heads;
+            a.n_kv = c.n_kv_heads;
+            a.n_rep = c.n_heads / c.n_kv_heads;
+            a.hd = c.head_dim;
+            a.cps = cps;
+            a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+            a.part_o = part_o;
+            a.part_ml = part_ml;
+            a.out16 = ap;
+            a.out_ld = ap_ld;
+            launch_attention(a, st);
+        }
+        {
+            GemmParams p{};
+            p.seg[0] = seg_of(L[K_ATTN_O], 0, h, H, 0, nullptr);
+            p.nseg = 1;
+            p.ntiles = L[K_ATTN_O].rows / 16;
+            p.xp = ap;
+            p.K = QD;
+            p.M = M;
+            p.mode = GM_RESID;
+            run_gemm(p, "wo", wbytes(L[K_ATTN_O]));
+        }
+        launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
+        {
+            GemmParams p{};
+            p.seg[0] = seg_of(L[K_FFN_GATE], 0, nullptr, 0, 0, nullptr);
+            p.seg[1] = seg_of(L[K_FFN_UP], 0, nullptr, 0, 0, nullptr);
+            p.nseg = 2;
+            p.ntiles = L[K_FFN_GATE].rows / 16 * 2;
+            p.xp = xp;
+            p.K = H;
+            p.M = M;
+            p.mode = GM_SWIGLU;
+            p.act = act;
+            p.act_ld = act_ld;
+            if (L[K_FFN_GATE].fmt != L[K_FFN_UP].fmt) throw UnsupportedError("ffn_gate and ffn_up must share a format");
+            run_gemm(p, "gate_up", wbytes(L[K_FFN_GATE]) + wbytes(L[K_FFN_UP]));
+        }
+        {
+            GemmParams p{};
+            p.seg[0] = seg_of(L[K_FFN_DOWN], 0, h, H, 0, nullptr);
+            p.nseg = 1;
+            p.ntiles = L[K_FFN_DOWN].rows / 16;
+            p.xp = act;
+            p.K = c.ffn;
+            p.M = M;
+            p.mode = GM_RESID;
+            run_gemm(p, "down", wbytes(L[K_FFN_DOWN]));
+        }
+        for (size_t ci = 0; ci < collect.size(); ci++)
+            if (collect[ci] == l)
+                SD_HIP_CHECK(hipMemcpyAsync(collect_buf + ci * H, h + (size_t)(M - 1) * H, H * 4,
+                                            hipMemcpyDeviceToDevice, st));
+    }
+    launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, xp, xp_ld, want_hidden ? hidden_out : nullptr,
+                   st);
+    logits_rows_last = 0;
+    if (logits_mode != 0) {
+        const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
+        const int rows = logits_mode == 1 ? 1 : M;
+        GemmParams p{};
+        p.seg[0] = seg_of(W, 0, logits, c.vocab, 0, nullptr);
+        p.nseg = 1;
+        p.ntiles = W.rows / 16;
+        p.xp = xp + (logits_mode == 1 ? (size_t)(M - 1) * xp_ld : 0);
+        p.K = H;
+        p.M = rows;
+        p.mode = GM_LOGITS;
+        p.amax_v = amax_v;
+        p.amax_i = amax_i;
+        if (xp_ld != H) throw UnsupportedError("lm_head needs hidden == q_dim activations stride");
+        p.amax_ld = qgemm_workgroups(p);
+        if (p.amax_ld > amax_ld) throw BackendError("argmax workspace too small");
+        run_gemm(p, "lm_head", wbytes(W));
+        launch_argmax_reduce(amax_v, amax_i, p.amax_ld, rows, argmax, st);
+        logits_rows_last = rows;
+    }
+    if (!collect.empty()) {
+        SD_HIP_CHECK(hipMemcpyAsync(collect_out, collect_buf, collect.size() * H * 4, hipMemcpyDeviceToHost, st));
+    }
+}
+
+void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
+    const ModelCfg &c = cfg;
+    SD_HIP_CHECK(hipSetDevice(c.device));
+    logits_rows_last = 0;
+    const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
+    for (int r0 = 0; r0 < rows; r0 += c.max_batch) {
+        const int n = std::min(c.max_batch, rows - r0);
+        SD_HIP_CHECK(hipMemcpyAsync(hidden_out, hidden_host + (size_t)r0 * c.hidden, (size_t)n * c.hidden * 4,
+                                    hipMemcpyHostToDevice, st));
+        launch_to_frag16(hidden_out, n, c.hidden, xp, xp_ld, st);
+        GemmParams p{};
+        p.seg[0] = seg_of(W, 0, logits, c.vocab, 0, nullptr);
+        p.nseg = 1;
+        p.ntiles = W.rows / 16;
+        p.xp = xp;
+        p.K = c.hidden;
+        p.M = n;
+        p.mode = GM_STORE;
+        launch_qgemm(p, st);
+        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.vocab, logits, (size_t)n * c.vocab * 4,
+                                    hipMemcpyDeviceToHost, st));
+        SD_HIP_CHECK(hipStreamSynchronize(st));
+    }
+}
+
+void Model::embed_rows(const int *ids, int n, float *out_host) {
+    const ModelCfg &c = cfg;
+    SD_HIP_CHECK(hipSetDevice(c.device));
+    for (int r0 = 0; r0 < n; r0 += c.max_batch) {
+        const int k = std::min(c.max_batch, n - r0);
+        for (int i = 0; i < k; i++)
+            if (ids[r0 + i] < 0 || ids[r0 + i] >= c.vocab) throw ArgError("token id out of range");
+        stage_wait();
+        std::memcpy(h_stage, ids + r0, k * sizeof(int));
+        SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, k * sizeof(int), hipMemcpyHostToDevice, st));
+        stage_done();
+        launch_embed(gw[K_TOK_EMBD].fmt, gw[K_TOK_EMBD].d, c.hidden, d_ids, k, hidden_out, st);
+        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.hidden, hidden_out, (size_t)k * c.hidden * 4,
+                                    hipMemcpyDeviceToHost, st));
+        SD_HIP_CHECK(hipStreamSynchronize(st));
+    }
+}
+
+void Model::compact_tail(int P, const std::vector<int> &src) {
+    const int n = (int)src.size();
+    if (n == 0) return;
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    stage_wait();
+    std::memcpy(h_stage, src.data(), n * sizeof(int));
+    SD_HIP_CHECK(hipMemcpyAsync(d_src, h_stage, n * sizeof(int), hipMemcpyHostToDevice, st));
+    stage_done();
+    launch_keep_kv_tail(kv, cfg.n_layers * 2 * cfg.n_kv_heads, cap * cfg.head_dim, cfg.head_dim, P, d_src, n, st);
+}
+
+// ===========================================================================
+// DraftTree (tree.rs)
+// ===========================================================================
+DraftTreeC DraftTreeC::from_arrays(const uint32_t *tokens, const uint32_t *parents, size_t n) {
+    if (n == 0) throw SamplingError("DraftTree must have at least a root");
+    DraftTreeC t;
+    t.tokens.assign(tokens, tokens + n);
+    t.parents.assign(n, 0);
+    for (size_t i = 1; i < n; i++) {
+        if (parents[i] >= i)
+            throw SamplingError("node " + std::to_string(i) + " has parent index " + std::to_string(parents[i]) +
+                                ", which is not strictly smaller");
+        t.parents[i] = parents[i];
+    }
+    return t;
+}
+
+int DraftTreeC::depth_of(size_t i) const {
+    int d = 0;
+    while (i != 0) {
+        i = parents[i];
+        d++;
+    }
+    return d;
+}
+
+bool DraftTreeC::is_ancestor_of(size_t a, size_t n) const {
+    size_t cur = n;
+    if (cur == a) return true;
+    while (cur != 0) {
+        cur = parents[cur];
+        if (cur == a) return true;
+    }
+    return a == 0;
+}
+
+std::vector<std::vector<size_t>> DraftTreeC::paths() const {
+    std::vector<bool> leaf(size(), true);
+    for (size_t i = 1; i < size(); i++) leaf[parents[i]] = false;
+    std::vector<std::vector<size_t>> out;
+    for (size_t i = 0; i < size(); i++) {
+        if (!leaf[i]) continue;
+        std::vector<size_t> chain{i};
+        size_t c = i;
+        while (c != 0) {
+            c = parents[c];
+            chain.push_back(c);
+        }
+        std::reverse(chain.begin(), chain.end());
+        out.push_back(chain);
+    }
+    return out;
+}
+
+void DraftTreeC::masks(std::vector<uint64_t> &words, int &nw) const {
+    const size_t n = size();
+    nw = (int)((n + 63) / 64);
+    words.assign(n * nw, 0ull);
+    for (size_t i = 0; i < n; i++) {
+        size_t c = i;
+        while (true) {
+            words[i * nw + c / 64] |= 1ull << (c % 64);
+            if (c == 0) break;
+            c = parents[c];
+        }
+    }
+}
+
+// ===========================================================================
+// Decoder (quantized_llama.rs)
+// ===========================================================================
+static void causal_masks(int M, std::vector<uint64_t> &w, int &nw) {
+    nw = (M + 63) / 64;
+    w.assign((size_t)M * nw, 0ull);
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j <= i; j++) w[(size_t)i * nw + j / 64] |= 1ull << (j % 64);
+}
+
+void Decoder::reset() {
+    history.clear();
+    cache_len = 0;
+    last_valid = false;
+}
+
+void Decoder::truncate(size_t len) {
+    // ModelWeights::truncate_kv_cache_to (quantized_llama_local.rs:162-175, 441-446)
+    if ((int)len > cache_len) throw BackendError("truncate_kv_cache_to(" + std::to_string(len) + ") exceeds " +
+                                                 std::to_string(cache_len));
+    cache_len = (int)len;
+}
+
+// forward_advance_logits (quantized_llama.rs:137-158): forward `tokens` at the
+// cache end; caches the last row's logits.  Chunks longer inputs by max_batch.
+void Decoder::forward_advance(const uint32_t *tokens, size_t n, bool all_rows) {
+    if (n == 0) throw SamplingError("forward_advance with empty tokens");
+    Model &m = *model;
+    const int V = m.cfg.vocab;
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)V) throw ArgError("token id out of range");
+    if (all_rows && n > (size_t)m.cfg.max_batch) throw ArgError("too many rows for one verify pass");
+    if (cache_len + n > (size_t)m.cfg.ctx_len) throw ArgError("KV capacity exceeded");
+    size_t done = 0;
+    std::vector<int> ids, pos;
+    std::vector<uint64_t> mw;
+    int nw;
+    while (done < n) {
+        const int M = (int)std::min<size_t>(m.cfg.max_batch, n - done);
+        const bool last_chunk = done + M == n;
+        ids.assign(tokens + done, tokens + done + M);
+        pos.resize(M);
+        for (int i = 0; i < M; i++) pos[i] = cache_len + i;
+        causal_masks(M, mw, nw);
+        m.forward(ids.data(), pos.data(), mw.data(), nw, M, cache_len, last_chunk ? (all_rows ? 2 : 1) : 0, false,
+                  {}, nullptr);
+        cache_len += M;
+        done += M;
+    }
+    const int rows = m.logits_rows_last;
+    SD_HIP_CHECK(hipMemcpyAsync(m.last_row, m.logits + (size_t)(rows - 1) * V, (size_t)V * 4,
+                                hipMemcpyDeviceToDevice, m.st));
+    last_valid = true;
+}
+
+void Decoder::observe(const uint32_t *ids, size_t n) {
+    if (n == 0) return;
+    forward_advance(ids, n, false);
+    history.insert(history.end(), ids, ids + n);
+    SD_HIP_CHECK(hipStreamSynchronize(model->st));
+}
+
+void Decoder::next_logits(float *out) {
+    if (history.empty()) throw SamplingError("next_logits called with empty history");
+    Model &m = *model;
+    if (!last_valid) {
+        const uint32_t last = history.back();
+        truncate(history.size() - 1);
+        forward_advance(&last, 1, false);
+    }
+    if (out) SD_HIP_CHECK(hipMemcpyAsync(out, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::batched_logits(const uint32_t *drafts, size_t k, float *out) {
+    if (k == 0) {
+        next_logits(out);
+        return;
+    }
+    if (history.empty()) throw SamplingError("batched_logits with empty history");
+    Model &m = *model;
+    if (k + 1 > (size_t)m.cfg.max_batch) throw ArgError("too many draft tokens for one verify pass");
+    for (size_t i = 0; i < k; i++)
+        if (drafts[i] >= (uint32_t)m.cfg.vocab) throw ArgError("token id out of range");
+    const uint32_t last = history.back();
+    truncate(history.size() - 1);
+    std::vector<uint32_t> comb;
+    comb.push_back(last);
+    comb.insert(comb.end(), drafts, drafts + k);
+    forward_advance(comb.data(), comb.size(), true);
+    if (out)
+        SD_HIP_CHECK(hipMemcpyAsync(out, m.logits, (k + 1) * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+    history.insert(history.end(), drafts, drafts + k);
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::rollback_to(size_t len) {
+    if (len > history.size())
+        throw RollbackError("rollback target " + std::to_string(len) + " > history length " +
+                            std::to_string(history.size()));
+    history.resize(len);
+    last_valid = false;
+    truncate(len);
+}
+
+void Decoder::tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden,
+                           int &prefix) {
+    Model &m = *model;
+    const DraftTreeC t = DraftTreeC::from_arrays(tokens, parents, n);
+    const uint32_t last = history.back();
+    if (t.tokens[0] != last)
+        throw SamplingError("tree root (" + std::to_string(t.tokens[0]) + ") must equal last committed token (" +
+                            std::to_string(last) + ")");
+    if (n > (size_t)m.cfg.max_batch) throw ArgError("tree larger than max_batch");
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)m.cfg.vocab) throw ArgError("token id out of range");
+    prefix = cache_len - 1;
+    if (prefix + (int)n > m.cfg.ctx_len) throw ArgError("KV capacity exceeded");
+    truncate(prefix);
+    std::vector<int> ids(tokens, tokens + n), pos(n);
+    for (size_t i = 0; i < n; i++) pos[i] = prefix + t.depth_of(i);
+    std::vector<uint64_t> mw;
+    int nw;
+    t.masks(mw, nw);
+    m.forward(ids.data(), pos.data(), mw.data(), nw, (int)n, prefix, 2, want_hidden, {}, nullptr);
+}
+
+void Decoder::tree_logits_keep_kv(const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits,
+                                  float *out_hidden) {
+    last_valid = false;
+    if (history.empty()) throw SamplingError("tree_logits with empty history");
+    Model &m = *model;
+    int prefix;
+    tree_forward(tokens, parents, n, true, prefix);
+    cache_len = prefix + (int)n;
+    if (out_logits)
+        SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.logits, n * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+    if (out_hidden)
+        SD_HIP_CHECK(
+            hipMemcpyAsync(out_hidden, m.hidden_out, n * (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::tree_logits(const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits) {
+    if (history.empty()) throw SamplingError("tree_logits with empty history");
+    Model &m = *model;
+    const uint32_t last = history.back();
+    int prefix;
+    tree_forward(tokens, parents, n, false, prefix);
+    if (out_logits)
+        SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.logits, n * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    truncate(prefix);
+    forward_advance(&last, 1, false);  // GEMV-path root row (quantized_llama.rs:306-322)
+    if (out_logits)
+        SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::commit_tree_path(const uint32_t *tokens, const uint32_t *parents, size_t n, const uint32_t *acc,
+                               size_t n_acc) {
+    last_valid = false;
+    if (history.empty()) throw SamplingError("commit_tree_path with empty history");
+    const DraftTreeC t = DraftTreeC::from_arrays(tokens, parents, n);
+    const int prefix = (int)history.size() - 1;
+    // keep = [0..prefix) ++ [prefix + ti]; every index must exist in the cache
+    std::vector<int> src(n_acc);
+    for (size_t j = 0; j < n_acc; j++) {
+        if (acc[j] >= n || prefix + (int)acc[j] >= cache_len)
+            throw BackendError("commit_tree_path: accepted index out of range of the tree / cache");
+        src[j] = (int)acc[j];
+    }
+    if (n_acc == 0) {
+        // keep_kv_indices(&[0..prefix)) keeps the prefix only
+        cache_len = prefix;
+    } else {
+        model->compact_tail(prefix, src);
+        cache_len = prefix + (int)n_acc;
+    }
+    for (size_t j = 1; j < n_acc; j++) history.push_back(t.tokens[acc[j]]);
+    SD_HIP_CHECK(hipStreamSynchronize(model->st));
+}
+
+void Decoder::last_hidden_state(float *out) {
+    if (history.empty()) throw SamplingError("last_hidden_state with empty history");
+    Model &m = *model;
+    const uint32_t last = history.back();
+    truncate(history.size() - 1);
+    int id = (int)last, pos = cache_len;
+    uint64_t mk = 1;
+    m.forward(&id, &pos, &mk, 1, 1, cache_len, 0, true, {}, nullptr);
+    cache_len += 1;
+    if (out) SD_HIP_CHECK(hipMemcpyAsync(out, m.hidden_out, (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::observe_returning_last_hidden(const uint32_t *ids, size_t n, float *out) {
+    if (n == 0) throw SamplingError("observe_returning_last_hidden with empty ids");
+    Model &m = *model;
+    if (cache_len + n > (size_t)m.cfg.ctx_len) throw ArgError("KV capacity exceeded");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)m.cfg.vocab) throw ArgError("token id out of range");
+    size_t done = 0;
+    std::vector<int> tk, pos;
+    std::vector<uint64_t> mw;
+    int nw;
+    int lastM = 1;
+    while (done < n) {
+        const int M = (int)std::min<size_t>(m.cfg.max_batch, n - done);
+        tk.assign(ids + done, ids + done + M);
+        pos.resize(M);
+        for (int i = 0; i < M; i++) pos[i] = cache_len + i;
+        causal_masks(M, mw, nw);
+        m.forward(tk.data(), pos.data(), mw.data(), nw, M, cache_len, 0, done + M == n, {}, nullptr);
+        cache_len += M;
+        done += M;
+        lastM = M;
+    }
+    history.insert(history.end(), ids, ids + n);
+    if (out)
+        SD_HIP_CHECK(hipMemcpyAsync(out, m.hidden_out + (size_t)(lastM - 1) * m.cfg.hidden, (size_t)m.cfg.hidden * 4,
+                                    hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+void Decoder::last_hidden_states_multi(const uint32_t *layers, size_t nl, float *out_final, float *out_layers) {
+    if (history.empty()) throw SamplingError("last_hidden_states_multi with empty history");
+    Model &m = *model;
+    std::vector<int> col(nl);
+    for (size_t i = 0; i < nl; i++) {
+        if (layers[i] >= (uint32_t)m.cfg.n_layers)
+            throw BackendError("collect_layers[" + std::to_string(i) + "] = " + std::to_string(layers[i]) +
+                               " out of range (n_layers=" + std::to_string(m.cfg.n_layers) + ")");
+        col[i] = (int)layers[i];
+    }
+    const uint32_t last = history.back();
+    truncate(history.size() - 1);
+    int id = (int)last, pos = cache_len;
+    uint64_t mk = 1;
+    std::vector<float> tmp(nl * (size_t)m.cfg.hidden);
+    m.forward(&id, &pos, &mk, 1, 1, cache_len, 0, true, col, tmp.data());
+    cache_len += 1;
+    if (out_final)
+        SD_HIP_CHECK(hipMemcpyAsync(out_final, m.hidden_out, (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    if (out_layers) std::memcpy(out_layers, tmp.data(), tmp.size() * 4);
+}
+
+// ---- device acceptance -----------------------------------------------------
+void Decoder::argmax_rows(int32_t *out, size_t n) {
+    Model &m = *model;
+    if (n > (size_t)m.logits_rows_last) throw ArgError("fewer rows in the last verify pass");
+    SD_HIP_CHECK(hipMemcpyAsync(out, m.argmax, n * 4, hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+}
+
+// batched_logits + greedy acceptance with the logits kept in HBM:
+// accept drafts while draft[i] == argmax(row i); the first mismatch (or the
+// bonus row k) contributes argmax of that row (vanilla.rs:178-210 at T=0,
+// equivalently the first-max fold of eagle.rs:626-637).
+void Decoder::verify_greedy_linear(const uint32_t *drafts, size_t k, uint32_t *commits, size_t *n_commit,
+                                   size_t *n_accepted) {
+    batched_logits(drafts, k, nullptr);
+    std::vector<int32_t> am(k + 1);
+    if (k == 0) {
+        launch_argmax_rows(model->last_row, model->cfg.vocab, model->cfg.vocab, 1, model->argmax, model->st);
+        model->logits_rows_last = 1;
+    }
+    argmax_rows(am.data(), k + 1);
+    size_t a = 0;
+    while (a < k && (uint32_t)am[a] == drafts[a]) a++;
+    for (size_t i = 0; i < a; i++) commits[i] = drafts[i];
+    commits[a] = (uint32_t)am[a];
+    *n_commit = a + 1;
+    *n_accepted = a;
+}
+
+// tree_logits_keep_kv + greedy longest accepted path (eagle.rs:605-661):
+// paths in ascending leaf order, a strictly longer count replaces the best
+// (ties keep the earliest leaf); bonus = argmax of the deepest accepted node;
+// bonus_node = first child of that node carrying the bonus token (eagle.rs:700-709),
+// -1 if none or in strict mode.
+void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, int strict,
+                                 uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node) {
+    if (history.empty()) throw SamplingError("tree_logits with empty history");
+    Model &m = *model;
+    int32_t root_am = -1;
+    if (strict) {
+        next_logits(nullptr);
+        launch_argmax_rows(m.last_row, m.cfg.vocab, m.cfg.vocab, 1, m.argmax, m.st);
+        SD_HIP_CHECK(hipMemcpyAsync(&root_am, m.argmax, 4, hipMemcpyDeviceToHost, m.st));
+        SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    }
+    tree_logits_keep_kv(tokens, parents, n, nullptr, nullptr);
+    std::vector<int32_t> am(n);
+    argmax_rows(am.data(), n);
+    if (strict) am[0] = root_am;
+    const DraftTreeC t = DraftTreeC::from_arrays(tokens, parents, n);
+    std::vector<size_t> best{0};
+    for (const auto &p : t.paths()) {
+        size_t acc = 0;
+        for (size_t w = 0; w + 1 < p.size(); w++) {
+            if ((uint32_t)am[p[w]] == t.tokens[p[w + 1]]) acc++;
+            else break;
+        }
+        if (acc + 1 > best.size()) best.assign(p.begin(), p.begin() + acc + 1);
+    }
+    for (size_t i = 0; i < best.size(); i++) path[i] = (uint32_t)best[i];
+    *path_len = best.size();
+    const size_t deepest = best.back();
+    *bonus = (uint32_t)am[deepest];
+    *bonus_node = -1;
+    if (!strict)
+        for (size_t c = 1; c < n; c++)
+            if (t.parents[c] == deepest && t.tokens[c] == *bonus) {
+                *bonus_node = (int32_t)c;
+                break;
+            }
+}
+
+void Decoder::prime_synthetic(const uint32_t *ids, size_t n, uint64_t kv_seed) {
+    Model &m = *model;
+    if (n == 0 || n > (size_t)m.cfg.ctx_len) throw ArgError("prefix length out of range");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)m.cfg.vocab) throw ArgError("token id out of range");
+    m.fill_kv_synthetic((int)n, kv_seed);
+    history.assign(ids, ids + n);
+    cache_len = (int)n;
+    last_valid = false;
+}
+
+}  // namespace sd

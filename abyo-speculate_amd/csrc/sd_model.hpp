@@ -1,0 +1,184 @@
+// Host runtime: device weights, fp16 KV cache, work buffers and the forward
+// pass of the quantised Llama / Qwen2 target, plus the decoder state machine
+// of the reference's LlamaQuantDecoder (crates/speculate/src/model/quantized_llama.rs).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <array>
+#include <string>
+#include <vector>
+
+#include "sd_kernels.hpp"
+#include "sd_kernels_attn.hpp"
+#include "sd_kernels_elem.hpp"
+
+namespace sd {
+
+// Error classes mapped 1:1 onto the reference's Error variants (error.rs:10-50).
+struct SamplingError : std::runtime_error {
+    explicit SamplingError(const std::string &m) : std::runtime_error(m) {}
+};
+struct RollbackError : std::runtime_error {
+    explicit RollbackError(const std::string &m) : std::runtime_error(m) {}
+};
+struct ArgError : std::runtime_error {
+    explicit ArgError(const std::string &m) : std::runtime_error(m) {}
+};
+struct UnsupportedError : std::runtime_error {
+    explicit UnsupportedError(const std::string &m) : std::runtime_error(m) {}
+};
+
+enum Kind : int {
+    K_TOK_EMBD = 0, K_OUTPUT = 1, K_OUTPUT_NORM = 2,
+    K_ATTN_Q = 3, K_ATTN_K = 4, K_ATTN_V = 5, K_ATTN_O = 6,
+    K_FFN_GATE = 7, K_FFN_UP = 8, K_FFN_DOWN = 9,
+    K_ATTN_NORM = 10, K_FFN_NORM = 11, K_BQ = 12, K_BK = 13, K_BV = 14,
+    K_NUM = 15
+};
+
+struct ModelCfg {
+    int arch = 0;  // 0 llama (rope_i, no bias), 1 qwen2 (rope, QKV bias)
+    int n_layers = 0, hidden = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0;
+    float rope_theta = 10000.f, rms_eps = 1e-5f;
+    int ctx_len = 0;     // KV capacity (max positions)
+    int max_batch = 128; // rows per forward pass
+    int tied_output = 0;
+    int device = 0;
+    int q_dim() const { return n_heads * head_dim; }
+    int kv_dim() const { return n_kv_heads * head_dim; }
+};
+
+struct DevTensor {
+    int fmt = -1;
+    int rows = 0, K = 0;
+    uint8_t *d = nullptr;
+    size_t bytes = 0;
+    bool set() const { return d != nullptr; }
+};
+
+// Per-kernel-class timing collected with HIP events on the model's stream.
+struct ProfEntry {
+    std::string name;
+    double bytes;  // algorithmic bytes of the launch
+    hipEvent_t a, b;
+};
+
+struct DraftTreeC;
+
+class Model {
+  public:
+    explicit Model(const ModelCfg &c);
+    ~Model();
+
+    ModelCfg cfg;
+    hipStream_t st = nullptr;
+
+    // weights
+    std::vector<std::array<DevTensor, K_NUM>> lw;  // per layer
+    std::array<DevTensor, K_NUM> gw;              // global (layer = -1)
+
+    void set_tensor(int layer, int kind, int fmt, const void *host, size_t bytes);
+    void get_tensor(int layer, int kind, void *host, size_t bytes);
+    void tensor_info(int layer, int kind, int *fmt, int *rows, int *K, size_t *gguf_bytes);
+    void dequant_tensor(int layer, int kind, float *host);
+    void synthesize(int mix, uint64_t seed, float std);
+    void fill_kv_synthetic(int P, uint64_t seed);
+    bool weights_ready() const;
+
+    // raw matmul (test entry): y[M][N] = x[M][K] . W^T (x rounded to fp16)
+    void qmatmul(int layer, int kind, const float *x, int M, float *y);
+
+    // forward of M tokens at cache positions [P, P+M); mask words per token.
+    // logits_mode: 0 none, 1 last row only (into logits row 0), 2 all rows.
+    void forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P, int logits_mode,
+                 bool want_hidden, const std::vector<int> &collect, float *collect_out);
+    void lm_head_rows(const float *hidden_host, int rows, float *out_host);
+    void embed_rows(const int *ids, int n, float *out_host);
+    void compact_tail(int P, const std::vector<int> &src);
+
+    // profiling of the dominant kernels
+    bool prof_on = false;
+    std::vector<ProfEntry> prof;
+    void prof_reset();
+
+    // device buffers
+    uint16_t *kv = nullptr;  // [L][2][n_kv][cap][hd]
+    int64_t cap = 0;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    float *h = nullptr, *qkv = nullptr, *logits = nullptr, *hidden_out = nullptr, *last_row = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr, *amax_v = nullptr, *collect_buf = nullptr;
+    int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
+    uint64_t *d_mask = nullptr;
+    uint16_t *xp = nullptr, *ap = nullptr, *act = nullptr, *q16 = nullptr;
+    int xp_ld = 0, ap_ld = 0, act_ld = 0;
+    int amax_ld = 0;
+    int nsplit_max = 0;
+    int logits_rows_last = 0;  // rows of `logits` / `argmax` produced by the last forward
+    // pinned staging for small H2D transfers
+    int *h_stage = nullptr;
+    size_t h_stage_bytes = 0;
+    hipEvent_t stage_ev = nullptr;  // recorded after the last copy out of h_stage
+    void stage_wait();               // host waits until h_stage may be rewritten
+    void stage_done();
+
+  private:
+    void alloc_buffers();
+    void run_gemm(GemmParams &p, const char *name, double bytes);
+    uint16_t *kc(int layer) const { return kv + (int64_t)layer * 2 * cfg.n_kv_heads * cap * cfg.head_dim; }
+    uint16_t *vc(int layer) const { return kc(layer) + (int64_t)cfg.n_kv_heads * cap * cfg.head_dim; }
+};
+
+// Decoder contract of LlamaQuantDecoder (quantized_llama.rs:443-600) over Model.
+class Decoder {
+  public:
+    explicit Decoder(Model *m) : model(m) {}
+    Model *model;
+    std::vector<uint32_t> history;
+    int cache_len = 0;
+    bool last_valid = false;  // last_logits cache (device row model->last_row)
+    std::vector<uint32_t> eos;
+
+    void reset();
+    void observe(const uint32_t *ids, size_t n);
+    void next_logits(float *out);
+    void batched_logits(const uint32_t *drafts, size_t k, float *out);
+    void rollback_to(size_t len);
+    void tree_logits_keep_kv(const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits,
+                             float *out_hidden);
+    void tree_logits(const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits);
+    void commit_tree_path(const uint32_t *tokens, const uint32_t *parents, size_t n, const uint32_t *acc,
+                          size_t n_acc);
+    void last_hidden_state(float *out);
+    void observe_returning_last_hidden(const uint32_t *ids, size_t n, float *out);
+    void last_hidden_states_multi(const uint32_t *layers, size_t nl, float *out_final, float *out_layers);
+
+    // device acceptance
+    void verify_greedy_linear(const uint32_t *drafts, size_t k, uint32_t *commits, size_t *n_commit,
+                              size_t *n_accepted);
+    void verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, int strict,
+                            uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node);
+    void argmax_rows(int32_t *out, size_t n);
+
+    // sets history and KV [0, n) to synthetic values (benchmarks, full-size tests)
+    void prime_synthetic(const uint32_t *ids, size_t n, uint64_t kv_seed);
+
+  private:
+    void forward_advance(const uint32_t *tokens, size_t n, bool all_rows);
+    void truncate(size_t len);
+    void tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden, int &prefix);
+};
+
+// Host DraftTree (tree.rs:38-282): parent table validation, depths, paths, masks.
+struct DraftTreeC {
+    std::vector<uint32_t> tokens;
+    std::vector<uint32_t> parents;
+    static DraftTreeC from_arrays(const uint32_t *tokens, const uint32_t *parents, size_t n);
+    size_t size() const { return tokens.size(); }
+    int depth_of(size_t i) const;
+    bool is_ancestor_of(size_t a, size_t n) const;
+    std::vector<std::vector<size_t>> paths() const;
+    void masks(std::vector<uint64_t> &words, int &nw) const;
+};
+
+}  // namespace sd

@@ -1,0 +1,375 @@
+"""Python binding of libspeculate_hip.so (the C ABI in include/speculate_hip.h).
+
+``HipQuantDecoder`` mirrors the reference's ``LlamaQuantDecoder`` /
+``Qwen2QuantDecoder`` surface -- the ``Decoder`` and ``TreeDecoder`` traits of
+crates/speculate/src/model/mod.rs:39-236 -- method for method, with the same
+error classes (``SamplingError``, ``CacheRollbackError``, ``BackendError``
+standing for Error::Sampling / Error::CacheRollback / Error::Candle).
+
+There is no CPU fallback: importing works anywhere, but constructing a
+decoder needs the built HIP library and a GPU, and fails loudly otherwise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libspeculate_hip.so")
+
+# sd_status
+SD_OK, SD_ERR_SAMPLING, SD_ERR_ROLLBACK, SD_ERR_BACKEND, SD_ERR_ARG, SD_ERR_UNSUPPORTED = range(6)
+# formats (GGML type ids)
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+# tensor kinds
+(TOK_EMBD, OUTPUT, OUTPUT_NORM, ATTN_Q, ATTN_K, ATTN_V, ATTN_OUTPUT, FFN_GATE, FFN_UP, FFN_DOWN,
+ ATTN_NORM, FFN_NORM, ATTN_Q_BIAS, ATTN_K_BIAS, ATTN_V_BIAS) = range(15)
+ARCH_LLAMA, ARCH_QWEN2 = 0, 1
+MIX_Q4_K, MIX_Q4_K_M, MIX_Q5K_Q80, MIX_Q6_K, MIX_Q5_K, MIX_Q8_0 = range(6)
+PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head")
+
+
+class SpeculateError(Exception):
+    """Base of the errors raised by the binding."""
+
+
+class SamplingError(SpeculateError):
+    """Error::Sampling (error.rs)."""
+
+
+class CacheRollbackError(SpeculateError):
+    """Error::CacheRollback (error.rs)."""
+
+
+class BackendError(SpeculateError):
+    """Error::Candle: device or runtime failure."""
+
+
+class ArgError(SpeculateError, ValueError):
+    """Invalid argument."""
+
+
+class UnsupportedMethod(SpeculateError):
+    """Error::UnsupportedMethod / unsupported shape or format."""
+
+
+_ERRS = {SD_ERR_SAMPLING: SamplingError, SD_ERR_ROLLBACK: CacheRollbackError, SD_ERR_BACKEND: BackendError,
+         SD_ERR_ARG: ArgError, SD_ERR_UNSUPPORTED: UnsupportedMethod}
+
+
+class SdConfig(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_int32), ("n_layers", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("ffn", ctypes.c_int32), ("vocab", ctypes.c_int32), ("rope_theta", ctypes.c_float),
+                ("rms_eps", ctypes.c_float), ("ctx_len", ctypes.c_int32), ("max_batch", ctypes.c_int32),
+                ("tied_output", ctypes.c_int32), ("device", ctypes.c_int32)]
+
+
+@dataclass
+class Config:
+    arch: int = ARCH_LLAMA
+    n_layers: int = 4
+    hidden: int = 512
+    n_heads: int = 8
+    n_kv_heads: int = 8
+    head_dim: int = 64
+    ffn: int = 1536
+    vocab: int = 32000
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-5
+    ctx_len: int = 4096
+    max_batch: int = 128
+    tied_output: int = 0
+    device: int = 0
+
+    def to_c(self) -> SdConfig:
+        return SdConfig(**{k: getattr(self, k) for k, _ in SdConfig._fields_})
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"HIP library not built: {path} (run __graft_entry__.build())")
+    L = ctypes.CDLL(path)
+    P, I32, U64, SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64, ctypes.c_size_t
+    pSZ = ctypes.POINTER(ctypes.c_size_t)
+    sigs = {
+        "sd_model_create": ([ctypes.POINTER(SdConfig), ctypes.POINTER(P)], I32),
+        "sd_model_destroy": ([P], None),
+        "sd_model_set_tensor": ([P, I32, I32, I32, P, SZ], I32),
+        "sd_model_get_tensor": ([P, I32, I32, P, SZ], I32),
+        "sd_model_tensor_info": ([P, I32, I32, P, P, P, P], I32),
+        "sd_model_synthesize": ([P, I32, U64, ctypes.c_float], I32),
+        "sd_model_dequant_tensor": ([P, I32, I32, P], I32),
+        "sd_model_qmatmul": ([P, I32, I32, P, SZ, P], I32),
+        "sd_last_error": ([], ctypes.c_char_p),
+        "sd_vocab_size": ([P], SZ),
+        "sd_history_len": ([P], SZ),
+        "sd_history": ([P, P, SZ], SZ),
+        "sd_reset": ([P], None),
+        "sd_observe": ([P, P, SZ], I32),
+        "sd_next_logits": ([P, P], I32),
+        "sd_batched_logits": ([P, P, SZ, P], I32),
+        "sd_rollback_to": ([P, SZ], I32),
+        "sd_set_eos_token_ids": ([P, P, SZ], I32),
+        "sd_eos_token_ids": ([P, P, SZ], SZ),
+        "sd_tree_logits_keep_kv": ([P, P, P, SZ, P, P], I32),
+        "sd_tree_logits": ([P, P, P, SZ, P], I32),
+        "sd_commit_tree_path": ([P, P, P, SZ, P, SZ], I32),
+        "sd_last_hidden_state": ([P, P], I32),
+        "sd_observe_returning_last_hidden": ([P, P, SZ, P], I32),
+        "sd_last_hidden_states_multi": ([P, P, SZ, P, P], I32),
+        "sd_apply_lm_head": ([P, P, SZ, P], I32),
+        "sd_embed_tokens": ([P, P, SZ, P], I32),
+        "sd_num_hidden_layers": ([P], SZ),
+        "sd_hidden_size": ([P], SZ),
+        "sd_verify_greedy_linear": ([P, P, SZ, P, pSZ, pSZ], I32),
+        "sd_verify_greedy_tree": ([P, P, P, SZ, I32, P, pSZ, P, P], I32),
+        "sd_last_argmax": ([P, P, SZ], I32),
+        "sd_prime_synthetic": ([P, P, SZ, U64], I32),
+        "sd_profile_enable": ([P, I32], I32),
+        "sd_profile_read": ([P, P, P, P, SZ], SZ),
+        "sd_synchronize": ([P], I32),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != SD_OK:
+        msg = _lib.sd_last_error().decode(errors="replace")
+        raise _ERRS.get(rc, BackendError)(msg)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int64).astype(np.uint32))
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def tree_arrays(tree) -> Tuple[np.ndarray, np.ndarray]:
+    """(tokens, parents) of a DraftTree-like object or a (tokens, parents) pair."""
+    if isinstance(tree, tuple):
+        toks, pars = tree
+    else:
+        toks, pars = tree.tokens(), tree.parents()
+    pars = list(pars)
+    if len(pars):
+        pars[0] = 0
+    return _u32(toks), _u32(pars)
+
+
+class HipQuantDecoder:
+    """One quantised target decoder resident on one GPU (LlamaQuantDecoder contract)."""
+
+    def __init__(self, cfg: Config):
+        L = load_library()
+        self.cfg = cfg
+        c = cfg.to_c()
+        h = ctypes.c_void_p()
+        _check(L.sd_model_create(ctypes.byref(c), ctypes.byref(h)))
+        self._h = h
+        self.vocab = cfg.vocab
+        self.hidden = cfg.hidden
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.sd_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- weights ----
+    def set_tensor(self, layer: int, kind: int, fmt: int, data: np.ndarray):
+        d = np.ascontiguousarray(data).view(np.uint8)
+        _check(_lib.sd_model_set_tensor(self._h, layer, kind, fmt, _ptr(d), d.nbytes))
+
+    def tensor_info(self, layer: int, kind: int):
+        f, r, k = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        b = ctypes.c_size_t()
+        _check(_lib.sd_model_tensor_info(self._h, layer, kind, ctypes.byref(f), ctypes.byref(r), ctypes.byref(k),
+                                         ctypes.byref(b)))
+        return f.value, r.value, k.value, b.value
+
+    def get_tensor(self, layer: int, kind: int) -> np.ndarray:
+        _, _, _, nbytes = self.tensor_info(layer, kind)
+        out = np.empty(nbytes, np.uint8)
+        _check(_lib.sd_model_get_tensor(self._h, layer, kind, _ptr(out), nbytes))
+        return out
+
+    def synthesize(self, mix: int, seed: int, std: float = 0.02):
+        _check(_lib.sd_model_synthesize(self._h, mix, seed, std))
+
+    def dequant_tensor(self, layer: int, kind: int) -> np.ndarray:
+        _, r, k, _ = self.tensor_info(layer, kind)
+        out = np.empty((r, k), np.float32)
+        _check(_lib.sd_model_dequant_tensor(self._h, layer, kind, _ptr(out)))
+        return out
+
+    def qmatmul(self, layer: int, kind: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        _, r, k, _ = self.tensor_info(layer, kind)
+        assert x.shape[1] == k
+        y = np.empty((x.shape[0], r), np.float32)
+        _check(_lib.sd_model_qmatmul(self._h, layer, kind, _ptr(x), x.shape[0], _ptr(y)))
+        return y
+
+    # ---- Decoder ----
+    def vocab_size(self) -> int:
+        return int(_lib.sd_vocab_size(self._h))
+
+    def history(self) -> List[int]:
+        n = int(_lib.sd_history_len(self._h))
+        out = np.empty(n, np.uint32)
+        _lib.sd_history(self._h, _ptr(out), n)
+        return [int(v) for v in out]
+
+    def history_len(self) -> int:
+        return int(_lib.sd_history_len(self._h))
+
+    def reset(self):
+        _lib.sd_reset(self._h)
+
+    def observe(self, ids: Sequence[int]):
+        a = _u32(ids)
+        _check(_lib.sd_observe(self._h, _ptr(a), a.size))
+
+    def next_logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        _check(_lib.sd_next_logits(self._h, _ptr(out)))
+        return out
+
+    def batched_logits(self, drafts: Sequence[int]) -> np.ndarray:
+        a = _u32(drafts)
+        out = np.empty((a.size + 1, self.vocab), np.float32)
+        _check(_lib.sd_batched_logits(self._h, _ptr(a), a.size, _ptr(out)))
+        return out
+
+    def rollback_to(self, n: int):
+        if n < 0:
+            raise ArgError("negative length")
+        _check(_lib.sd_rollback_to(self._h, n))
+
+    def set_eos_token_ids(self, ids: Sequence[int]):
+        a = _u32(ids)
+        _check(_lib.sd_set_eos_token_ids(self._h, _ptr(a), a.size))
+
+    def eos_token_ids(self) -> List[int]:
+        n = int(_lib.sd_eos_token_ids(self._h, None, 0))
+        out = np.empty(n, np.uint32)
+        _lib.sd_eos_token_ids(self._h, _ptr(out), n)
+        return [int(v) for v in out]
+
+    # ---- TreeDecoder ----
+    def tree_logits_keep_kv(self, tree, want_logits: bool = True, want_hidden: bool = True):
+        t, p = tree_arrays(tree)
+        lg = np.empty((t.size, self.vocab), np.float32) if want_logits else None
+        hd = np.empty((t.size, self.hidden), np.float32) if want_hidden else None
+        _check(_lib.sd_tree_logits_keep_kv(self._h, _ptr(t), _ptr(p), t.size, _ptr(lg), _ptr(hd)))
+        return lg, hd
+
+    def tree_logits(self, tree) -> np.ndarray:
+        t, p = tree_arrays(tree)
+        lg = np.empty((t.size, self.vocab), np.float32)
+        _check(_lib.sd_tree_logits(self._h, _ptr(t), _ptr(p), t.size, _ptr(lg)))
+        return lg
+
+    def commit_tree_path(self, tree, accepted: Sequence[int]):
+        t, p = tree_arrays(tree)
+        a = _u32(accepted)
+        _check(_lib.sd_commit_tree_path(self._h, _ptr(t), _ptr(p), t.size, _ptr(a), a.size))
+
+    def last_hidden_state(self) -> np.ndarray:
+        out = np.empty(self.hidden, np.float32)
+        _check(_lib.sd_last_hidden_state(self._h, _ptr(out)))
+        return out
+
+    def observe_returning_last_hidden(self, ids: Sequence[int]) -> np.ndarray:
+        a = _u32(ids)
+        out = np.empty(self.hidden, np.float32)
+        _check(_lib.sd_observe_returning_last_hidden(self._h, _ptr(a), a.size, _ptr(out)))
+        return out
+
+    def last_hidden_states_multi(self, layers: Sequence[int]):
+        a = _u32(layers)
+        fin = np.empty(self.hidden, np.float32)
+        mids = np.empty((a.size, self.hidden), np.float32)
+        _check(_lib.sd_last_hidden_states_multi(self._h, _ptr(a), a.size, _ptr(fin), _ptr(mids)))
+        return fin, [mids[i] for i in range(a.size)]
+
+    def apply_lm_head(self, hidden: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(np.atleast_2d(hidden), np.float32)
+        out = np.empty((h.shape[0], self.vocab), np.float32)
+        _check(_lib.sd_apply_lm_head(self._h, _ptr(h), h.shape[0], _ptr(out)))
+        return out
+
+    def embed_tokens(self, ids: Sequence[int]) -> np.ndarray:
+        a = _u32(ids)
+        out = np.empty((a.size, self.hidden), np.float32)
+        _check(_lib.sd_embed_tokens(self._h, _ptr(a), a.size, _ptr(out)))
+        return out
+
+    def num_hidden_layers(self) -> int:
+        return int(_lib.sd_num_hidden_layers(self._h))
+
+    # ---- device acceptance ----
+    def verify_greedy_linear(self, drafts: Sequence[int]) -> Tuple[List[int], int]:
+        a = _u32(drafts)
+        commits = np.empty(a.size + 1, np.uint32)
+        nc, na = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(_lib.sd_verify_greedy_linear(self._h, _ptr(a), a.size, _ptr(commits), ctypes.byref(nc),
+                                            ctypes.byref(na)))
+        return [int(v) for v in commits[:nc.value]], int(na.value)
+
+    def verify_greedy_tree(self, tree, strict: bool = False):
+        t, p = tree_arrays(tree)
+        path = np.empty(t.size, np.uint32)
+        plen = ctypes.c_size_t()
+        bonus = ctypes.c_uint32()
+        bnode = ctypes.c_int32()
+        _check(_lib.sd_verify_greedy_tree(self._h, _ptr(t), _ptr(p), t.size, 1 if strict else 0, _ptr(path),
+                                          ctypes.byref(plen), ctypes.byref(bonus), ctypes.byref(bnode)))
+        return [int(v) for v in path[:plen.value]], int(bonus.value), int(bnode.value)
+
+    def last_argmax(self, n: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        _check(_lib.sd_last_argmax(self._h, _ptr(out), n))
+        return out
+
+    # ---- synthetic state / measurement ----
+    def prime_synthetic(self, ids: Sequence[int], kv_seed: int):
+        a = _u32(ids)
+        _check(_lib.sd_prime_synthetic(self._h, _ptr(a), a.size, kv_seed))
+
+    def profile_enable(self, on: bool):
+        _check(_lib.sd_profile_enable(self._h, 1 if on else 0))
+
+    def profile_read(self, cap: int = 65536):
+        cls = np.empty(cap, np.int32)
+        by = np.empty(cap, np.float64)
+        ms = np.empty(cap, np.float32)
+        n = int(_lib.sd_profile_read(self._h, _ptr(cls), _ptr(by), _ptr(ms), cap))
+        return [(PROFILE_CLASSES[cls[i]], float(by[i]), float(ms[i])) for i in range(n)]
+
+    def synchronize(self):
+        _check(_lib.sd_synchronize(self._h))

@@ -1,0 +1,203 @@
+/*
+ * speculate_hip.h -- C ABI of the MI355X (gfx950) target-verify library.
+ *
+ * The drop-in point is the reference's decoder boundary: the `Decoder` and
+ * `TreeDecoder` traits (crates/speculate/src/model/mod.rs:39-108, :118-236) as
+ * implemented by `LlamaQuantDecoder` (crates/speculate/src/model/quantized_llama.rs)
+ * and `Qwen2QuantDecoder` (crates/speculate/src/model/quantized_qwen2.rs).  One
+ * `sd_model` handle is one such decoder: quantised weights, fp16 KV cache,
+ * token history and the cached next-token logits, all resident on one GPU.
+ * Paths cited below are relative to the reference checkout.
+ *
+ * Conventions
+ *  - Every entry point that can fail returns an sd_status; on failure the
+ *    decoder state is unchanged (model/mod.rs:35-38) and sd_last_error()
+ *    returns a thread-local message.
+ *  - Output buffers are owned by the caller (host memory); pass NULL to skip an
+ *    output.  Logits are row-major [rows][vocab] f32, hidden states [rows][hidden] f32.
+ *  - A draft tree is passed as two arrays of n entries, node tokens and parent
+ *    indices in BFS order (parents[0] is ignored; parents[i] < i), exactly the
+ *    parent table of DraftTree::from_parent_table (tree.rs:52-74).
+ *  - A handle is not thread-safe; it may move between threads.  Every call
+ *    sets its device and uses the handle's own stream.
+ */
+#ifndef SPECULATE_HIP_H
+#define SPECULATE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, one per reference Error variant (crates/speculate/src/error.rs:10-50). */
+typedef enum sd_status {
+    SD_OK = 0,
+    SD_ERR_SAMPLING = 1,    /* Error::Sampling: empty history/tokens, tree root mismatch, bad tree */
+    SD_ERR_ROLLBACK = 2,    /* Error::CacheRollback: rollback past the history */
+    SD_ERR_BACKEND = 3,     /* Error::Candle: device/runtime failure, truncate past the cache */
+    SD_ERR_ARG = 4,         /* invalid argument (sizes, ids, capacity) */
+    SD_ERR_UNSUPPORTED = 5  /* Error::UnsupportedMethod / unsupported shape or format */
+} sd_status;
+
+/* Tensor formats: the GGML type ids of the GGUF blocks. */
+enum { SD_F32 = 0, SD_Q8_0 = 8, SD_Q4_K = 12, SD_Q5_K = 13, SD_Q6_K = 14 };
+
+/* Tensor kinds.  The GGUF names follow quantized_llama_local.rs:242-281 and
+ * quantized_qwen2_local.rs:232-275 ("blk.{i}." prefix for per-layer tensors). */
+enum {
+    SD_TOK_EMBD = 0,    /* token_embd.weight   [vocab][hidden]  (layer -1) */
+    SD_OUTPUT = 1,      /* output.weight       [vocab][hidden]  (layer -1) */
+    SD_OUTPUT_NORM = 2, /* output_norm.weight  [hidden] F32     (layer -1) */
+    SD_ATTN_Q = 3,      /* attn_q.weight       [q_dim][hidden] */
+    SD_ATTN_K = 4,      /* attn_k.weight       [kv_dim][hidden] */
+    SD_ATTN_V = 5,      /* attn_v.weight       [kv_dim][hidden] */
+    SD_ATTN_OUTPUT = 6, /* attn_output.weight  [hidden][q_dim] */
+    SD_FFN_GATE = 7,    /* ffn_gate.weight     [ffn][hidden] */
+    SD_FFN_UP = 8,      /* ffn_up.weight       [ffn][hidden] */
+    SD_FFN_DOWN = 9,    /* ffn_down.weight     [hidden][ffn] */
+    SD_ATTN_NORM = 10,  /* attn_norm.weight    [hidden] F32 */
+    SD_FFN_NORM = 11,   /* ffn_norm.weight     [hidden] F32 */
+    SD_ATTN_Q_BIAS = 12,/* attn_q.bias         [q_dim] F32   (qwen2 only) */
+    SD_ATTN_K_BIAS = 13,/* attn_k.bias         [kv_dim] F32  (qwen2 only) */
+    SD_ATTN_V_BIAS = 14 /* attn_v.bias         [kv_dim] F32  (qwen2 only) */
+};
+
+/* Architectures: llama = interleaved rope_i, no bias (quantized_llama_local.rs);
+ * qwen2 = half-rotation rope, QKV bias (quantized_qwen2_local.rs). */
+enum { SD_ARCH_LLAMA = 0, SD_ARCH_QWEN2 = 1 };
+
+/* Synthetic quantisation mixes for sd_model_synthesize. */
+enum {
+    SD_MIX_Q4_K = 0,     /* every matrix Q4_K */
+    SD_MIX_Q4_K_M = 1,   /* Q6_K on attn_v / ffn_down where llama.cpp's use_more_bits holds, Q4_K elsewhere */
+    SD_MIX_Q5K_Q80 = 2,  /* attention Q5_K, FFN / embedding / lm_head Q8_0 */
+    SD_MIX_Q6_K = 3, SD_MIX_Q5_K = 4, SD_MIX_Q8_0 = 5
+};
+
+/* Model hyper-parameters: the GGUF metadata read at quantized_llama_local.rs:229-238
+ * (llama.*) / quantized_qwen2_local.rs:220-228 (qwen2.*). */
+typedef struct sd_config {
+    int32_t arch;
+    int32_t n_layers;     /* block_count */
+    int32_t hidden;       /* embedding_length */
+    int32_t n_heads;      /* attention.head_count */
+    int32_t n_kv_heads;   /* attention.head_count_kv */
+    int32_t head_dim;     /* embedding_length / head_count (= rope.dimension_count) */
+    int32_t ffn;          /* feed_forward_length */
+    int32_t vocab;
+    float rope_theta;     /* rope.freq_base */
+    float rms_eps;        /* attention.layer_norm_rms_epsilon */
+    int32_t ctx_len;      /* KV capacity in positions (context_length) */
+    int32_t max_batch;    /* rows of one forward pass (<= 128); longer observes are chunked */
+    int32_t tied_output;  /* 1: lm_head reuses token_embd (quantized_llama_local.rs:249-252) */
+    int32_t device;       /* HIP device ordinal */
+} sd_config;
+
+typedef struct sd_model sd_model;
+
+/* ---- lifecycle and weights ------------------------------------------------ */
+
+/* Allocates the handle, KV cache and work buffers; weights start unset.
+ * Replaces LlamaQuantDecoder::from_gguf's allocation (quantized_llama.rs:57-98). */
+sd_status sd_model_create(const sd_config *cfg, sd_model **out);
+void sd_model_destroy(sd_model *m);
+
+/* Uploads one tensor given in its GGUF byte layout (`layer` = -1 for the
+ * global tensors).  Replaces the `ct.tensor(reader, name, device)` loads at
+ * quantized_llama_local.rs:242-281. */
+sd_status sd_model_set_tensor(sd_model *m, int32_t layer, int32_t kind, int32_t fmt, const void *data, size_t bytes);
+/* Downloads one tensor in its GGUF byte layout. */
+sd_status sd_model_get_tensor(sd_model *m, int32_t layer, int32_t kind, void *out, size_t bytes);
+sd_status sd_model_tensor_info(sd_model *m, int32_t layer, int32_t kind, int32_t *fmt, int32_t *rows, int32_t *cols,
+                               size_t *gguf_bytes);
+/* Generates every tensor on the GPU from `seed`: matrices N(0, std)-like values
+ * quantised with `mix`, norms 1.0, biases N(0, std)-like F32. */
+sd_status sd_model_synthesize(sd_model *m, int32_t mix, uint64_t seed, float std);
+/* Exact f32 dequantisation of one tensor (QTensor::dequantize,
+ * quantized_llama_local.rs:242-243): [rows][cols]. */
+sd_status sd_model_dequant_tensor(sd_model *m, int32_t layer, int32_t kind, float *out);
+/* One fused dequant-matmul, y[rows][N] = x[rows][K] . W^T, x rounded to fp16
+ * (QMatMul::forward, quantized_llama_local.rs:47-49, 73-90, 135, 317). */
+sd_status sd_model_qmatmul(sd_model *m, int32_t layer, int32_t kind, const float *x, size_t rows, float *y);
+
+const char *sd_last_error(void);
+
+/* ---- Decoder (model/mod.rs:39-108) ------------------------------------------ */
+size_t sd_vocab_size(const sd_model *m);                      /* Decoder::vocab_size */
+size_t sd_history_len(const sd_model *m);                     /* Decoder::history_len */
+size_t sd_history(const sd_model *m, uint32_t *out, size_t cap); /* Decoder::history (copies min(cap, len)) */
+void sd_reset(sd_model *m);                                   /* Decoder::reset, quantized_llama.rs:512-517 */
+/* Decoder::observe (quantized_llama.rs:519-526): forward + cache the next-token logits. */
+sd_status sd_observe(sd_model *m, const uint32_t *ids, size_t n);
+/* Decoder::next_logits (quantized_llama.rs:528-551): out [vocab]. */
+sd_status sd_next_logits(sd_model *m, float *out);
+/* Decoder::batched_logits (quantized_llama.rs:553-583): out [(k+1)][vocab]; history += drafts. */
+sd_status sd_batched_logits(sd_model *m, const uint32_t *drafts, size_t k, float *out);
+/* Decoder::rollback_to (quantized_llama.rs:585-599). */
+sd_status sd_rollback_to(sd_model *m, size_t len);
+/* Decoder::eos_token_ids (quantized_llama.rs:500-502): caller-supplied at construction in the reference. */
+sd_status sd_set_eos_token_ids(sd_model *m, const uint32_t *ids, size_t n);
+size_t sd_eos_token_ids(const sd_model *m, uint32_t *out, size_t cap);
+
+/* ---- TreeDecoder (model/mod.rs:118-236) -------------------------------------- */
+/* TreeDecoder::tree_logits_keep_kv (quantized_llama.rs:341-394): out_logits [n][vocab],
+ * out_hidden [n][hidden] (final-norm hidden); cache left at prefix + n. */
+sd_status sd_tree_logits_keep_kv(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                 float *out_logits, float *out_hidden);
+/* TreeDecoder::tree_logits (quantized_llama.rs:262-325): strict form, row 0 from an
+ * M=1 pass of the root, cache restored. */
+sd_status sd_tree_logits(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits);
+/* TreeDecoder::commit_tree_path (quantized_llama.rs:409-440): keep [0..P) ++ [P + accepted[j]]. */
+sd_status sd_commit_tree_path(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                              const uint32_t *accepted, size_t n_accepted);
+/* TreeDecoder::last_hidden_state (quantized_llama.rs:193-214): out [hidden]. */
+sd_status sd_last_hidden_state(sd_model *m, float *out);
+/* TreeDecoder::observe_returning_last_hidden (quantized_llama.rs:174-191): out [hidden]. */
+sd_status sd_observe_returning_last_hidden(sd_model *m, const uint32_t *ids, size_t n, float *out);
+/* TreeDecoder::last_hidden_states_multi (quantized_llama.rs:221-250):
+ * out_final [hidden], out_layers [n_layers_requested][hidden]. */
+sd_status sd_last_hidden_states_multi(sd_model *m, const uint32_t *layers, size_t n_layers, float *out_final,
+                                      float *out_layers);
+/* TreeDecoder::apply_lm_head (quantized_llama.rs:112-122): hidden [rows][hidden] -> out [rows][vocab]. */
+sd_status sd_apply_lm_head(sd_model *m, const float *hidden, size_t rows, float *out);
+/* TreeDecoder::embed_tokens (quantized_llama.rs:258-260 via ModelWeights::embed_tokens): out [n][hidden]. */
+sd_status sd_embed_tokens(sd_model *m, const uint32_t *ids, size_t n, float *out);
+size_t sd_num_hidden_layers(const sd_model *m);               /* TreeDecoder::num_hidden_layers */
+size_t sd_hidden_size(const sd_model *m);                     /* LlamaQuantDecoder::hidden_size */
+
+/* ---- device acceptance (the logits never leave HBM) ------------------------- */
+/* batched_logits + the greedy walk of vanilla.rs:178-210 at temperature 0:
+ * commits = drafts[..a] ++ [argmax(row a)], a = accepted drafts.  State as
+ * after sd_batched_logits; the caller re-anchors with rollback_to + observe
+ * (vanilla.rs:219-223).  commits has room for k+1 entries. */
+sd_status sd_verify_greedy_linear(sd_model *m, const uint32_t *drafts, size_t k, uint32_t *commits,
+                                  size_t *n_commit, size_t *n_accepted);
+/* tree_logits_keep_kv + the greedy longest-path walk of eagle.rs:605-661
+ * (eagle3.rs:714-756): path = accepted node indices from the root (room for n),
+ * bonus = argmax of the deepest accepted row, bonus_node = the first child of
+ * that node carrying the bonus token or -1 (eagle.rs:700-709; -1 when strict).
+ * strict != 0 takes row 0 from next_logits (EagleRunConfig::strict_root_gemv). */
+sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                int32_t strict, uint32_t *path, size_t *path_len, uint32_t *bonus,
+                                int32_t *bonus_node);
+/* First-max argmax of each row of the last verify pass (eagle.rs:626-637 fold). */
+sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n);
+
+/* ---- synthetic state and measurement ---------------------------------------- */
+/* Sets history = ids and fills KV rows [0, n) with seeded N(0,1)-like fp16
+ * values; the next-token logits cache is invalid afterwards. */
+sd_status sd_prime_synthetic(sd_model *m, const uint32_t *ids, size_t n, uint64_t kv_seed);
+/* Enables (1) / disables (0) HIP-event timing of every quantised matmul launch. */
+sd_status sd_profile_enable(sd_model *m, int32_t on);
+/* Reads and clears the timed launches: class ids (0 qkv, 1 wo, 2 gate_up,
+ * 3 down, 4 lm_head), algorithmic weight bytes and milliseconds.  Returns the
+ * number of entries written. */
+size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap);
+sd_status sd_synchronize(sd_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPECULATE_HIP_H */

@@ -1,0 +1,96 @@
+"""GPU parity of the block generator, the exact dequantiser and the fused
+dequant-matmul (K1) against the CPU oracle, through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle as O
+from _models import MIX_IDS, all_tensor_keys, hip_cfg, oracle_cfg, rel_err
+
+pytestmark = pytest.mark.gpu
+
+MIXES = ["q4_k", "q4_k_m", "q5k_q80", "q6_k", "q5_k", "q8_0"]
+
+
+def _model(hip, mix, **over):
+    ocfg = oracle_cfg(mix=mix, **over)
+    dec = hip.HipQuantDecoder(hip_cfg(hip, ocfg))
+    dec.synthesize(MIX_IDS[mix], ocfg.seed, ocfg.weight_std)
+    return ocfg, dec
+
+
+@pytest.mark.parametrize("mix", MIXES)
+def test_synth_blocks_bit_exact(hip, mix):
+    """GPU generator == CPU generator, byte for byte, for every tensor."""
+    ocfg, dec = _model(hip, mix, n_layers=2, vocab=2048)
+    for (li, k) in all_tensor_keys(ocfg):
+        fmt, expect = O.synth_tensor(ocfg, li, k)
+        f, rows, K, nbytes = dec.tensor_info(li, k)
+        assert f == fmt and nbytes == expect.size, (li, k)
+        got = dec.get_tensor(li, k)
+        assert np.array_equal(got, expect), (mix, li, k)
+
+
+@pytest.mark.parametrize("mix", MIXES)
+def test_dequant_bit_exact(hip, mix):
+    """Device dequantisation (device block layout) == oracle dequantisation, bitwise."""
+    ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
+    for (li, k) in all_tensor_keys(ocfg):
+        fmt, raw = O.synth_tensor(ocfg, li, k)
+        if fmt == O.F32:
+            continue
+        rows, K = ocfg.shape(k)
+        got = dec.dequant_tensor(li, k)
+        exp = O.dequant_matrix(fmt, raw, rows, K)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), (mix, li, k)
+
+
+@pytest.mark.parametrize("mix", ["q4_k", "q6_k", "q8_0"])
+def test_set_tensor_roundtrip(hip, mix):
+    """Host GGUF bytes -> device layout -> GGUF bytes is the identity."""
+    ocfg = oracle_cfg(mix=mix, n_layers=1, vocab=2048)
+    dec = hip.HipQuantDecoder(hip_cfg(hip, ocfg))
+    rng = np.random.default_rng(3)
+    fmt = ocfg.fmt(0, O.K_FFN_DOWN)
+    rows, K = ocfg.shape(O.K_FFN_DOWN)
+    raw = O.quantize(fmt, rng.standard_normal(rows * K).astype(np.float32) * 0.02)
+    dec.set_tensor(0, O.K_FFN_DOWN, fmt, raw)
+    assert np.array_equal(dec.get_tensor(0, O.K_FFN_DOWN), raw)
+    got = dec.dequant_tensor(0, O.K_FFN_DOWN)
+    assert np.array_equal(got.view(np.uint32), O.dequant_matrix(fmt, raw, rows, K).view(np.uint32))
+
+
+CASES = [("q4_k", 0, O.K_ATTN_Q), ("q4_k", 0, O.K_FFN_DOWN), ("q6_k", 0, O.K_FFN_GATE),
+         ("q5_k", 0, O.K_ATTN_O), ("q8_0", 0, O.K_FFN_UP), ("q8_0", 0, O.K_ATTN_K)]
+
+
+@pytest.mark.parametrize("mix,layer,kind", CASES)
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 60, 64, 100, 128])
+def test_qmatmul_vs_oracle(hip, mix, layer, kind, M):
+    """K1 against (a) fp16-rounded operands with f64 accumulation (tight) and
+    (b) the f32 oracle QMatMul (the 1e-2 relative contract)."""
+    ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
+    fmt, raw = O.synth_tensor(ocfg, layer, kind)
+    rows, K = ocfg.shape(kind)
+    W = O.dequant_matrix(fmt, raw, rows, K)
+    x = np.random.default_rng(M * 7 + kind).standard_normal((M, K)).astype(np.float32)
+    y = dec.qmatmul(layer, kind, x)
+    ref16 = O.round_f16(x).astype(np.float64) @ O.round_f16(W).astype(np.float64).T
+    ref32 = x.astype(np.float64) @ W.astype(np.float64).T
+    assert rel_err(y, ref16) < 1e-4, rel_err(y, ref16)
+    assert rel_err(y, ref32) < 1e-2, rel_err(y, ref32)
+
+
+@pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q6_k", O.K_FFN_DOWN), ("q8_0", O.K_FFN_UP),
+                                      ("q5_k", O.K_ATTN_V)])
+def test_qmatmul_m_invariant(hip, mix, kind):
+    """Row i of an M-row product equals the single-row product bit for bit, for
+    every M (tile shape changes at 16/32/64 rows)."""
+    ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
+    K = ocfg.shape(kind)[1]
+    x = np.random.default_rng(11).standard_normal((128, K)).astype(np.float32)
+    singles = [dec.qmatmul(0, kind, x[i:i + 1])[0] for i in (0, 3, 15, 16, 63, 64, 127)]
+    for M in (5, 16, 17, 60, 64, 65, 128):
+        y = dec.qmatmul(0, kind, x[:M])
+        for j, i in enumerate((0, 3, 15, 16, 63, 64, 127)):
+            if i < M:
+                assert np.array_equal(y[i].view(np.uint32), singles[j].view(np.uint32)), (M, i)
