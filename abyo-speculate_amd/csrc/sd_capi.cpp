@@ -350,4 +350,23 @@ sd_status sd_synchronize(sd_model *m) {
     });
 }
 
+sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t head, size_t pos0, size_t n,
+                          uint16_t *out) {
+    return guard([&] {
+        need(m);
+        const sd::ModelCfg &c = m->model->cfg;
+        if (!out) throw sd::ArgError("null output");
+        if (layer < 0 || layer >= c.n_layers || which < 0 || which > 1 || head < 0 || head >= c.n_kv_heads)
+            throw sd::ArgError("kv row selector out of range");
+        if (pos0 + n > (size_t)m->model->cap) throw sd::ArgError("kv rows out of range");
+        setdev(m);
+        const uint16_t *base = m->model->kv + (((int64_t)layer * 2 + which) * c.n_kv_heads + head) * m->model->cap *
+                                                  c.head_dim;
+        SD_HIP_CHECK(hipStreamSynchronize(m->model->st));
+        SD_HIP_CHECK(hipMemcpy(out, base + pos0 * c.head_dim, n * c.head_dim * 2, hipMemcpyDeviceToHost));
+    });
+}
+
+size_t sd_cache_len(const sd_model *m) { return m && m->dec ? (size_t)m->dec->cache_len : 0; }
+
 }  // extern "C"

@@ -33,10 +33,13 @@ static int64_t gguf_row_bytes(int fmt, int64_t K) {
     return K / fmt_block_elems(fmt) * fmt_block_bytes(fmt);
 }
 
+// Zeroed device allocation.  The fill runs on the null stream, which does not
+// order against the model's non-blocking stream, so wait for it here.
 template <typename T> static T *dalloc(size_t n) {
     void *p = nullptr;
     SD_HIP_CHECK(hipMalloc(&p, n * sizeof(T) + 256));
     SD_HIP_CHECK(hipMemset(p, 0, n * sizeof(T) + 256));
+    SD_HIP_CHECK(hipDeviceSynchronize());
     return (T *)p;
 }
 

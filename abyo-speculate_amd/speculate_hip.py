@@ -140,6 +140,8 @@ def load_library(path: str = LIB_PATH):
         "sd_profile_enable": ([P, I32], I32),
         "sd_profile_read": ([P, P, P, P, SZ], SZ),
         "sd_synchronize": ([P], I32),
+        "sd_read_kv_rows": ([P, I32, I32, I32, SZ, SZ, P], I32),
+        "sd_cache_len": ([P], SZ),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -373,3 +375,11 @@ class HipQuantDecoder:
 
     def synchronize(self):
         _check(_lib.sd_synchronize(self._h))
+
+    def read_kv_rows(self, layer: int, which: int, head: int, pos0: int, n: int) -> np.ndarray:
+        out = np.empty((n, self.cfg.head_dim), np.uint16)
+        _check(_lib.sd_read_kv_rows(self._h, layer, which, head, pos0, n, _ptr(out)))
+        return out
+
+    def cache_len(self) -> int:
+        return int(_lib.sd_cache_len(self._h))

@@ -196,6 +196,12 @@ sd_status sd_profile_enable(sd_model *m, int32_t on);
  * number of entries written. */
 size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap);
 sd_status sd_synchronize(sd_model *m);
+/* Copies n fp16 cache rows [pos0, pos0+n) of one (layer, K=0/V=1, kv head):
+ * out [n][head_dim] (checks of the in-place KV layout). */
+sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t head, size_t pos0, size_t n,
+                          uint16_t *out);
+/* Number of positions currently held in the KV cache. */
+size_t sd_cache_len(const sd_model *m);
 
 #ifdef __cplusplus
 }
