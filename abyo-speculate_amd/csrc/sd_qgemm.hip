@@ -395,6 +395,7 @@ int launch_qgemm(const GemmParams &p, hipStream_t st) {
         case 1: launch_rt_ct<2, 1>(p, nwg, st); break;
         case 2: launch_rt_ct<2, 2>(p, nwg, st); break;
         case 4: launch_rt_ct<2, 4>(p, nwg, st); break;
+        case 8: launch_rt_ct<2, 8>(p, nwg, st); break;
         default: throw BackendError("qgemm: unsupported tile");
         }
     } else {

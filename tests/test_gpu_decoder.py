@@ -1,0 +1,223 @@
+"""Decoder-level GPU parity (through the C ABI) against the oracle decoder.
+
+Contract (per the path's spec): logits and hidden states within 1e-2
+relative (max |a-b| / max |b| per row block); greedy acceptance results
+identical except where the oracle row has a near tie (top-2 margin below the
+logits tolerance); KV compaction bit-exact (a pure row copy).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from _models import MIX_IDS, hip_cfg, oracle_cfg, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+_WEIGHTS = {}
+
+
+def make_pair(hip, prefix_len=128, seed=1, **over):
+    ocfg = oracle_cfg(**over)
+    key = tuple(sorted(over.items()))
+    if key not in _WEIGHTS:
+        _WEIGHTS[key] = O.OracleModel(ocfg).raw
+    om = O.OracleModel(ocfg, _WEIGHTS[key])
+    od = O.OracleDecoder(om)
+    hd = hip.HipQuantDecoder(hip_cfg(hip, ocfg))
+    hd.synthesize(MIX_IDS[ocfg.mix], ocfg.seed, ocfg.weight_std)
+    prefix = [int(v) for v in np.random.default_rng(seed).integers(0, ocfg.vocab, prefix_len)]
+    od.observe(prefix)
+    hd.observe(prefix)
+    return od, hd, prefix
+
+
+def safe(row: np.ndarray) -> bool:
+    s = np.sort(row.astype(np.float64))[::-1]
+    return (s[0] - s[1]) > 4 * TOL * np.max(np.abs(row))
+
+
+def greedy_chain(od, n):
+    """The oracle's own greedy continuation (then restored)."""
+    L = len(od.history)
+    chain = []
+    for _ in range(n):
+        g = O.argmax_fold(od.next_logits())
+        chain.append(g)
+        od.observe([g])
+    od.rollback_to(L)
+    return chain
+
+
+def test_observe_and_next_logits(hip):
+    od, hd, _ = make_pair(hip)
+    a, b = hd.next_logits(), od.next_logits()
+    assert rel_err(a, b) < TOL
+    if safe(b):
+        assert int(np.argmax(a)) == O.argmax_fold(b)
+    assert hd.history() == od.history and hd.cache_len() == len(od.history)
+
+
+def test_batched_logits_and_greedy_linear(hip):
+    od, hd, prefix = make_pair(hip)
+    chain = greedy_chain(od, 4)
+    drafts = [chain[0], chain[1], (chain[2] + 1) % 32000, chain[3]]
+    L = len(prefix)
+    b = od.batched_logits(drafts)
+    a = hd.batched_logits(drafts)
+    assert a.shape == b.shape == (5, 32000)
+    for i in range(5):
+        assert rel_err(a[i], b[i]) < TOL, i
+    assert hd.history() == od.history
+    # device greedy acceptance == oracle walk on oracle logits
+    hd.rollback_to(L)
+    commits, n_acc = hd.verify_greedy_linear(drafts)
+    am = [O.argmax_fold(r) for r in b]
+    exp_acc, exp_bonus = O.greedy_linear_accept(drafts, am)
+    if all(safe(b[i]) for i in range(exp_acc + 1)):
+        assert n_acc == exp_acc == 2
+        assert commits == drafts[:exp_acc] + [exp_bonus]
+    # device argmax == host first-max fold of the device logits (bit-exact logic)
+    got_am = hd.last_argmax(5)
+    assert [int(v) for v in got_am] == [O.argmax_fold(r) for r in a]
+
+
+def _tree_with_chain(chain, vocab, seed=5):
+    rng = np.random.default_rng(seed)
+    r = [int(v) for v in rng.integers(0, vocab, 8)]
+    cands = [[r[0], chain[0], r[1]], [chain[1], r[2]], [r[3], chain[2]]]
+    return cands
+
+
+def test_tree_keep_kv_verify_and_commit(hip):
+    od, hd, prefix = make_pair(hip)
+    chain = greedy_chain(od, 3)
+    tree = O.build_cartesian_tree(prefix[-1], _tree_with_chain(chain, 32000))
+    n = len(tree)
+    P = len(prefix) - 1
+    lo, ho = od.tree_logits_keep_kv(tree)
+    lg, hg = hd.tree_logits_keep_kv(tree)
+    for i in range(n):
+        assert rel_err(lg[i], lo[i]) < TOL, i
+        assert rel_err(hg[i], ho[i]) < TOL, i
+    assert hd.cache_len() == P + n
+    # device walk on a fresh copy of the state
+    hd.rollback_to(len(prefix))
+    path, bonus, bnode = hd.verify_greedy_tree(tree)
+    am_o = [O.argmax_fold(r) for r in lo]
+    best, exp_bonus = O.greedy_tree_accept(tree, lo, am_o)
+    if all(safe(lo[i]) for i in range(n)):
+        assert path == best and bonus == exp_bonus
+        assert bnode == (O.bonus_in_tree(tree, best[-1], exp_bonus) or -1)
+        assert len(best) == 4  # root + the embedded 3-token greedy chain
+    # KV compaction: rows [P, P+len(keep)) become the selected tree rows, bit for bit
+    keep = path + ([bnode] if bnode >= 0 else [])
+    before = {(l, w, h): hd.read_kv_rows(l, w, h, P, n) for l in (0, 3) for w in (0, 1) for h in (0, 7)}
+    prefix_rows = hd.read_kv_rows(2, 0, 5, 0, P)
+    hd.commit_tree_path(tree, keep)
+    for (l, w, h), rows in before.items():
+        after = hd.read_kv_rows(l, w, h, P, len(keep))
+        assert np.array_equal(after, rows[keep]), (l, w, h)
+    assert np.array_equal(hd.read_kv_rows(2, 0, 5, 0, P), prefix_rows)
+    assert hd.cache_len() == P + len(keep)
+    assert hd.history() == prefix + [tree.token_at(i) for i in keep[1:]]
+    # continue: both sides commit the same path and observe the bonus if it was not in the tree
+    od.commit_tree_path(tree, keep)
+    if bnode < 0:
+        od.observe([bonus])
+        hd.observe([bonus])
+    a, b = hd.next_logits(), od.next_logits()
+    assert rel_err(a, b) < TOL
+
+
+def test_strict_root_row_is_m_invariant(hip):
+    """Row 0 of a tree pass equals the single-token pass bit for bit, so the
+    strict (GEMV-root) mode changes nothing."""
+    od, hd, prefix = make_pair(hip)
+    chain = greedy_chain(od, 3)
+    tree = O.build_cartesian_tree(prefix[-1], _tree_with_chain(chain, 32000))
+    nl = hd.next_logits()
+    strict = hd.tree_logits(tree)
+    assert hd.cache_len() == len(prefix)
+    fast, _ = hd.tree_logits_keep_kv(tree)
+    assert np.array_equal(strict[0].view(np.uint32), nl.view(np.uint32))
+    assert np.array_equal(fast[0].view(np.uint32), nl.view(np.uint32))
+    assert np.array_equal(strict[1:].view(np.uint32), fast[1:].view(np.uint32))
+
+
+def test_error_semantics_keep_state(hip):
+    od, hd, prefix = make_pair(hip, prefix_len=16)
+    fresh = hip.HipQuantDecoder(hd.cfg)
+    fresh.synthesize(0, 1)
+    for call in (fresh.next_logits, lambda: fresh.batched_logits([1]), lambda: fresh.last_hidden_state(),
+                 lambda: fresh.tree_logits_keep_kv(O.DraftTree.linear(1, [2])),
+                 lambda: fresh.commit_tree_path(O.DraftTree.linear(1, [2]), [0])):
+        with pytest.raises(hip.SamplingError):
+            call()
+    with pytest.raises(hip.CacheRollbackError):
+        fresh.rollback_to(1)
+    with pytest.raises(hip.SamplingError):
+        fresh.observe_returning_last_hidden([])
+    fresh.observe([])  # empty observe is a no-op
+    assert fresh.history() == []
+    # root mismatch / bad parent table leave history and cache untouched
+    h0, c0 = hd.history(), hd.cache_len()
+    with pytest.raises(hip.SamplingError):
+        hd.tree_logits_keep_kv(O.DraftTree.linear(prefix[-1] + 1, [3]))
+    with pytest.raises(hip.SamplingError):
+        hd.tree_logits_keep_kv(([prefix[-1], 5, 6], [0, 2, 0]))
+    with pytest.raises(hip.CacheRollbackError):
+        hd.rollback_to(len(prefix) + 1)
+    assert hd.history() == h0 and hd.cache_len() == c0
+    # rollback then next_logits replays the last token (truncate-and-replay path)
+    hd.rollback_to(len(prefix) - 3)
+    od.rollback_to(len(prefix) - 3)
+    assert rel_err(hd.next_logits(), od.next_logits()) < TOL
+    with pytest.raises(hip.ArgError):
+        hd.observe([40000])
+
+
+def test_hidden_state_apis(hip):
+    od, hd, prefix = make_pair(hip, prefix_len=32)
+    hs = hd.last_hidden_state()
+    od.rollback_to(len(prefix) - 1)
+    final, mids = od.m.forward([prefix[-1]], [len(prefix) - 1], np.ones((1, len(prefix)), bool), (1, 2))
+    od.cache_len = len(prefix)
+    od.history = list(prefix)
+    assert rel_err(hs, final[0]) < TOL
+    fin, hm = hd.last_hidden_states_multi([1, 2])
+    assert rel_err(fin, final[0]) < TOL
+    assert rel_err(hm[0], mids[0][0]) < TOL and rel_err(hm[1], mids[1][0]) < TOL
+    # embeddings are the exact dequantised rows
+    ids = [0, 5, 31999, prefix[3]]
+    assert np.array_equal(hd.embed_tokens(ids), od.m.embed(ids))
+    # apply_lm_head on arbitrary hidden rows
+    h = np.random.default_rng(2).standard_normal((3, 512)).astype(np.float32)
+    assert rel_err(hd.apply_lm_head(h), od.m.lm_head(h)) < TOL
+    # observe_returning_last_hidden == oracle forward of the same token
+    hn = hd.observe_returning_last_hidden([7, 8])
+    P = len(od.history)
+    fo, _ = od.m.forward([7, 8], [P, P + 1], O.causal_mask(P, 2))
+    assert rel_err(hn, fo[-1]) < TOL
+    assert hd.history() == prefix + [7, 8]
+
+
+@pytest.mark.parametrize("over", [
+    dict(n_kv_heads=2, mix="q4_k_m", n_layers=3),
+    dict(arch="qwen2", n_kv_heads=2, mix="q5k_q80", n_layers=2, rms_eps=1e-6, rope_theta=1e6),
+    dict(n_heads=4, n_kv_heads=1, head_dim=128, mix="q6_k", n_layers=2),
+])
+def test_variants_batched_and_tree(hip, over):
+    od, hd, prefix = make_pair(hip, prefix_len=70, **over)
+    drafts = greedy_chain(od, 5)
+    b = od.batched_logits(drafts)
+    a = hd.batched_logits(drafts)
+    for i in range(len(drafts) + 1):
+        assert rel_err(a[i], b[i]) < TOL, (over, i)
+    hd.rollback_to(len(prefix))
+    od.rollback_to(len(prefix))
+    tree = O.build_cartesian_tree(prefix[-1], [[drafts[0], 3, 4], [drafts[1], 9], [drafts[2]]])
+    lo, _ = od.tree_logits_keep_kv(tree)
+    lg, _ = hd.tree_logits_keep_kv(tree)
+    for i in range(len(tree)):
+        assert rel_err(lg[i], lo[i]) < TOL, (over, i)
