@@ -330,10 +330,9 @@ size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size
     size_t n = 0;
     for (auto &e : P) {
         if (n >= cap) break;
-        int c = e.name == "qkv" ? 0 : e.name == "wo" ? 1 : e.name == "gate_up" ? 2 : e.name == "down" ? 3 : 4;
         float t = 0.f;
-        (void)hipEventElapsedTime(&t, e.a, e.b);
-        if (cls) cls[n] = c;
+        (void)hipEventElapsedTime(&t, m->model->ev_pool[e.ev], m->model->ev_pool[e.ev + 1]);
+        if (cls) cls[n] = e.cls;
         if (bytes) bytes[n] = e.bytes;
         if (ms) ms[n] = t;
         n++;
@@ -368,5 +367,33 @@ sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t hea
 }
 
 size_t sd_cache_len(const sd_model *m) { return m && m->dec ? (size_t)m->dec->cache_len : 0; }
+
+sd_status sd_tree_cartesian(uint32_t root, const uint32_t *cand, const uint32_t *branching, size_t depth,
+                            uint32_t *tokens, uint32_t *parents, size_t cap, size_t *n) {
+    return guard([&] {
+        if (!n || (depth && (!cand || !branching))) throw sd::ArgError("null argument");
+        const size_t need = sd::cartesian_size(branching, depth);
+        *n = need;
+        if (!tokens || !parents) return;  // size query
+        if (need > cap) throw sd::ArgError("output capacity smaller than the Cartesian tree");
+        const sd::DraftTreeC t = sd::cartesian_tree(root, cand, branching, depth);
+        std::memcpy(tokens, t.tokens.data(), need * 4);
+        std::memcpy(parents, t.parents.data(), need * 4);
+    });
+}
+
+sd_status sd_tree_prune(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *log_probs,
+                        const uint32_t *branching, size_t depth, size_t max_total, uint32_t *out_tokens,
+                        uint32_t *out_parents, size_t *n_out) {
+    return guard([&] {
+        if (!tokens || !parents || !out_tokens || !out_parents || !n_out || (depth && (!log_probs || !branching)))
+            throw sd::ArgError("null argument");
+        const sd::DraftTreeC full = sd::DraftTreeC::from_arrays(tokens, parents, n);
+        const sd::DraftTreeC t = sd::prune_cartesian(full, log_probs, branching, depth, max_total);
+        std::memcpy(out_tokens, t.tokens.data(), t.size() * 4);
+        std::memcpy(out_parents, t.parents.data(), t.size() * 4);
+        *n_out = t.size();
+    });
+}
 
 }  // extern "C"

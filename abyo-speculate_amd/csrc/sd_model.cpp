@@ -74,10 +74,7 @@ Model::~Model() {
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
-    for (auto &e : prof) {
-        hipEventDestroy(e.a);
-        hipEventDestroy(e.b);
-    }
+    for (hipEvent_t e : ev_pool) hipEventDestroy(e);
     if (st) hipStreamDestroy(st);
 }
 
@@ -302,25 +299,45 @@ void Model::fill_kv_synthetic(int P, uint64_t seed) {
     SD_HIP_CHECK(hipStreamSynchronize(st));
 }
 
-void Model::prof_reset() {
-    for (auto &e : prof) {
-        hipEventDestroy(e.a);
-        hipEventDestroy(e.b);
+void Model::prof_reset() { prof.clear(); }
+
+int Model::prof_begin() {
+    const size_t need = 2 * (prof.size() + 1);
+    while (ev_pool.size() < need) {
+        hipEvent_t e;
+        SD_HIP_CHECK(hipEventCreate(&e));
+        ev_pool.push_back(e);
     }
-    prof.clear();
+    const int ev = (int)(2 * prof.size());
+    SD_HIP_CHECK(hipEventRecord(ev_pool[ev], st));
+    return ev;
 }
 
-void Model::run_gemm(GemmParams &p, const char *name, double bytes) {
+void Model::prof_end(int ev, int cls, double bytes) {
+    SD_HIP_CHECK(hipEventRecord(ev_pool[ev + 1], st));
+    prof.push_back(ProfEntry{cls, bytes, ev});
+}
+
+// Algorithmic bytes of one dequant-matmul launch: the weight blocks (given),
+// the fp16 activations read once, and the output written once (read too when
+// the epilogue adds the residual).
+static double gemm_bytes(const GemmParams &p, double wbytes) {
+    const double x = 2.0 * p.M * p.K;
+    double y = 0.0;
+    if (p.mode == GM_SWIGLU) {
+        y = 2.0 * p.M * p.seg[0].rows;
+    } else {
+        for (int i = 0; i < p.nseg; i++) y += 4.0 * p.M * p.seg[i].rows * (p.mode == GM_RESID ? 2 : 1);
+    }
+    return wbytes + x + y;
+}
+
+void Model::run_gemm(GemmParams &p, int cls, double bytes) {
+    bytes = gemm_bytes(p, bytes);
     if (prof_on) {
-        ProfEntry e;
-        e.name = name;
-        e.bytes = bytes;
-        SD_HIP_CHECK(hipEventCreate(&e.a));
-        SD_HIP_CHECK(hipEventCreate(&e.b));
-        SD_HIP_CHECK(hipEventRecord(e.a, st));
+        const int ev = prof_begin();
         launch_qgemm(p, st);
-        SD_HIP_CHECK(hipEventRecord(e.b, st));
-        prof.push_back(e);
+        prof_end(ev, cls, bytes);
     } else {
         launch_qgemm(p, st);
     }
@@ -408,7 +425,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = H;
             p.M = M;
             p.mode = GM_STORE;
-            run_gemm(p, "qkv", wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
+            run_gemm(p, PC_QKV, wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
         }
         {
             RopeKvParams r{};
@@ -447,7 +464,15 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             a.part_ml = part_ml;
             a.out16 = ap;
             a.out_ld = ap_ld;
-            launch_attention(a, st);
+            if (prof_on) {
+                // K and V rows read once per layer: [0, P + M) of every KV head
+                const double kvb = 2.0 * c.n_kv_heads * (double)(P + M) * c.head_dim * 2.0;
+                const int ev = prof_begin();
+                launch_attention(a, st);
+                prof_end(ev, PC_ATTN, kvb);
+            } else {
+                launch_attention(a, st);
+            }
         }
         {
             GemmParams p{};
@@ -458,7 +483,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = QD;
             p.M = M;
             p.mode = GM_RESID;
-            run_gemm(p, "wo", wbytes(L[K_ATTN_O]));
+            run_gemm(p, PC_WO, wbytes(L[K_ATTN_O]));
         }
         launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
         {
@@ -474,7 +499,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.act = act;
             p.act_ld = act_ld;
             if (L[K_FFN_GATE].fmt != L[K_FFN_UP].fmt) throw UnsupportedError("ffn_gate and ffn_up must share a format");
-            run_gemm(p, "gate_up", wbytes(L[K_FFN_GATE]) + wbytes(L[K_FFN_UP]));
+            run_gemm(p, PC_GATE_UP, wbytes(L[K_FFN_GATE]) + wbytes(L[K_FFN_UP]));
         }
         {
             GemmParams p{};
@@ -485,7 +510,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = c.ffn;
             p.M = M;
             p.mode = GM_RESID;
-            run_gemm(p, "down", wbytes(L[K_FFN_DOWN]));
+            run_gemm(p, PC_DOWN, wbytes(L[K_FFN_DOWN]));
         }
         for (size_t ci = 0; ci < collect.size(); ci++)
             if (collect[ci] == l)
@@ -511,7 +536,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         if (xp_ld != H) throw UnsupportedError("lm_head needs hidden == q_dim activations stride");
         p.amax_ld = qgemm_workgroups(p);
         if (p.amax_ld > amax_ld) throw BackendError("argmax workspace too small");
-        run_gemm(p, "lm_head", wbytes(W));
+        run_gemm(p, PC_LM_HEAD, wbytes(W));
         launch_argmax_reduce(amax_v, amax_i, p.amax_ld, rows, argmax, st);
         logits_rows_last = rows;
     }

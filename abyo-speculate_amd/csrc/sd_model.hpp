@@ -58,10 +58,13 @@ struct DevTensor {
 };
 
 // Per-kernel-class timing collected with HIP events on the model's stream.
+// Classes: 0 qkv, 1 wo, 2 gate_up, 3 down, 4 lm_head (the dequant-matmul
+// launches) and 5 attn (split attention + combine of one layer).
+enum ProfClass : int { PC_QKV = 0, PC_WO = 1, PC_GATE_UP = 2, PC_DOWN = 3, PC_LM_HEAD = 4, PC_ATTN = 5 };
 struct ProfEntry {
-    std::string name;
+    int cls;
     double bytes;  // algorithmic bytes of the launch
-    hipEvent_t a, b;
+    int ev;        // index of the start event in the pool; the stop event is ev + 1
 };
 
 struct DraftTreeC;
@@ -97,10 +100,15 @@ class Model {
     void embed_rows(const int *ids, int n, float *out_host);
     void compact_tail(int P, const std::vector<int> &src);
 
-    // profiling of the dominant kernels
+    // profiling of the dominant kernels (events come from a pool that grows
+    // on demand and is reused after every read, so timing adds no allocation
+    // to a steady-state step)
     bool prof_on = false;
     std::vector<ProfEntry> prof;
+    std::vector<hipEvent_t> ev_pool;
     void prof_reset();
+    int prof_begin();                              // records a start event, returns its index
+    void prof_end(int ev, int cls, double bytes);  // records the stop event
 
     // device buffers
     uint16_t *kv = nullptr;  // [L][2][n_kv][cap][hd]
@@ -124,7 +132,7 @@ class Model {
 
   private:
     void alloc_buffers();
-    void run_gemm(GemmParams &p, const char *name, double bytes);
+    void run_gemm(GemmParams &p, int cls, double bytes);
     uint16_t *kc(int layer) const { return kv + (int64_t)layer * 2 * cfg.n_kv_heads * cap * cfg.head_dim; }
     uint16_t *vc(int layer) const { return kc(layer) + (int64_t)cfg.n_kv_heads * cap * cfg.head_dim; }
 };
@@ -180,5 +188,11 @@ struct DraftTreeC {
     std::vector<std::vector<size_t>> paths() const;
     void masks(std::vector<uint64_t> &words, int &nw) const;
 };
+
+// Tree builders (sd_tree.cpp): medusa.rs:172-193 and eagle.rs:763-845.
+DraftTreeC cartesian_tree(uint32_t root, const uint32_t *cand, const uint32_t *branching, size_t depth);
+size_t cartesian_size(const uint32_t *branching, size_t depth);
+DraftTreeC prune_cartesian(const DraftTreeC &full, const float *log_probs, const uint32_t *branching, size_t depth,
+                           size_t max_total);
 
 }  // namespace sd

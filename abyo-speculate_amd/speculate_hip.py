@@ -30,7 +30,7 @@ F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
  ATTN_NORM, FFN_NORM, ATTN_Q_BIAS, ATTN_K_BIAS, ATTN_V_BIAS) = range(15)
 ARCH_LLAMA, ARCH_QWEN2 = 0, 1
 MIX_Q4_K, MIX_Q4_K_M, MIX_Q5K_Q80, MIX_Q6_K, MIX_Q5_K, MIX_Q8_0 = range(6)
-PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head")
+PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head", "attn")
 
 
 class SpeculateError(Exception):
@@ -142,6 +142,8 @@ def load_library(path: str = LIB_PATH):
         "sd_synchronize": ([P], I32),
         "sd_read_kv_rows": ([P, I32, I32, I32, SZ, SZ, P], I32),
         "sd_cache_len": ([P], SZ),
+        "sd_tree_cartesian": ([ctypes.c_uint32, P, P, SZ, P, P, SZ, pSZ], I32),
+        "sd_tree_prune": ([P, P, SZ, P, P, SZ, SZ, P, P, pSZ], I32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -383,3 +385,30 @@ class HipQuantDecoder:
 
     def cache_len(self) -> int:
         return int(_lib.sd_cache_len(self._h))
+
+
+# ---- draft-tree builders (host only) ----
+def tree_cartesian(root: int, head_top_k: Sequence[Sequence[int]]) -> Tuple[np.ndarray, np.ndarray]:
+    """build_cartesian_tree (methods/medusa.rs:172-193) -> (tokens, parents)."""
+    L = load_library()
+    br = _u32([len(c) for c in head_top_k])
+    cand = _u32([t for c in head_top_k for t in c]) if len(br) else _u32([0])
+    n = ctypes.c_size_t()
+    _check(L.sd_tree_cartesian(root, _ptr(cand), _ptr(br), br.size, None, None, 0, ctypes.byref(n)))
+    toks, pars = np.empty(n.value, np.uint32), np.empty(n.value, np.uint32)
+    _check(L.sd_tree_cartesian(root, _ptr(cand), _ptr(br), br.size, _ptr(toks), _ptr(pars), n.value,
+                               ctypes.byref(n)))
+    return toks, pars
+
+
+def tree_prune(tree, per_step_log_probs: Sequence[Sequence[float]], max_total: int) -> Tuple[np.ndarray, np.ndarray]:
+    """prune_cartesian_tree (methods/eagle.rs:763-845) -> (tokens, parents)."""
+    L = load_library()
+    t, p = tree_arrays(tree)
+    br = _u32([len(r) for r in per_step_log_probs])
+    lp = np.ascontiguousarray([v for r in per_step_log_probs for v in r] or [0.0], np.float32)
+    ot, op = np.empty(t.size, np.uint32), np.empty(t.size, np.uint32)
+    n = ctypes.c_size_t()
+    _check(L.sd_tree_prune(_ptr(t), _ptr(p), t.size, _ptr(lp), _ptr(br), br.size, max_total, _ptr(ot), _ptr(op),
+                           ctypes.byref(n)))
+    return ot[:n.value].copy(), op[:n.value].copy()

@@ -1,0 +1,258 @@
+"""Verify-step benchmark of the MI355X target-verify path (one GPU).
+
+Workload (the headline one): a Llama-3-8B-shaped Q4_K_M target (32 layers,
+hidden 4096, 32 query / 8 KV heads, head_dim 128, FFN 14336, vocab 128256,
+RoPE theta 500000; Q6_K on attn_v / ffn_down in the 16 use_more_bits layers,
+Q4_K elsewhere including lm_head), random-init weights N(0, 0.02) synthesised
+on the GPU, 512 fp16 KV positions filled with N(0, 1)-like values.
+
+  step = one linear verify of k=4 draft tokens (M=5 rows: the last committed
+         token + 4 drafts) with greedy acceptance on the device
+         (sd_verify_greedy_linear), then rollback_to() the pre-verify length
+         so every step verifies at the same KV length.
+
+The same run also times the 60-node tree verify of the same weights: a
+(4,3,2,2,1,1) Cartesian draft tree pruned to 60 nodes (depth 6) over 4096 KV
+positions, greedy longest-path acceptance and compaction of the accepted
+path's KV rows (sd_verify_greedy_tree + sd_commit_tree_path), then rollback.
+
+Timing: W untimed warmup steps, then K steps bracketed by device
+synchronisation.  A second pass of K steps with HIP-event timing on the
+decoder's stream gives each dequant-matmul launch's duration, from which the
+roofline figure is computed (algorithmic bytes = weight blocks + activations
+in + out, per launch).
+
+The CPU baseline times the oracle's C dequant-matmul (f32 dequantisation,
+f64 accumulation, OpenMP over output rows) on a bounded sample of the same
+step -- one Q6_K-mix layer, one Q4_K layer and the lm_head at M=5 -- and
+scales it to a whole verify step (16 layers of each kind + lm_head).
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "abyo-speculate_amd"))
+
+METRIC = "Llama-3-8B Q4_K_M verify-step µs + HBM GB/s at M=5 and 60-node tree"
+PEAK_HBM_GBPS = 8000.0
+SEED = 0x5EED0002
+KV_SEED = 0x4B560002
+
+LLAMA8B = dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+               rope_theta=500000.0, rms_eps=1e-5)
+
+
+def log(msg: str):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-tree", action="store_true", help="skip the 60-node tree leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--prefix", type=int, default=512, help="KV positions before the M=5 verify")
+    ap.add_argument("--tree-prefix", type=int, default=4096, help="KV positions before the tree verify")
+    return ap.parse_args()
+
+
+def make_tree(S, root: int, rng: np.random.Generator):
+    branching = (4, 3, 2, 2, 1, 1)
+    cands = [[int(v) for v in rng.integers(0, LLAMA8B["vocab"], b)] for b in branching]
+    lps = [list(np.sort(np.log(rng.dirichlet(np.ones(b))))[::-1].astype(np.float32)) for b in branching]
+    full = S.tree_cartesian(root, cands)
+    return S.tree_prune(full, lps, 60)
+
+
+def gemm_rows(prof, classes):
+    return [e for e in prof if e[0] in classes]
+
+
+def summarize(prof):
+    out = {}
+    for cls in ("qkv", "wo", "gate_up", "down", "lm_head", "attn"):
+        es = [e for e in prof if e[0] == cls]
+        if not es:
+            continue
+        b = sum(e[1] for e in es)
+        t = sum(e[2] for e in es) * 1e-3
+        out[cls] = {"launches": len(es), "avg_us": round(t / len(es) * 1e6, 2),
+                    "gbps": round(b / t / 1e9, 1)}
+    return out
+
+
+def cpu_baseline():
+    """Oracle CPU dequant-matmul on a bounded sample, scaled to one M=5 verify step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    if not os.path.exists(O.LIB_PATH):
+        import build_oracle
+        build_oracle.build()
+    cfg = O.ModelConfig(arch="llama", mix="q4_k_m", seed=SEED, ctx_len=1024, **LLAMA8B)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    x = np.random.default_rng(1).standard_normal((5, cfg.ffn)).astype(np.float32)
+    L = O.lib()
+
+    def time_matrix(layer, kind):
+        fmt, raw = O.synth_tensor(cfg, layer, kind)
+        N, K = cfg.shape(kind)
+        y = np.empty((5, N), np.float32)
+        xs = np.ascontiguousarray(x[:, :K])
+        t0 = time.perf_counter()
+        L.or_qmatmul(fmt, O._p(raw), N, K, O._p(xs), 5, O._p(y))
+        return time.perf_counter() - t0
+
+    kinds = (O.K_ATTN_Q, O.K_ATTN_K, O.K_ATTN_V, O.K_ATTN_O, O.K_FFN_GATE, O.K_FFN_UP, O.K_FFN_DOWN)
+    t_q6 = sum(time_matrix(0, k) for k in kinds)      # layer 0: Q6_K attn_v / ffn_down
+    log(f"cpu baseline: Q6_K-mix layer {t_q6:.2f} s")
+    t_q4 = sum(time_matrix(4, k) for k in kinds)      # layer 4: all Q4_K
+    log(f"cpu baseline: Q4_K layer {t_q4:.2f} s")
+    t_lm = time_matrix(-1, O.K_OUTPUT)
+    log(f"cpu baseline: lm_head {t_lm:.2f} s")
+    n_q6 = sum(1 for i in range(cfg.n_layers) if O.use_more_bits(i, cfg.n_layers))
+    step_s = n_q6 * t_q6 + (cfg.n_layers - n_q6) * t_q4 + t_lm
+    return {"value": round(step_s * 1e6, 1), "unit": "us/verify (M=5)", "cores": threads, "kind": "port",
+            "sample": "oracle C dequant-matmul (f32 dequant, f64 accumulate, OpenMP over rows) at M=5 on one "
+                      "Q6_K-mix layer, one Q4_K layer and the Q4_K lm_head of the same synthetic weights, scaled to "
+                      f"{n_q6}+{cfg.n_layers - n_q6} layers + lm_head; attention and norms not included"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the verify step of one batch-1 decoder "
+              "runs on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+    import speculate_hip as S
+    if not os.path.exists(S.LIB_PATH):
+        sys.path.insert(0, ROOT)
+        import __graft_entry__
+        __graft_entry__.build()
+    S.load_library()
+
+    ctx = max(args.prefix + 8, args.tree_prefix + 64) + 64
+    cfg = S.Config(arch=S.ARCH_LLAMA, ctx_len=ctx, max_batch=64, **LLAMA8B)
+    log(f"creating decoder (ctx {ctx}) and synthesising Q4_K_M weights")
+    dec = S.HipQuantDecoder(cfg)
+    dec.synthesize(S.MIX_Q4_K_M, SEED, 0.02)
+    rng = np.random.default_rng(SEED)
+
+    # ---------------- M=5 linear verify ----------------
+    hist = [int(v) for v in rng.integers(0, cfg.vocab, args.prefix + 1)]
+    dec.prime_synthetic(hist, KV_SEED)
+    drafts = [int(v) for v in rng.integers(0, cfg.vocab, 4)]
+    n0 = len(hist)
+
+    def step_linear():
+        commits, acc = dec.verify_greedy_linear(drafts)
+        dec.rollback_to(n0)
+        return commits, acc
+
+    log(f"M=5 verify: {args.warmup} warmup + {args.steps} timed steps at KV {args.prefix}")
+    for _ in range(args.warmup):
+        step_linear()
+    dec.synchronize()
+    t0 = time.perf_counter()
+    accepted = 0
+    for _ in range(args.steps):
+        _, acc = step_linear()
+        accepted += acc
+    dec.synchronize()
+    t_lin = (time.perf_counter() - t0) / args.steps
+    log(f"M=5 verify: {t_lin * 1e6:.1f} us/step")
+
+    dec.profile_enable(True)
+    for _ in range(args.steps):
+        step_linear()
+    dec.synchronize()
+    prof = dec.profile_read()
+    dec.profile_enable(False)
+    gem = gemm_rows(prof, ("qkv", "wo", "gate_up", "down", "lm_head"))
+    gb = sum(e[1] for e in gem)
+    gt = sum(e[2] for e in gem) * 1e-3
+    per_launch_bytes = gb / len(gem)
+    avg_launch_s = gt / len(gem)
+    achieved = per_launch_bytes / avg_launch_s / 1e9
+    step_bytes = gb / args.steps + sum(e[1] for e in prof if e[0] == "attn") / args.steps
+    log(f"K1 dequant-matmul: {achieved:.0f} GB/s over {len(gem)} launches")
+
+    result = {
+        "metric": METRIC, "value": round(t_lin * 1e6, 1), "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(t_lin * 1e3, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/q6_k weights, fp16 MFMA, f32 accumulate",
+        "data": "synthetic (random-init N(0,0.02) weights quantised on the GPU, N(0,1) fp16 KV)",
+        "config": {"workload": "Llama-3-8B-shaped Q4_K_M verify step, M=5 (k=4 drafts), KV 512 fp16, greedy "
+                               "acceptance on the device",
+                   "layers": 32, "hidden": 4096, "heads": "32q/8kv", "ffn": 14336, "vocab": 128256,
+                   "M": 5, "kv_positions": args.prefix},
+        "verify_steps_per_s": round(1.0 / t_lin, 1),
+        "tokens_per_s": round((accepted / args.steps + 1) / t_lin, 1),
+        "step_hbm_gbps": round(step_bytes / t_lin / 1e9, 1),
+        "step_algorithmic_bytes": int(step_bytes),
+        "kernels": summarize(prof),
+        "roofline": {"bound": "hbm", "kernel": "k_qgemm (fused dequant-matmul, all 129 launches of a step)",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": int(per_launch_bytes), "avg_launch_us": round(avg_launch_s * 1e6, 2)},
+    }
+
+    # ---------------- 60-node tree verify ----------------
+    if not args.no_tree:
+        hist = [int(v) for v in rng.integers(0, cfg.vocab, args.tree_prefix + 1)]
+        dec.prime_synthetic(hist, KV_SEED + 1)
+        toks, pars = make_tree(S, hist[-1], rng)
+        n1 = len(hist)
+        tree = (toks, pars)
+
+        def step_tree():
+            path, bonus, bnode = dec.verify_greedy_tree(tree)
+            dec.commit_tree_path(tree, path)
+            dec.rollback_to(n1)
+            return path
+
+        log(f"tree verify: {len(toks)} nodes at KV {args.tree_prefix}")
+        for _ in range(args.warmup):
+            step_tree()
+        dec.synchronize()
+        t0 = time.perf_counter()
+        plen = 0
+        for _ in range(args.steps):
+            plen += len(step_tree())
+        dec.synchronize()
+        t_tree = (time.perf_counter() - t0) / args.steps
+        dec.profile_enable(True)
+        for _ in range(args.steps):
+            step_tree()
+        dec.synchronize()
+        tprof = dec.profile_read()
+        dec.profile_enable(False)
+        tg = gemm_rows(tprof, ("qkv", "wo", "gate_up", "down", "lm_head"))
+        tb = sum(e[1] for e in tg)
+        tt = sum(e[2] for e in tg) * 1e-3
+        log(f"tree verify: {t_tree * 1e6:.1f} us/step, K1 {tb / tt / 1e9:.0f} GB/s")
+        result["tree60"] = {"us": round(t_tree * 1e6, 1), "nodes": int(len(toks)), "kv_positions": args.tree_prefix,
+                            "tokens_per_s": round((plen / args.steps) / t_tree, 1),
+                            "k1_gbps": round(tb / tt / 1e9, 1),
+                            "k1_frac": round(tb / tt / 1e9 / PEAK_HBM_GBPS, 4),
+                            "kernels": summarize(tprof)}
+    dec.close()
+
+    if not args.no_cpu:
+        log("CPU baseline (bounded sample)")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -189,11 +189,13 @@ sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n);
 /* Sets history = ids and fills KV rows [0, n) with seeded N(0,1)-like fp16
  * values; the next-token logits cache is invalid afterwards. */
 sd_status sd_prime_synthetic(sd_model *m, const uint32_t *ids, size_t n, uint64_t kv_seed);
-/* Enables (1) / disables (0) HIP-event timing of every quantised matmul launch. */
+/* Enables (1) / disables (0) HIP-event timing, on the handle's stream, of every
+ * quantised matmul launch and of every layer's attention. */
 sd_status sd_profile_enable(sd_model *m, int32_t on);
 /* Reads and clears the timed launches: class ids (0 qkv, 1 wo, 2 gate_up,
- * 3 down, 4 lm_head), algorithmic weight bytes and milliseconds.  Returns the
- * number of entries written. */
+ * 3 down, 4 lm_head, 5 attn), algorithmic bytes (weight blocks for the
+ * matmuls, K and V rows for attention) and milliseconds.  Returns the number of
+ * entries written. */
 size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap);
 sd_status sd_synchronize(sd_model *m);
 /* Copies n fp16 cache rows [pos0, pos0+n) of one (layer, K=0/V=1, kv head):
@@ -202,6 +204,24 @@ sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t hea
                           uint16_t *out);
 /* Number of positions currently held in the KV cache. */
 size_t sd_cache_len(const sd_model *m);
+
+/* ---- draft-tree builders (host only; no GPU needed) ---------------------------- */
+/* build_cartesian_tree (methods/medusa.rs:172-193): step d has branching[d]
+ * candidate tokens, stored back to back in cand[]; layer d+1 hangs every
+ * candidate of step d under every node of layer d, in BFS order.  *n receives
+ * the node count 1 + b0 + b0*b1 + ...; with tokens or parents NULL only the
+ * size is returned.  SD_ERR_ARG if the tree exceeds cap. */
+sd_status sd_tree_cartesian(uint32_t root, const uint32_t *cand, const uint32_t *branching, size_t depth,
+                            uint32_t *tokens, uint32_t *parents, size_t cap, size_t *n);
+/* prune_cartesian_tree (methods/eagle.rs:763-845): keeps the max_total - 1
+ * non-root nodes with the highest summed per-step log-prob (log_probs holds
+ * branching[d] values for step d, back to back; equal scores keep BFS order)
+ * plus their ancestors, re-emitted stably by depth.  A tree of at most
+ * max_total nodes is returned unchanged.  out_* need room for n entries: the
+ * ancestor closure can exceed max_total when log-probs are not all <= 0. */
+sd_status sd_tree_prune(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *log_probs,
+                        const uint32_t *branching, size_t depth, size_t max_total, uint32_t *out_tokens,
+                        uint32_t *out_parents, size_t *n_out);
 
 #ifdef __cplusplus
 }
