@@ -14,13 +14,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libspeculate_hip.so")
+INCLUDE = os.environ.get("SD_INCLUDE_DIR", os.path.join(os.path.dirname(HERE), "include"))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
           # no packed-FP32 instructions anywhere (hipcc's host pass warns that it
           # does not know the feature; that warning is expected)
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-Wno-unused-result"]
+          "-Wno-unused-result", "-I" + INCLUDE]
 
 
 def _compile(src: str) -> str:

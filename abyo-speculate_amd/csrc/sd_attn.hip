@@ -236,23 +236,35 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p) {
 }
 
 // ---- combine splits -> fp16 fragment-layout input of wo ----------------------
-// grid (n_heads, M), block HD threads
+// grid (n_heads, M), block HD threads.  Every split's (m, l) and output are
+// loaded before use (up to 64 splits in registers), so the combine costs one
+// memory round trip.
+constexpr int MAX_SPLITS = 64;
 __global__ void k_attn_combine(AttnParams p, int nsplit) {
     const int head = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const int HD = p.hd;
-    float mx = -INFINITY;
-    for (int s = 0; s < nsplit; s++) {
-        const float ms = p.part_ml[2 * (((int64_t)s * p.n_heads + head) * p.M + m)];
-        mx = fmaxf(mx, ms);
+    float ms[MAX_SPLITS], ls[MAX_SPLITS], os[MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; s++) {
+        if (s < nsplit) {
+            const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
+            ms[s] = p.part_ml[2 * pi];
+            ls[s] = p.part_ml[2 * pi + 1];
+            os[s] = p.part_o[pi * HD + d];
+        }
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; s++)
+        if (s < nsplit) mx = fmaxf(mx, ms[s]);
     float L = 0.f, acc = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
-        const float ms = p.part_ml[2 * pi];
-        if (ms == -INFINITY) continue;
-        const float f = exp2f(ms - mx);
-        L += p.part_ml[2 * pi + 1] * f;
-        acc += p.part_o[pi * HD + d] * f;
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; s++) {
+        if (s < nsplit && ms[s] != -INFINITY) {
+            const float f = exp2f(ms[s] - mx);
+            L += ls[s] * f;
+            acc += os[s] * f;
+        }
     }
     const float y = acc / L;
     const int64_t k = (int64_t)head * HD + d;
@@ -267,6 +279,7 @@ void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
 int attn_chunks_per_split(int P, int n_kv) {
     const int nch_p = (P + 1 + KCH - 1) / KCH;
     int target = 256 / (n_kv > 0 ? n_kv : 1);
+    if (target > MAX_SPLITS - 3) target = MAX_SPLITS - 3;  // up to 3 more splits for <= 128 new rows
     if (target < 1) target = 1;
     if (target > nch_p) target = nch_p;
     return (nch_p + target - 1) / target;
@@ -285,6 +298,7 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.hd == 128) hipLaunchKernelGGL(k_attn_split<128>, grid, dim3(256), 0, st, p);
     else if (p.hd == 64) hipLaunchKernelGGL(k_attn_split<64>, grid, dim3(256), 0, st, p);
     else throw BackendError("attention: head_dim must be 64 or 128");
+    if (nsplit > MAX_SPLITS) throw BackendError("attention: too many splits");
     hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p, nsplit);
 }
 

@@ -3,9 +3,11 @@
 #include <memory>
 #include <string>
 
-#include "../../include/speculate_hip.h"
+#include "speculate_hip.h"
 #include "sd_model.hpp"
 #include "sd_common.hpp"
+#include "sd_qcodes.hpp"
+#include "sd_tiles.hpp"
 
 struct sd_model {
     std::unique_ptr<sd::Model> model;
@@ -134,6 +136,15 @@ sd_status sd_model_qmatmul(sd_model *m, int32_t layer, int32_t kind, const float
         need(m);
         if (!x || !y) throw sd::ArgError("null argument");
         m->model->qmatmul(layer, kind, x, (int)rows, y);
+    });
+}
+
+sd_status sd_bench_qmatmul(sd_model *m, int32_t layer, int32_t kind, size_t rows, int32_t iters, double *us,
+                           double *bytes) {
+    return guard([&] {
+        need_weights(m);
+        if (!us) throw sd::ArgError("null argument");
+        *us = m->model->bench_qmatmul(layer, kind, (int)rows, iters, bytes);
     });
 }
 
@@ -367,6 +378,84 @@ sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t hea
 }
 
 size_t sd_cache_len(const sd_model *m) { return m && m->dec ? (size_t)m->dec->cache_len : 0; }
+
+static int64_t quant_rows_check(int32_t fmt, size_t rows, size_t K) {
+    if (fmt != SD_Q4_K && fmt != SD_Q5_K && fmt != SD_Q6_K && fmt != SD_Q8_0)
+        throw sd::UnsupportedError("format must be Q4_K, Q5_K, Q6_K or Q8_0");
+    if (rows == 0 || rows % 16 || K == 0 || K % 256) throw sd::ArgError("rows must be a multiple of 16 and K of 256");
+    return (int64_t)(K / 256);
+}
+
+sd_status sd_repack_gguf(int32_t fmt, const void *gguf, size_t rows, size_t K, void *out) {
+    return guard([&] {
+        if (!gguf || !out) throw sd::ArgError("null argument");
+        const int64_t nsb = quant_rows_check(fmt, rows, K);
+        const int sbb = sd::fmt_sb_bytes(fmt), tbb = sd::tile_block_bytes(fmt);
+        const uint8_t *src = (const uint8_t *)gguf;
+        uint8_t *dst = (uint8_t *)out;
+        for (size_t r = 0; r < rows; r++)
+            for (int64_t sb = 0; sb < nsb; sb++)
+                sd::pack_sb(fmt, src + ((int64_t)r * nsb + sb) * sbb, dst + ((int64_t)(r >> 4) * nsb + sb) * tbb,
+                            (int)(r & 15));
+    });
+}
+
+sd_status sd_unpack_tiles(int32_t fmt, const void *tiles, size_t rows, size_t K, void *gguf_out) {
+    return guard([&] {
+        if (!tiles || !gguf_out) throw sd::ArgError("null argument");
+        const int64_t nsb = quant_rows_check(fmt, rows, K);
+        const int sbb = sd::fmt_sb_bytes(fmt), tbb = sd::tile_block_bytes(fmt);
+        const uint8_t *src = (const uint8_t *)tiles;
+        uint8_t *dst = (uint8_t *)gguf_out;
+        for (size_t r = 0; r < rows; r++)
+            for (int64_t sb = 0; sb < nsb; sb++)
+                sd::unpack_sb(fmt, src + ((int64_t)(r >> 4) * nsb + sb) * tbb, (int)(r & 15),
+                              dst + ((int64_t)r * nsb + sb) * sbb);
+    });
+}
+
+sd_status sd_lane_codes(int32_t fmt, const void *tile_block, int32_t lane, int32_t chunk, uint32_t *out) {
+    return guard([&] {
+        if (!tile_block || !out) throw sd::ArgError("null argument");
+        if (lane < 0 || lane > 63 || chunk < 0 || chunk > 7) throw sd::ArgError("lane in [0, 64), chunk in [0, 8)");
+        const uint8_t *tb = (const uint8_t *)tile_block;
+        auto v4 = [&](int off) {
+            sd::uintx4 v;
+            std::memcpy(&v, tb + off, 16);
+            return v;
+        };
+        const int g = lane >> 4;
+        if (fmt == SD_Q4_K) {
+            sd::LaneQ4K d;
+            d.hdr = v4(d.off_hdr(lane));
+            d.q0 = v4(d.off_q0(lane));
+            d.q1 = v4(d.off_q1(lane));
+            d.codes(g, chunk, out);
+        } else if (fmt == SD_Q5_K) {
+            sd::LaneQ5K d;
+            d.hdr = v4(d.off_hdr(lane));
+            std::memcpy(&d.qh, tb + d.off_qh(lane), 8);
+            d.q0 = v4(d.off_q0(lane));
+            d.q1 = v4(d.off_q1(lane));
+            d.codes(g, chunk, out);
+        } else if (fmt == SD_Q6_K) {
+            sd::LaneQ6K d;
+            d.n0 = v4(d.off_n0(lane));
+            d.n1 = v4(d.off_n1(lane));
+            d.hb = v4(d.off_hb(lane));
+            d.codes(g, chunk, out);
+        } else if (fmt == SD_Q8_0) {
+            sd::LaneQ80 d;
+            d.a0 = v4(d.off_part(lane, 0));
+            d.a1 = v4(d.off_part(lane, 1));
+            d.b0 = v4(d.off_part(lane, 2));
+            d.b1 = v4(d.off_part(lane, 3));
+            d.codes(g, chunk, out);
+        } else {
+            throw sd::UnsupportedError("format must be Q4_K, Q5_K, Q6_K or Q8_0");
+        }
+    });
+}
 
 sd_status sd_tree_cartesian(uint32_t root, const uint32_t *cand, const uint32_t *branching, size_t depth,
                             uint32_t *tokens, uint32_t *parents, size_t cap, size_t *n) {

@@ -1,11 +1,16 @@
 // Shared definitions for the MI355X (gfx950) target-verify library.
 //
-// Weights stay in their GGUF block layouts (row-major [N][K/elems] blocks, as
+// Weights arrive in their GGUF block layouts (row-major [N][K/elems] blocks, as
 // candle's QMatMul holds them: crates/speculate/src/model/quantized_llama_local.rs:258-281):
 //   Q4_K  144 B / 256: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
 //   Q5_K  176 B / 256: f16 d | f16 dmin | u8 scales[12] | u8 qh[32] | u8 qs[128]
 //   Q6_K  210 B / 256: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
 //   Q8_0   34 B /  32: f16 d | i8 qs[32]
+// and are kept in HBM in a tile-interleaved layout (sd_layout.hip): a matrix of
+// R rows (R % 16 == 0) is R/16 x K/256 tile blocks, tile-major, each holding
+// the 16 rows' blocks of one 256-column superblock rearranged so that every
+// load of the MFMA lane mapping (lane = r + 16 g) reads contiguous bytes.  The
+// byte size is the GGUF size; only the order changes.
 //
 // Activations feeding a quantised matmul are fp16 in a "fragment" order: within
 // each 256-element superblock, slot p = c*32 + g*8 + s (chunk c = 0..7, lane
@@ -25,18 +30,19 @@ __host__ __device__ inline int fmt_block_bytes(int f) {
     return f == Q4_K ? 144 : f == Q5_K ? 176 : f == Q6_K ? 210 : f == Q8_0 ? 34 : 0;
 }
 __host__ __device__ inline int fmt_block_elems(int f) { return f == Q8_0 ? 32 : 256; }
-// bytes of one 256-element superblock (8 Q8_0 blocks for Q8_0)
+// bytes of one 256-element superblock of one row (8 Q8_0 blocks for Q8_0)
 __host__ __device__ inline int fmt_sb_bytes(int f) { return f == Q8_0 ? 272 : fmt_block_bytes(f); }
-// row stride of the device layout (GGUF row bytes rounded up to 16)
-__host__ __device__ inline int64_t dev_row_stride(int f, int64_t K) {
-    if (f == F32) return 4 * K;
-    const int64_t raw = K / fmt_block_elems(f) * fmt_block_bytes(f);
-    return (raw + 15) / 16 * 16;
+// bytes of one tile block (16 rows x one superblock) of the device layout
+__host__ __device__ inline int tile_block_bytes(int f) { return 16 * fmt_sb_bytes(f); }
+// bytes of a whole [rows][K] tensor (F32: plain row-major)
+__host__ __device__ inline int64_t dev_tensor_bytes(int f, int64_t rows, int64_t K) {
+    return f == F32 ? 4 * rows * K : rows * (K / 256) * fmt_sb_bytes(f);
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int uintx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int uintx2 __attribute__((ext_vector_type(2)));
 
 // element index inside a superblock for fragment slot p (see header comment)
 __host__ __device__ inline int frag_elem(int p) {

@@ -1,9 +1,5 @@
-// Embedding gather, RMSNorm, device-layout dequantisation, KV compaction.
+// RMSNorm, argmax reductions, KV compaction.
 //
-//  * embedding: Embedding::forward over the f32-dequantised token table
-//    (crates/speculate/src/model/quantized_llama_local.rs:242-243, 380, 419);
-//    rows are dequantised on the fly from the quantised table with the exact
-//    f32 expressions, so no 2 GB f32 copy of the table is kept.
 //  * rms_norm: RmsNorm::forward (:385, 389, 398): x / sqrt(mean(x^2) + eps) * w.
 //    Writes the fp16 fragment-layout operand of the next matmul, and optionally
 //    the f32 row (the final hidden state returned by tree_logits_keep_kv).
@@ -17,78 +13,54 @@ namespace sd {
 
 #pragma clang fp contract(off)
 
-__device__ inline float ld_h(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
-
-// element e of a device-layout row (exact f32, two roundings per expression)
-__device__ float deq_elem(int fmt, const uint8_t *row, int nsb, int e) {
-    if (fmt == F32) return ((const float *)row)[e];
-    if (fmt == Q8_0) {
-        const int nb = nsb * 8, b = e >> 5, l = e & 31;
-        const float d = ld_h(row + 32 * nb + 2 * b);
-        return d * (float)(int8_t)row[32 * b + l];
-    }
-    const int sb = e >> 8, r = e & 255;
-    if (fmt == Q4_K || fmt == Q5_K) {
-        const uint8_t *b = row + (int64_t)sb * (fmt == Q4_K ? 144 : 176);
-        const float d = ld_h(b), mn = ld_h(b + 2);
-        const uint8_t *sc = b + 4;
-        const int part = r >> 5, j = r >> 6, hi = (r >> 5) & 1, l = r & 31;
-        int s, m;
-        if (part < 4) {
-            s = sc[part] & 63;
-            m = sc[part + 4] & 63;
-        } else {
-            s = (sc[part + 4] & 0xF) | ((sc[part - 4] >> 6) << 4);
-            m = (sc[part + 4] >> 4) | ((sc[part] >> 6) << 4);
-        }
-        const float d1 = d * (float)s, m1 = mn * (float)m;
-        int q;
-        if (fmt == Q4_K) {
-            const uint8_t qb = b[16 + 32 * j + l];
-            q = hi ? (qb >> 4) : (qb & 0xF);
-        } else {
-            const uint8_t qb = b[48 + 32 * j + l], qh = b[16 + l];
-            q = (hi ? (qb >> 4) : (qb & 0xF)) + (((qh >> (2 * j + hi)) & 1) ? 16 : 0);
-        }
-        return d1 * (float)q - m1;
-    }
-    // Q6_K planar
-    const float d = ld_h(row + (int64_t)nsb * 208 + 2 * sb);
-    const int h = r >> 7, qd = (r >> 5) & 3, l = r & 31;
-    const uint8_t qlb = row[(int64_t)sb * 128 + 64 * h + 32 * (qd & 1) + l];
-    const uint8_t qhb = row[(int64_t)nsb * 128 + (int64_t)sb * 64 + 32 * h + l];
-    const int8_t sc = (int8_t)row[(int64_t)nsb * 192 + (int64_t)sb * 16 + 8 * h + l / 16 + 2 * qd];
-    const int nib = qd < 2 ? (qlb & 0xF) : (qlb >> 4);
-    const int q = (nib | (((qhb >> (2 * qd)) & 3) << 4)) - 32;
-    return d * (float)sc * (float)q;
-}
-
-__global__ void k_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, int64_t stride, float *y) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= rows * K) return;
-    const int64_t r = i / K;
-    const int e = (int)(i % K);
-    y[i] = deq_elem(fmt, w + r * stride, K / 256, e);
-}
-
-// h[m][k] = table[ids[m]][k]
-__global__ void k_embed(int fmt, const uint8_t *table, int64_t stride, int K, const int *ids, float *h) {
-    const int m = blockIdx.y;
-    const int k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= K) return;
-    h[(int64_t)m * K + k] = deq_elem(fmt, table + (int64_t)ids[m] * stride, K / 256, k);
-}
-
-// one workgroup (256 threads) per row
+// One workgroup (256 threads) per row.  Each thread keeps its K/256 values in
+// registers (vector loads, all issued before the first use), so the row is
+// read from memory once and there is one memory round trip, not K/256 of them.
+template <int NV>  // float4 vectors per thread: K = 1024 * NV
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *w, int K, float eps, uint16_t *out16,
                                                  int ld16, float *out32) {
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float4 *row = (const float4 *)(x + (int64_t)m * K);
+    const float4 *wv = (const float4 *)w;
+    float4 v[NV], wr[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = row[t + 256 * i];
+#pragma unroll
+    for (int i = 0; i < NV; i++) wr[i] = wv[t + 256 * i];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    ss += __shfl_xor(ss, 8);
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    __shared__ float red[4];
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float mrms = sqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * (t + 256 * i);
+        const float y[4] = {v[i].x / mrms * wr[i].x, v[i].y / mrms * wr[i].y, v[i].z / mrms * wr[i].z,
+                            v[i].w / mrms * wr[i].w};
+        if (out16) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) out16[(int64_t)m * ld16 + frag_index(k + j)] = f2h(y[j]);
+        }
+        if (out32) *(float4 *)(out32 + (int64_t)m * K + k) = make_float4(y[0], y[1], y[2], y[3]);
+    }
+}
+
+// generic K (multiple of 4): strided loop
+__global__ __launch_bounds__(256) void k_rmsnorm_any(const float *x, const float *w, int K, float eps, uint16_t *out16,
+                                                     int ld16, float *out32) {
     const int m = blockIdx.x;
     const float *row = x + (int64_t)m * K;
     float ss = 0.f;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float v = row[k];
-        ss += v * v;
-    }
+    for (int k = threadIdx.x; k < K; k += 256) ss += row[k] * row[k];
     __shared__ float red[256];
     red[threadIdx.x] = ss;
     __syncthreads();
@@ -113,37 +85,44 @@ __global__ void k_to_frag16(const float *x, int K, uint16_t *out16, int ld16) {
 }
 
 // ---- argmax over per-workgroup partials (first max wins, NaN/-inf skipped) ----
-// grid M, block 256
+// grid M, block 256.  Each thread loads its (up to 32) partials before
+// comparing, so the reduction costs one memory round trip.
+__device__ __forceinline__ void amax_take(float &bv, int &bi, float v, int i) {
+    if (i != 0x7fffffff && (v > bv || (v == bv && i < bi) || bi == 0x7fffffff)) {
+        bv = v;
+        bi = i;
+    }
+}
 __global__ __launch_bounds__(256) void k_argmax_reduce(const float *pv, const int *pi, int nwg, int *out) {
     const int m = blockIdx.x;
+    constexpr int PER = 32;
+    float v[PER];
+    int ix[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int w = threadIdx.x + 256 * j;
+        const bool ok = w < nwg;
+        v[j] = ok ? pv[(int64_t)m * nwg + w] : -INFINITY;
+        ix[j] = ok ? pi[(int64_t)m * nwg + w] : 0x7fffffff;
+    }
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int w = threadIdx.x; w < nwg; w += 256) {
-        const float v = pv[(int64_t)m * nwg + w];
-        const int i = pi[(int64_t)m * nwg + w];
-        if (i != 0x7fffffff && (v > bv || (v == bv && i < bi) || bi == 0x7fffffff)) {
-            bv = v;
-            bi = i;
-        }
+#pragma unroll
+    for (int j = 0; j < PER; j++) amax_take(bv, bi, v[j], ix[j]);
+    for (int w = threadIdx.x + 256 * PER; w < nwg; w += 256) amax_take(bv, bi, pv[(int64_t)m * nwg + w], pi[(int64_t)m * nwg + w]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) amax_take(bv, bi, __shfl_xor(bv, off), __shfl_xor(bi, off));
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
     }
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) {
-            const float v = sv[threadIdx.x + o];
-            const int i = si[threadIdx.x + o];
-            if (i != 0x7fffffff &&
-                (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && i < si[threadIdx.x]) || si[threadIdx.x] == 0x7fffffff)) {
-                sv[threadIdx.x] = v;
-                si[threadIdx.x] = i;
-            }
-        }
-        __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++) amax_take(bv, bi, sv[k], si[k]);
+        out[m] = bi == 0x7fffffff ? 0 : bi;
     }
-    if (threadIdx.x == 0) out[m] = si[0] == 0x7fffffff ? 0 : si[0];
 }
 
 // ---- argmax directly over f32 rows (rows not produced by the fused lm_head) ----
@@ -199,18 +178,18 @@ __global__ __launch_bounds__(256) void k_keep_kv_tail(uint16_t *kv, int64_t stre
 }
 
 // ---- launchers ----
-void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y, hipStream_t st) {
-    const int64_t n = rows * K;
-    hipLaunchKernelGGL(k_dequant_dev, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, fmt, w, rows, K,
-                       dev_row_stride(fmt, K), y);
-}
-void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3((K + 255) / 256, M), dim3(256), 0, st, fmt, table, dev_row_stride(fmt, K), K,
-                       ids, h);
-}
 void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
                     hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32);
+    switch (K) {
+    case 512: hipLaunchKernelGGL(k_rmsnorm_any, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 1024: hipLaunchKernelGGL(k_rmsnorm<1>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 2048: hipLaunchKernelGGL(k_rmsnorm<2>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 3072: hipLaunchKernelGGL(k_rmsnorm<3>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 4096: hipLaunchKernelGGL(k_rmsnorm<4>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 5120: hipLaunchKernelGGL(k_rmsnorm<5>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 8192: hipLaunchKernelGGL(k_rmsnorm<8>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    default: hipLaunchKernelGGL(k_rmsnorm_any, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    }
 }
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st) {
     hipLaunchKernelGGL(k_to_frag16, dim3((K + 255) / 256, M), dim3(256), 0, st, x, K, out16, ld16);

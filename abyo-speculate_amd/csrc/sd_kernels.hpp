@@ -20,7 +20,7 @@ void launch_fill_kv(uint16_t *kv, int L, int n_kv, int64_t cap, int hd, int P, u
 // GGUF block bytes -> f32, exact (input must be in GGUF layout)
 void launch_dequant(int fmt, const uint8_t *w, int64_t n_elems, float *y, hipStream_t st);
 
-// ---- sd_layout.hip: GGUF rows <-> device rows (Q6_K / Q8_0 regrouped into planes) ----
+// ---- sd_layout.hip: GGUF rows <-> tile-interleaved device layout ----
 void launch_gguf_to_dev(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st);
 void launch_dev_to_gguf(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st);
 
@@ -28,7 +28,7 @@ void launch_dev_to_gguf(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows,
 enum GemmMode : int { GM_STORE = 0, GM_RESID = 1, GM_SWIGLU = 2, GM_LOGITS = 3 };
 
 struct GemmSeg {
-    const uint8_t *w;  // device layout rows, stride dev_row_stride(fmt, K)
+    const uint8_t *w;  // tile-interleaved device layout (sd_layout.hip)
     int fmt;
     int rows;          // multiple of 16
     int tile0;         // first 16-row tile of this segment in the launch

@@ -4,7 +4,10 @@
 
 namespace sd {
 
-// exact f32 dequantisation of device-layout rows
+// sd_layout.hip: exact f32 dequantisation of device-layout rows, and the
+// embedding gather (Embedding::forward over the dequantised token table,
+// crates/speculate/src/model/quantized_llama_local.rs:242-243, 380, 419; rows
+// are dequantised on the fly, so no f32 copy of the table is kept)
 void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y, hipStream_t st);
 void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st);
 void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,

@@ -1,62 +1,142 @@
-// GGUF rows <-> device rows.
+// Device weight layout: GGUF rows <-> tile-interleaved tile blocks, and the
+// exact f32 dequantisation of device-layout tensors.
 //
-// Q4_K (144 B) and Q5_K (176 B) blocks are 16-byte multiples and stay as GGUF
-// stores them.  Q6_K (210 B) and Q8_0 (34 B) blocks are not 16-byte aligned,
-// so each row's bytes are regrouped into planes (a permutation of the same
-// bytes, so HBM traffic is unchanged):
-//   Q6_K row: ql[128*nsb] | qh[64*nsb] | scales[16*nsb] | d[2*nsb]   (stride padded to 16 B)
-//   Q8_0 row: qs[32*nb]   | d[2*nb]
+// A tile block holds the superblock sb of rows 16t .. 16t+15.  Inside it, the
+// bytes a lane (r, g) of the matmul kernel needs (r = row within the tile, g =
+// lane group, lane = r + 16 g) are packed so that each of its loads reads a
+// contiguous range across the wave:
+//
+//   Q4_K (2304 B): hdr[r][16]                     (d, dmin, scales: 256 B)
+//                  qs  part p = 0,1: [lane][16]   (qs bytes 32g + 16p .. +16)
+//   Q5_K (2816 B): hdr[r][16] | qhp[lane][8] | qs part 0,1 as Q4_K
+//                  qhp holds the lane's 64 fifth bits, placed where the matmul
+//                  ORs them into its fp16 codes (layout_q5_bit below)
+//   Q6_K (3360 B): nib part 0,1: [lane][16]       nib byte l = low 4 bits of the
+//                  elements (s'=0, l) | (s'=1, l) << 4, s' = element half
+//                  hbp[lane][16]                  2-bit high parts (layout_q6_bit)
+//                  sc[r][16] | d[r][2]
+//   Q8_0 (4352 B): qs part p = 0..3: [lane][16]   (blocks 2g, 2g+1: 64 bytes)
+//                  d[r][8 x f16]
+//
+// Lane (r, g) covers elements 64g .. 64g+63 of the superblock: for the K-quants
+// low/high nibble of qs group g (sub-blocks 2g and 2g+1); for Q6_K the elements
+// 128h + 32(2 odd + s') + l with h = g >> 1, odd = g & 1; for Q8_0 the blocks
+// 2g and 2g+1.  Chunk c of a lane = bytes 4c .. 4c+3 of its 32-byte group, i.e.
+// elements l = 4c .. 4c+3 of both halves.
 #include "sd_common.hpp"
 #include "sd_kernels.hpp"
+#include "sd_kernels_elem.hpp"
+#include "sd_tiles.hpp"
 
 namespace sd {
 
-// one thread per block; dir 0: gguf -> dev, 1: dev -> gguf
-__global__ void k_relayout(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb, int64_t stride_dev,
-                           int dir) {
+#pragma clang fp contract(off)
+
+// one thread per (row, superblock); dir 0: GGUF -> device, 1: device -> GGUF
+__global__ void k_relayout(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nsb, int dir) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= rows * nb) return;
-    const int64_t r = i / nb, b = i % nb;
-    const int bb = fmt_block_bytes(fmt);
-    const int64_t g_off = r * nb * bb + b * bb;  // gguf row stride is unpadded
-    const int64_t d_row = r * stride_dev;
-    if (fmt == Q6_K) {
-        // gguf block: ql[0..128) qh[128..192) sc[192..208) d[208..210)
-        const int64_t off_ql = d_row + 128 * b, off_qh = d_row + 128 * nb + 64 * b,
-                      off_sc = d_row + 192 * nb + 16 * b, off_d = d_row + 208 * nb + 2 * b;
-        for (int j = 0; j < 210; j++) {
-            const int64_t dev = j < 128 ? off_ql + j : j < 192 ? off_qh + (j - 128) : j < 208 ? off_sc + (j - 192)
-                                                                                            : off_d + (j - 208);
-            if (dir == 0) dst[dev] = src[g_off + j];
-            else dst[g_off + j] = src[dev];
-        }
-    } else if (fmt == Q8_0) {
-        const int64_t off_q = d_row + 32 * b, off_d = d_row + 32 * nb + 2 * b;
-        for (int j = 0; j < 34; j++) {
-            const int64_t dev = j < 2 ? off_d + j : off_q + (j - 2);
-            if (dir == 0) dst[dev] = src[g_off + j];
-            else dst[g_off + j] = src[dev];
-        }
+    if (i >= rows * nsb) return;
+    const int64_t row = i / nsb, sb = i % nsb;
+    const int sbb = fmt_sb_bytes(fmt), tbb = tile_block_bytes(fmt);
+    const int64_t g_off = (row * nsb + sb) * sbb;               // GGUF row-major
+    const int64_t t_off = ((row >> 4) * nsb + sb) * (int64_t)tbb;  // tile block
+    if (dir == 0) pack_sb(fmt, src + g_off, dst + t_off, (int)(row & 15));
+    else unpack_sb(fmt, src + t_off, (int)(row & 15), dst + g_off);
+}
+
+// ---- exact f32 dequantisation of one GGUF superblock (no FMA contraction) ------
+__device__ inline float ldh(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
+
+__device__ inline void gsm_k4(int j, const uint8_t *q, int &d, int &m) {
+    if (j < 4) {
+        d = q[j] & 63;
+        m = q[j + 4] & 63;
     } else {
-        for (int j = 0; j < bb; j++) {
-            if (dir == 0) dst[d_row + b * bb + j] = src[g_off + j];
-            else dst[g_off + j] = src[d_row + b * bb + j];
-        }
+        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
     }
 }
 
-static void relayout(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, int dir, hipStream_t st) {
-    const int64_t nb = K / fmt_block_elems(fmt);
-    const int64_t n = rows * nb;
-    hipLaunchKernelGGL(k_relayout, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, fmt, src, dst, rows, nb,
-                       dev_row_stride(fmt, K), dir);
+// element e (0..255) of a GGUF superblock
+__device__ float deq_gguf(int fmt, const uint8_t *b, int e) {
+    if (fmt == Q8_0) {
+        const uint8_t *blk = b + 34 * (e >> 5);
+        return ldh(blk) * (float)(int8_t)blk[2 + (e & 31)];
+    }
+    if (fmt == Q4_K || fmt == Q5_K) {
+        const int part = e >> 5, j = e >> 6, hi = part & 1, l = e & 31;
+        int s, m;
+        gsm_k4(part, b + 4, s, m);
+        const float d1 = ldh(b) * (float)s, m1 = ldh(b + 2) * (float)m;
+        int q;
+        if (fmt == Q4_K) {
+            const uint8_t qb = b[16 + 32 * j + l];
+            q = hi ? (qb >> 4) : (qb & 0xF);
+        } else {
+            const uint8_t qb = b[48 + 32 * j + l];
+            q = (hi ? (qb >> 4) : (qb & 0xF)) + (((b[16 + l] >> (2 * j + hi)) & 1) ? 16 : 0);
+        }
+        return d1 * (float)q - m1;
+    }
+    // Q6_K: element 128h + 32qd + l
+    const int h = e >> 7, qd = (e >> 5) & 3, l = e & 31;
+    const uint8_t qlb = b[64 * h + 32 * (qd & 1) + l], qhb = b[128 + 32 * h + l];
+    const int nib = qd < 2 ? (qlb & 0xF) : (qlb >> 4);
+    const int q = (nib | (((qhb >> (2 * qd)) & 3) << 4)) - 32;
+    return ldh(b + 208) * (float)(int8_t)b[192 + 8 * h + l / 16 + 2 * qd] * (float)q;
 }
 
+// y[row][k] of a device-layout tensor: one thread per (row, superblock)
+__global__ void k_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int64_t nsb, float *y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nsb) return;
+    const int64_t row = i / nsb, sb = i % nsb;
+    if (fmt == F32) {
+        for (int e = 0; e < 256; e++) y[row * nsb * 256 + sb * 256 + e] = ((const float *)w)[row * nsb * 256 + sb * 256 + e];
+        return;
+    }
+    uint8_t gg[272];
+    unpack_sb(fmt, w + ((row >> 4) * nsb + sb) * (int64_t)tile_block_bytes(fmt), (int)(row & 15), gg);
+    float *o = y + (row * nsb + sb) * 256;
+    for (int e = 0; e < 256; e++) o[e] = deq_gguf(fmt, gg, e);
+}
+
+// h[m][k] = table[ids[m]][k] (Embedding over the dequantised token table):
+// one thread per (token, superblock)
+__global__ void k_embed(int fmt, const uint8_t *table, int64_t nsb, const int *ids, int M, float *h) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * nsb) return;
+    const int m = (int)(i / nsb);
+    const int64_t sb = i % nsb, row = ids[m];
+    float *o = h + (int64_t)m * nsb * 256 + sb * 256;
+    if (fmt == F32) {
+        for (int e = 0; e < 256; e++) o[e] = ((const float *)table)[row * nsb * 256 + sb * 256 + e];
+        return;
+    }
+    uint8_t gg[272];
+    unpack_sb(fmt, table + ((row >> 4) * nsb + sb) * (int64_t)tile_block_bytes(fmt), (int)(row & 15), gg);
+    for (int e = 0; e < 256; e++) o[e] = deq_gguf(fmt, gg, e);
+}
+
+// ---- launchers ----
+static void relayout(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, int dir, hipStream_t st) {
+    if (rows % 16 || K % 256) throw BackendError("relayout: rows must be a multiple of 16 and K of 256");
+    const int64_t nsb = K / 256, n = rows * nsb;
+    hipLaunchKernelGGL(k_relayout, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, fmt, src, dst, rows, nsb, dir);
+}
 void launch_gguf_to_dev(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st) {
     relayout(fmt, src, dst, rows, K, 0, st);
 }
 void launch_dev_to_gguf(int fmt, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t K, hipStream_t st) {
     relayout(fmt, src, dst, rows, K, 1, st);
+}
+void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y, hipStream_t st) {
+    const int64_t nsb = K / 256, n = rows * nsb;
+    hipLaunchKernelGGL(k_dequant_dev, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, fmt, w, rows, nsb, y);
+}
+void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st) {
+    const int64_t nsb = K / 256, n = (int64_t)M * nsb;
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, st, fmt, table, nsb, ids, M, h);
 }
 
 }  // namespace sd

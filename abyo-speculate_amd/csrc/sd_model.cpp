@@ -176,13 +176,15 @@ void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t by
         SD_HIP_CHECK(hipFree(t.d));
         t.d = nullptr;
     }
+    if ((size_t)dev_tensor_bytes(fmt, rows, K) >= ((size_t)1 << 31))
+        throw UnsupportedError("a matrix must be smaller than 2 GiB (32-bit buffer offsets)");
+    if (fmt != F32 && rows % 16) throw UnsupportedError("quantised matrices need a multiple of 16 rows");
     t.fmt = fmt;
     t.rows = rows;
     t.K = K;
-    t.bytes = (size_t)rows * dev_row_stride(fmt, K);
+    t.bytes = (size_t)dev_tensor_bytes(fmt, rows, K);
     t.d = dalloc<uint8_t>(t.bytes);
-    if (fmt == F32 || fmt == Q4_K || fmt == Q5_K) {
-        // identical layout (row strides are already 16-byte multiples)
+    if (fmt == F32) {
         SD_HIP_CHECK(hipMemcpy(t.d, host, bytes, hipMemcpyHostToDevice));
     } else {
         uint8_t *tmp = dalloc<uint8_t>(bytes);
@@ -208,7 +210,7 @@ void Model::get_tensor(int layer, int kind, void *host, size_t bytes) {
     const size_t g = (size_t)t.rows * gguf_row_bytes(t.fmt, t.K);
     if (bytes != g) throw ArgError("buffer size does not match the tensor");
     SD_HIP_CHECK(hipSetDevice(cfg.device));
-    if (t.fmt == F32 || t.fmt == Q4_K || t.fmt == Q5_K) {
+    if (t.fmt == F32) {
         SD_HIP_CHECK(hipMemcpy(host, t.d, g, hipMemcpyDeviceToHost));
     } else {
         uint8_t *tmp = dalloc<uint8_t>(g);
@@ -224,6 +226,10 @@ void Model::dequant_tensor(int layer, int kind, float *host) {
     if (!t.set()) throw ArgError("tensor not set");
     SD_HIP_CHECK(hipSetDevice(cfg.device));
     const size_t n = (size_t)t.rows * t.K;
+    if (t.fmt == F32) {
+        SD_HIP_CHECK(hipMemcpy(host, t.d, n * 4, hipMemcpyDeviceToHost));
+        return;
+    }
     float *y = dalloc<float>(n);
     launch_dequant_dev(t.fmt, t.d, t.rows, t.K, y, st);
     SD_HIP_CHECK(hipStreamSynchronize(st));
@@ -259,19 +265,20 @@ void Model::synthesize(int mix, uint64_t seed, float stdv) {
         int rows, K;
         shape_of(cfg, kind, rows, K);
         const int fmt = mix_fmt(mix, cfg.n_layers, layer, kind);
+        if ((size_t)dev_tensor_bytes(fmt, rows, K) >= ((size_t)1 << 31))
+            throw UnsupportedError("a matrix must be smaller than 2 GiB (32-bit buffer offsets)");
+        if (fmt != F32 && rows % 16) throw UnsupportedError("quantised matrices need a multiple of 16 rows");
         if (t.d) SD_HIP_CHECK(hipFree(t.d));
         t.fmt = fmt;
         t.rows = rows;
         t.K = K;
-        t.bytes = (size_t)rows * dev_row_stride(fmt, K);
+        t.bytes = (size_t)dev_tensor_bytes(fmt, rows, K);
         t.d = dalloc<uint8_t>(t.bytes);
         const uint64_t ts = tensor_seed(seed, layer, kind);
         if (kind == K_OUTPUT_NORM || kind == K_ATTN_NORM || kind == K_FFN_NORM) {
             launch_fill_f32((float *)t.d, (int64_t)rows * K, 1.0f, st);
         } else if (fmt == F32) {
             launch_synth_f32((float *)t.d, (int64_t)rows * K, ts, mult, st);
-        } else if (fmt == Q4_K || fmt == Q5_K) {
-            launch_synth_quant(fmt, t.d, rows, K, ts, mult, st);
         } else {
             const size_t g = (size_t)rows * gguf_row_bytes(fmt, K);
             uint8_t *tmp = dalloc<uint8_t>(g);
@@ -344,6 +351,7 @@ void Model::run_gemm(GemmParams &p, int cls, double bytes) {
 }
 
 static double wbytes(const DevTensor &t) { return (double)t.rows * gguf_row_bytes(t.fmt, t.K); }
+static double gemm_bytes(const GemmParams &p, double wbytes);
 
 static GemmSeg seg_of(const DevTensor &t, int tile0, float *out, int ldo, int col0, const float *bias) {
     GemmSeg s;
@@ -382,6 +390,73 @@ void Model::qmatmul(int layer, int kind, const float *x, int M, float *y) {
     hipFree(dx);
     hipFree(dy);
     hipFree(dxp);
+}
+
+// Times `iters` back-to-back launches of one dequant-matmul with HIP events on
+// the model's stream (activations: whatever the work buffers hold).  kind is a
+// matrix kind, or BENCH_QKV / BENCH_GATE_UP for the fused launches of a layer.
+double Model::bench_qmatmul(int layer, int kind, int M, int iters, double *bytes_out) {
+    if (M < 1 || M > cfg.max_batch) throw ArgError("M out of range");
+    if (layer < -1 || layer >= cfg.n_layers) throw ArgError("layer out of range");
+    if ((kind == BENCH_QKV || kind == BENCH_GATE_UP) && layer < 0) throw ArgError("fused launches need a layer");
+    if (iters < 1) throw ArgError("iters must be positive");
+    SD_HIP_CHECK(hipSetDevice(cfg.device));
+    auto &L = lw[layer < 0 ? 0 : layer];
+    GemmParams p{};
+    p.xp = xp;
+    p.M = M;
+    double wb = 0.0;
+    if (kind == BENCH_QKV) {
+        int t0 = 0;
+        const int QD = cfg.q_dim(), KVD = cfg.kv_dim(), QKVD = QD + 2 * KVD;
+        p.seg[0] = seg_of(L[K_ATTN_Q], t0, qkv, QKVD, 0, nullptr);
+        t0 += L[K_ATTN_Q].rows / 16;
+        p.seg[1] = seg_of(L[K_ATTN_K], t0, qkv, QKVD, QD, nullptr);
+        t0 += L[K_ATTN_K].rows / 16;
+        p.seg[2] = seg_of(L[K_ATTN_V], t0, qkv, QKVD, QD + KVD, nullptr);
+        t0 += L[K_ATTN_V].rows / 16;
+        p.nseg = 3;
+        p.ntiles = t0;
+        p.K = cfg.hidden;
+        p.mode = GM_STORE;
+        wb = wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]);
+    } else if (kind == BENCH_GATE_UP) {
+        p.seg[0] = seg_of(L[K_FFN_GATE], 0, nullptr, 0, 0, nullptr);
+        p.seg[1] = seg_of(L[K_FFN_UP], 0, nullptr, 0, 0, nullptr);
+        p.nseg = 2;
+        p.ntiles = L[K_FFN_GATE].rows / 16 * 2;
+        p.K = cfg.hidden;
+        p.mode = GM_SWIGLU;
+        p.act = act;
+        p.act_ld = act_ld;
+        wb = wbytes(L[K_FFN_GATE]) + wbytes(L[K_FFN_UP]);
+    } else {
+        DevTensor &t = slot(*this, layer, kind);
+        if (!t.set() || t.fmt == F32) throw ArgError("bench_qmatmul needs a quantised matrix");
+        if ((size_t)M * t.rows > (size_t)cfg.max_batch * cfg.vocab) throw ArgError("output too large");
+        p.seg[0] = seg_of(t, 0, logits, t.rows, 0, nullptr);
+        p.nseg = 1;
+        p.ntiles = t.rows / 16;
+        p.K = t.K;
+        p.mode = GM_STORE;
+        wb = wbytes(t);
+    }
+    if (p.K > xp_ld && kind != K_FFN_DOWN) throw ArgError("activation buffer too narrow");
+    if (kind == K_FFN_DOWN) p.xp = act;
+    if (bytes_out) *bytes_out = gemm_bytes(p, wb);
+    hipEvent_t a, b;
+    SD_HIP_CHECK(hipEventCreate(&a));
+    SD_HIP_CHECK(hipEventCreate(&b));
+    launch_qgemm(p, st);  // warm
+    SD_HIP_CHECK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) launch_qgemm(p, st);
+    SD_HIP_CHECK(hipEventRecord(b, st));
+    SD_HIP_CHECK(hipEventSynchronize(b));
+    float ms = 0.f;
+    SD_HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return (double)ms * 1e3 / iters;
 }
 
 void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P,

@@ -31,6 +31,7 @@ F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
 ARCH_LLAMA, ARCH_QWEN2 = 0, 1
 MIX_Q4_K, MIX_Q4_K_M, MIX_Q5K_Q80, MIX_Q6_K, MIX_Q5_K, MIX_Q8_0 = range(6)
 PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head", "attn")
+BENCH_QKV, BENCH_GATE_UP = 100, 101
 
 
 class SpeculateError(Exception):
@@ -140,9 +141,13 @@ def load_library(path: str = LIB_PATH):
         "sd_profile_enable": ([P, I32], I32),
         "sd_profile_read": ([P, P, P, P, SZ], SZ),
         "sd_synchronize": ([P], I32),
+        "sd_bench_qmatmul": ([P, I32, I32, SZ, I32, P, P], I32),
         "sd_read_kv_rows": ([P, I32, I32, I32, SZ, SZ, P], I32),
         "sd_cache_len": ([P], SZ),
         "sd_tree_cartesian": ([ctypes.c_uint32, P, P, SZ, P, P, SZ, pSZ], I32),
+        "sd_repack_gguf": ([I32, P, SZ, SZ, P], I32),
+        "sd_unpack_tiles": ([I32, P, SZ, SZ, P], I32),
+        "sd_lane_codes": ([I32, P, I32, I32, P], I32),
         "sd_tree_prune": ([P, P, SZ, P, P, SZ, SZ, P, P, pSZ], I32),
     }
     for name, (args, res) in sigs.items():
@@ -375,6 +380,12 @@ class HipQuantDecoder:
         n = int(_lib.sd_profile_read(self._h, _ptr(cls), _ptr(by), _ptr(ms), cap))
         return [(PROFILE_CLASSES[cls[i]], float(by[i]), float(ms[i])) for i in range(n)]
 
+    def bench_qmatmul(self, layer: int, kind: int, rows: int, iters: int = 50) -> Tuple[float, float]:
+        """(microseconds per launch, algorithmic bytes per launch) of one dequant-matmul."""
+        us, by = ctypes.c_double(), ctypes.c_double()
+        _check(_lib.sd_bench_qmatmul(self._h, layer, kind, rows, iters, ctypes.byref(us), ctypes.byref(by)))
+        return us.value, by.value
+
     def synchronize(self):
         _check(_lib.sd_synchronize(self._h))
 
@@ -412,3 +423,30 @@ def tree_prune(tree, per_step_log_probs: Sequence[Sequence[float]], max_total: i
     _check(L.sd_tree_prune(_ptr(t), _ptr(p), t.size, _ptr(lp), _ptr(br), br.size, max_total, _ptr(ot), _ptr(op),
                            ctypes.byref(n)))
     return ot[:n.value].copy(), op[:n.value].copy()
+
+
+# ---- device weight layout (host only) ----
+def repack_gguf(fmt: int, gguf: np.ndarray, rows: int, K: int) -> np.ndarray:
+    """GGUF row-major blocks -> the library's tile-interleaved device order (same size)."""
+    L = load_library()
+    src = np.ascontiguousarray(gguf).view(np.uint8)
+    out = np.empty_like(src)
+    _check(L.sd_repack_gguf(fmt, _ptr(src), rows, K, _ptr(out)))
+    return out
+
+
+def unpack_tiles(fmt: int, tiles: np.ndarray, rows: int, K: int) -> np.ndarray:
+    L = load_library()
+    src = np.ascontiguousarray(tiles).view(np.uint8)
+    out = np.empty_like(src)
+    _check(L.sd_unpack_tiles(fmt, _ptr(src), rows, K, _ptr(out)))
+    return out
+
+
+def lane_codes(fmt: int, tile_block: np.ndarray, lane: int, chunk: int) -> np.ndarray:
+    """The 4 code words lane `lane` builds for K-chunk `chunk` of one tile block."""
+    L = load_library()
+    tb = np.ascontiguousarray(tile_block).view(np.uint8)
+    out = np.empty(4, np.uint32)
+    _check(L.sd_lane_codes(fmt, _ptr(tb), lane, chunk, _ptr(out)))
+    return out

@@ -198,12 +198,36 @@ sd_status sd_profile_enable(sd_model *m, int32_t on);
  * entries written. */
 size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap);
 sd_status sd_synchronize(sd_model *m);
+/* Microbenchmark of one dequant-matmul launch of layer `layer`: kind is a
+ * matrix kind, SD_BENCH_QKV (fused Q/K/V) or SD_BENCH_GATE_UP (fused gate/up +
+ * SiLU), at `rows` activation rows; *us = mean microseconds per launch over
+ * `iters` back-to-back launches timed with HIP events, *bytes = algorithmic
+ * bytes per launch (weight blocks + activations in + outputs). */
+enum { SD_BENCH_QKV = 100, SD_BENCH_GATE_UP = 101 };
+sd_status sd_bench_qmatmul(sd_model *m, int32_t layer, int32_t kind, size_t rows, int32_t iters, double *us,
+                           double *bytes);
 /* Copies n fp16 cache rows [pos0, pos0+n) of one (layer, K=0/V=1, kv head):
  * out [n][head_dim] (checks of the in-place KV layout). */
 sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t head, size_t pos0, size_t n,
                           uint16_t *out);
 /* Number of positions currently held in the KV cache. */
 size_t sd_cache_len(const sd_model *m);
+
+/* ---- device weight layout (host only; no GPU needed) ---------------------------- */
+/* The library keeps quantised matrices in a tile-interleaved order: each
+ * 16-row x 256-column tile block is rearranged so that every load of the
+ * matmul kernel's MFMA lane mapping reads contiguous bytes (same byte count as
+ * GGUF).  sd_model_set_tensor repacks on the device; these do it on the host,
+ * e.g. for a loader that streams a GGUF file straight into the device layout.
+ * rows must be a multiple of 16 and K of 256.  GGUF: row-major blocks as in
+ * the file; tiles: rows/16 x K/256 tile blocks, tile-major. */
+sd_status sd_repack_gguf(int32_t fmt, const void *gguf, size_t rows, size_t K, void *out);
+sd_status sd_unpack_tiles(int32_t fmt, const void *tiles, size_t rows, size_t K, void *gguf_out);
+/* The four 32-bit words (two fp16 codes each, slots 0-1, 2-3, 4-5, 6-7) that
+ * lane `lane` of the matmul builds for K-chunk `chunk` from one tile block: a
+ * layout self-check hook; codes are 1024 + q (0x6400 | q) for slots 0-3 and
+ * 64 + q for slots 4-7 (1024 + q + 128 throughout for Q8_0). */
+sd_status sd_lane_codes(int32_t fmt, const void *tile_block, int32_t lane, int32_t chunk, uint32_t *out);
 
 /* ---- draft-tree builders (host only; no GPU needed) ---------------------------- */
 /* build_cartesian_tree (methods/medusa.rs:172-193): step d has branching[d]
