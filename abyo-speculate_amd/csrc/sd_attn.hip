@@ -5,17 +5,25 @@
 // rotation at quantized_qwen2_local.rs:98-109) and the additive masks of
 // causal_bias (:332-350) / DraftTree::full_attention_bias (tree.rs:220-264).
 //
-// KV layout per layer: K[n_kv][cap][hd], V[n_kv][cap][hd] fp16.  The M new
+// KV layout per layer: n_kv streams of K and of V, each cap positions x hd
+// fp16 in the blocked order of kv_k_off / kv_v_off (sd_common.hpp).  The M new
 // rows are written in place at [P, P+M) (no cat, no repeat_kv copies).
 // Visibility: key j < P is visible to every query; key P+t is visible to
 // query token i iff bit t of mask[i] is set (ancestor-or-self for trees,
 // t <= i for a causal chain).
 //
-// Attention runs as split flash-decoding.  A workgroup owns one KV head, one
-// contiguous range of 64-key chunks (a split) and up to 256 queries (the
-// n_rep query heads of the group times the M tokens).  Scores are computed
-// transposed, S^T = K Q^T, so the MFMA result layout is directly the B
-// operand of O^T = V^T P^T.  Split boundaries depend only on P, so a query's
+// Attention is split flash-decoding with the KV streamed straight from HBM
+// into MFMA operand registers (no LDS staging): the blocked cache layout makes
+// every operand a 16-byte load per lane, 1 KiB contiguous per wave.  Scores
+// are computed transposed, S^T = K Q^T (16 keys x 16 queries per MFMA tile),
+// so a lane's accumulator already holds the P^T operand of O^T = V^T P^T.
+//
+// Grid (kv head, key split, query group).  A workgroup's 4 waves take 4
+// consecutive key ranges of keys_per_wave keys and all query tiles of the
+// group (the n_rep query heads of the KV head times the M tokens, 16 per
+// tile); their partial softmax states are merged in LDS in a fixed order, and
+// the splits by a combine kernel (skipped when one split covers all keys).
+// keys_per_wave and the split boundaries depend on P only, so a query's
 // result does not depend on how many other queries share the call.
 #include "sd_common.hpp"
 #include "sd_kernels_attn.hpp"
@@ -51,224 +59,298 @@ __global__ void k_rope_kv(RopeKvParams p) {
         const int h = hh - p.n_heads;
         const float *xk = row + p.n_heads * p.hd + h * p.hd;
         const float *xv = row + (p.n_heads + p.n_kv) * p.hd + h * p.hd;
-        const int64_t dst = ((int64_t)h * p.cap + p.P + m) * p.hd;
+        uint16_t *ks = p.kc + (int64_t)h * p.cap * p.hd, *vs = p.vc + (int64_t)h * p.cap * p.hd;
+        const int64_t t = p.P + m;
         const float k0 = xk[a], k1 = xk[b];
-        p.kc[dst + a] = f2h(k0 * c - k1 * s);
-        p.kc[dst + b] = f2h(k0 * s + k1 * c);
-        p.vc[dst + a] = f2h(xv[a]);
-        p.vc[dst + b] = f2h(xv[b]);
+        ks[kv_k_off(t, a, p.hd)] = f2h(k0 * c - k1 * s);
+        ks[kv_k_off(t, b, p.hd)] = f2h(k0 * s + k1 * c);
+        vs[kv_v_off(t, a, p.hd)] = f2h(xv[a]);
+        vs[kv_v_off(t, b, p.hd)] = f2h(xv[b]);
     }
 }
 
 #pragma clang fp contract(fast)
 
-// ---- flash-decode over one split --------------------------------------------
-constexpr int QPW = 4;   // query tiles per wave
-constexpr int KCH = 64;  // keys per chunk
+// ---- flash-decode over one key split -------------------------------------------
+template <int HD> struct KvStep {
+    uintx4 k[2][HD / 32];  // S^T A operands: two 16-key tiles x HD/32 d-chunks
+    uintx4 v[HD / 16];     // O^T A operands: HD/16 d-tiles x 32 key slots
+};
 
+// 32 keys [kk, kk+32) of one stream: 16-byte pieces, 1 KiB per wave each
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_split(AttnParams p) {
+__device__ __forceinline__ void kv_load_k(KvStep<HD> &b, const uint16_t *kb, int kk, int r16, int g) {
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int dc = 0; dc < HD / 32; dc++)
+            b.k[kt][dc] = *(const uintx4 *)(kb + (int64_t)((kk >> 4) + kt) * 16 * HD + dc * 512 + r16 * 32 + g * 8);
+}
+template <int HD>
+__device__ __forceinline__ void kv_load_v(KvStep<HD> &b, const uint16_t *vb, int kk, int r16, int g) {
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++)
+        b.v[dt] = *(const uintx4 *)(vb + (int64_t)(kk >> 5) * 32 * HD + (dt * 16 + r16) * 32 + g * 8);
+}
+
+template <int HD, int QT> struct AttnState {
+    half8 qf[QT][HD / 32];
+    floatx4 o[QT][HD / 16];
+    float m[QT], l[QT];
+    uint64_t mk0[QT], mk1[QT];
+};
+
+// key of P^T / V^T slot j (0..7) of lane group g within a 32-key step
+__device__ __forceinline__ int slot_key(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
+
+// One 32-key step for all query tiles: scores and softmax first, then the
+// next step's V loads are issued (the current K is dead by then, so the two
+// register buffers never hold four operand sets at once), then O^T += V^T P^T.
+template <int HD, int QT>
+__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const uint16_t *vb,
+                                          int kk, int k1, int P, int T, float sl2, int r16, int g) {
+    constexpr int NDC = HD / 32, NDT = HD / 16;
+    const bool full = kk + 32 <= P;  // every key of the step is visible to every query
+    half8 bp[QT];
+    float alpha[QT];
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        floatx4 st[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dc = 0; dc < NDC; dc++)
+                st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b.k[kt][dc]), S.qf[t][dc],
+                                                                st[kt], 0, 0, 0);
+        }
+        float cm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = st[kt][i] * sl2;
+                if (!full) {
+                    const int key = kk + kt * 16 + 4 * g + i;
+                    bool vis = key < P;
+                    if (!vis && key < T) {
+                        const int tt = key - P;
+                        vis = (((tt < 64 ? S.mk0[t] : S.mk1[t]) >> (tt & 63)) & 1ull) != 0;
+                    }
+                    v = vis ? v : -INFINITY;
+                }
+                st[kt][i] = v;
+                cm = fmaxf(cm, v);
+            }
+        cm = fmaxf(cm, __shfl_xor(cm, 16));
+        cm = fmaxf(cm, __shfl_xor(cm, 32));
+        const float mnew = fmaxf(S.m[t], cm);
+        const float muse = mnew == -INFINITY ? 0.f : mnew;
+        alpha[t] = exp2f(S.m[t] - muse);
+        float ps = 0.f;
+        uint32_t pk[4];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                e[i] = exp2f(st[kt][i] - muse);
+                ps += e[i];
+            }
+            pk[2 * kt] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
+            pk[2 * kt + 1] = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        S.l[t] = S.l[t] * alpha[t] + ps;
+        S.m[t] = mnew;
+        const uintx4 bu = {pk[0], pk[1], pk[2], pk[3]};
+        bp[t] = __builtin_bit_cast(half8, bu);
+    }
+    if (kk + 32 < k1) kv_load_v<HD>(nb, vb, kk + 32, r16, g);
+    if (kk + 32 > T) {
+        // keys >= T hold stale cache rows: their P^T entries are 0, and their V
+        // entries are zeroed so that nothing but finite values meets the MFMA
+        uint32_t keep[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            keep[w] = (kk + slot_key(g, 2 * w) < T ? 0x0000ffffu : 0u) |
+                      (kk + slot_key(g, 2 * w + 1) < T ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            b.v[dt].x &= keep[0];
+            b.v[dt].y &= keep[1];
+            b.v[dt].z &= keep[2];
+            b.v[dt].w &= keep[3];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < QT; t++)
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            S.o[t][dt] *= alpha[t];
+            S.o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b.v[dt]), bp[t], S.o[t][dt],
+                                                                0, 0, 0);
+        }
+}
+
+template <int HD, int QT>
+__global__ __launch_bounds__(256) void k_attn(AttnParams p) {
+    constexpr int NDC = HD / 32, NDT = HD / 16;
     const int h = blockIdx.x, s = blockIdx.y, qg = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int nq = p.M * p.n_rep;
     const int T = p.P + p.M;
-    const int nchunks = (T + KCH - 1) / KCH;
-    const int c0 = s * p.cps, c1 = min(c0 + p.cps, nchunks);
-    constexpr int NDC = HD / 32, NDT = HD / 16;
+    const int k0 = (s * 4 + wave) * p.keys_per_wave;
+    const int k1 = min(k0 + p.keys_per_wave, T);
+    const uint16_t *kb = p.kc + (int64_t)h * p.cap * HD;
+    const uint16_t *vb = p.vc + (int64_t)h * p.cap * HD;
 
-    __shared__ uint16_t Ks[KCH][HD + 8];
-    __shared__ uint16_t Vt[HD][KCH + 8];
-
-    const uint16_t *kbase = p.kc + (int64_t)h * p.cap * HD;
-    const uint16_t *vbase = p.vc + (int64_t)h * p.cap * HD;
-
-    // this wave's query tiles
-    int ntl = 0;
-    int tq0[QPW];
+    AttnState<HD, QT> S;
 #pragma unroll
-    for (int t = 0; t < QPW; t++) {
-        const int tile = qg * (4 * QPW) + wave + 4 * t;
-        tq0[t] = tile * 16;
-        if (tile * 16 < nq) ntl = t + 1;
-    }
-
-    half8 qf[QPW][NDC];
-    floatx4 o[QPW][NDT];
-    float mrun[QPW], lrun[QPW];
-    int tok[QPW];
-    bool qlive[QPW];
-#pragma unroll
-    for (int t = 0; t < QPW; t++) {
-        const int q = tq0[t] + r16;
-        qlive[t] = t < ntl && q < nq;
-        const int m = qlive[t] ? q / p.n_rep : 0, r = qlive[t] ? q % p.n_rep : 0;
-        tok[t] = m;
+    for (int t = 0; t < QT; t++) {
+        const int q = (qg * QT + t) * 16 + r16;
+        const bool live = q < nq;
+        const int m = live ? q / p.n_rep : 0, r = live ? q % p.n_rep : 0;
         const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + r) * p.M + m) * HD;
 #pragma unroll
         for (int dc = 0; dc < NDC; dc++) {
             uintx4 v = {0u, 0u, 0u, 0u};
-            if (qlive[t]) v = *(const uintx4 *)(qr + dc * 32 + g * 8);
-            qf[t][dc] = __builtin_bit_cast(half8, v);
+            if (live) v = *(const uintx4 *)(qr + dc * 32 + g * 8);
+            S.qf[t][dc] = __builtin_bit_cast(half8, v);
         }
+        S.mk0[t] = p.mask[(int64_t)m * p.mask_words];
+        S.mk1[t] = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        mrun[t] = -INFINITY;
-        lrun[t] = 0.f;
+        for (int dt = 0; dt < NDT; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        S.m[t] = -INFINITY;
+        S.l[t] = 0.f;
+    }
+    const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
+
+    // two register buffers: the next 32 keys load while the current ones compute
+    // (K at the start of a step, V once the step's scores are done)
+    KvStep<HD> b0, b1;
+    int kk = k0;
+    if (kk < k1) {
+        kv_load_k<HD>(b0, kb, kk, r16, g);
+        kv_load_v<HD>(b0, vb, kk, r16, g);
+    }
+    while (kk < k1) {
+        if (kk + 32 < k1) kv_load_k<HD>(b1, kb, kk + 32, r16, g);
+        attn_step<HD, QT>(S, b0, b1, vb, kk, k1, p.P, T, sl2, r16, g);
+        kk += 32;
+        if (kk >= k1) break;
+        if (kk + 32 < k1) kv_load_k<HD>(b0, kb, kk + 32, r16, g);
+        attn_step<HD, QT>(S, b1, b0, vb, kk, k1, p.P, T, sl2, r16, g);
+        kk += 32;
     }
 
-    const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e)
-
-    for (int c = c0; c < c1; c++) {
-        __syncthreads();
-        // stage K (key-major) and V (dim-major) of keys [c*64, c*64+64)
-        for (int piece = threadIdx.x; piece < KCH * HD / 8; piece += 256) {
-            const int key = piece / (HD / 8), d8 = piece % (HD / 8);
-            const int kg = c * KCH + key;
-            uintx4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-            if (kg < T) {
-                kv = *(const uintx4 *)(kbase + (int64_t)kg * HD + d8 * 8);
-                vv = *(const uintx4 *)(vbase + (int64_t)kg * HD + d8 * 8);
-            }
-            *(uintx4 *)&Ks[key][d8 * 8] = kv;
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+    // ---- merge the 4 waves' states: rescale to the common max, then
+    // (o0 + o2) + (o1 + o3) through LDS ----
+    __shared__ float sml[4][QT][16][2];
+    __shared__ floatx4 sob[2][QT][NDT][64];
+    if (g == 0) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                Vt[d8 * 8 + 2 * e][key] = (uint16_t)(vw[e] & 0xffff);
-                Vt[d8 * 8 + 2 * e + 1][key] = (uint16_t)(vw[e] >> 16);
-            }
-        }
-        __syncthreads();
-
-#pragma unroll
-        for (int t = 0; t < QPW; t++) {
-            if (t >= ntl) break;
-            // S^T tile: keys (4 x 16) x 16 queries
-            floatx4 st[4];
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int dc = 0; dc < NDC; dc++) {
-                    const half8 a = *(const half8 *)&Ks[kt * 16 + r16][dc * 32 + g * 8];
-                    st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[t][dc], st[kt], 0, 0, 0);
-                }
-            }
-            // scale + mask, column max
-            float cm = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = c * KCH + kt * 16 + 4 * g + i;
-                    bool vis;
-                    if (key < p.P) {
-                        vis = true;
-                    } else if (key < T) {
-                        const int tt = key - p.P;
-                        const uint64_t w = p.mask[(int64_t)tok[t] * p.mask_words + (tt >> 6)];
-                        vis = (w >> (tt & 63)) & 1ull;
-                    } else {
-                        vis = false;
-                    }
-                    const float v = vis ? st[kt][i] * sl2 : -INFINITY;
-                    st[kt][i] = v;
-                    cm = fmaxf(cm, v);
-                }
-            cm = fmaxf(cm, __shfl_xor(cm, 16));
-            cm = fmaxf(cm, __shfl_xor(cm, 32));
-            const float mnew = fmaxf(mrun[t], cm);
-            const float muse = mnew == -INFINITY ? 0.f : mnew;
-            const float alpha = exp2f(mrun[t] - muse);
-            float ps = 0.f;
-            uint32_t pk[4][2];
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                float e[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    e[i] = exp2f(st[kt][i] - muse);
-                    ps += e[i];
-                }
-                pk[kt][0] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
-                pk[kt][1] = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
-            }
-            ps += __shfl_xor(ps, 16);
-            ps += __shfl_xor(ps, 32);
-            lrun[t] = lrun[t] * alpha + ps;
-            mrun[t] = mnew;
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) o[t][dt] *= alpha;
-            // O^T += V^T P^T over two 32-key groups
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                uintx4 bu = {pk[2 * j][0], pk[2 * j][1], pk[2 * j + 1][0], pk[2 * j + 1][1]};
-                const half8 b = __builtin_bit_cast(half8, bu);
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) {
-                    const uint16_t *vr = &Vt[dt * 16 + r16][0];
-                    const uint2 lo = *(const uint2 *)(vr + (2 * j) * 16 + 4 * g);
-                    const uint2 hi = *(const uint2 *)(vr + (2 * j + 1) * 16 + 4 * g);
-                    uintx4 au = {lo.x, lo.y, hi.x, hi.y};
-                    o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, au), b, o[t][dt],
-                                                                      0, 0, 0);
-                }
-            }
+        for (int t = 0; t < QT; t++) {
+            sml[wave][t][r16][0] = S.m[t];
+            sml[wave][t][r16][1] = S.l[t];
         }
     }
-
-    // partials: o [split][head][m][HD], ml [split][head][m][2]
+    __syncthreads();
+    float Lt[QT], Mt[QT];
 #pragma unroll
-    for (int t = 0; t < QPW; t++) {
-        if (t >= ntl || !qlive[t]) continue;
-        const int q = tq0[t] + r16;
+    for (int t = 0; t < QT; t++) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) mx = fmaxf(mx, sml[w][t][r16][0]);
+        float L = 0.f, fme = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = sml[w][t][r16][0];
+            const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+            L += sml[w][t][r16][1] * f;
+            if (w == wave) fme = f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) S.o[t][dt] *= fme;
+        Lt[t] = L;
+        Mt[t] = mx;
+    }
+    if (wave >= 2) {
+#pragma unroll
+        for (int t = 0; t < QT; t++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) sob[wave - 2][t][dt][lane] = S.o[t][dt];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+        for (int t = 0; t < QT; t++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) S.o[t][dt] += sob[wave][t][dt][lane];
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+        for (int t = 0; t < QT; t++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) sob[0][t][dt][lane] = S.o[t][dt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        const int q = (qg * QT + t) * 16 + r16;
+        if (q >= nq) continue;
         const int m = q / p.n_rep, r = q % p.n_rep;
         const int head = h * p.n_rep + r;
-        const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
-        float *po = p.part_o + pi * HD;
+        if (p.nsplit == 1) {
+            const float inv = 1.0f / Lt[t];
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) *(floatx4 *)(po + dt * 16 + 4 * g) = o[t][dt];
-        if (g == 0) {
-            p.part_ml[2 * pi] = mrun[t];
-            p.part_ml[2 * pi + 1] = lrun[t];
+            for (int dt = 0; dt < NDT; dt++) {
+                const floatx4 y = S.o[t][dt] + sob[0][t][dt][lane];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int64_t k = (int64_t)head * HD + dt * 16 + 4 * g + i;
+                    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(y[i] * inv);
+                }
+            }
+        } else {
+            const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
+            float *po = p.part_o + pi * HD;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) *(floatx4 *)(po + dt * 16 + 4 * g) = S.o[t][dt] + sob[0][t][dt][lane];
+            if (g == 0) {
+                p.part_ml[2 * pi] = Mt[t];
+                p.part_ml[2 * pi + 1] = Lt[t];
+            }
         }
     }
 }
 
 // ---- combine splits -> fp16 fragment-layout input of wo ----------------------
-// grid (n_heads, M), block HD threads.  Every split's (m, l) and output are
-// loaded before use (up to 64 splits in registers), so the combine costs one
-// memory round trip.
-constexpr int MAX_SPLITS = 64;
-__global__ void k_attn_combine(AttnParams p, int nsplit) {
+// grid (n_heads, M), block hd threads; splits are merged in index order.
+__global__ __launch_bounds__(128) void k_attn_combine(AttnParams p) {
     const int head = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
-    const int HD = p.hd;
-    float ms[MAX_SPLITS], ls[MAX_SPLITS], os[MAX_SPLITS];
-#pragma unroll
-    for (int s = 0; s < MAX_SPLITS; s++) {
-        if (s < nsplit) {
-            const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
-            ms[s] = p.part_ml[2 * pi];
-            ls[s] = p.part_ml[2 * pi + 1];
-            os[s] = p.part_o[pi * HD + d];
-        }
-    }
+    const int HD = p.hd, ns = p.nsplit;
+    const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
+    const int64_t pi0 = (int64_t)head * p.M + m;
     float mx = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < MAX_SPLITS; s++)
-        if (s < nsplit) mx = fmaxf(mx, ms[s]);
+    for (int s = 0; s < ns; s++) mx = fmaxf(mx, p.part_ml[2 * (pi0 + s * stride)]);
     float L = 0.f, acc = 0.f;
-#pragma unroll
-    for (int s = 0; s < MAX_SPLITS; s++) {
-        if (s < nsplit && ms[s] != -INFINITY) {
-            const float f = exp2f(ms[s] - mx);
-            L += ls[s] * f;
-            acc += os[s] * f;
-        }
+#pragma unroll 4
+    for (int s = 0; s < ns; s++) {
+        const int64_t pi = pi0 + s * stride;
+        const float ms = p.part_ml[2 * pi];
+        const float f = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+        L += p.part_ml[2 * pi + 1] * f;
+        acc += p.part_o[pi * HD + d] * f;
     }
-    const float y = acc / L;
     const int64_t k = (int64_t)head * HD + d;
-    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(y);
+    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / L);
 }
 
 // ---- host launchers ----------------------------------------------------------
@@ -276,30 +358,43 @@ void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
     hipLaunchKernelGGL(k_rope_kv, dim3(p.M, p.n_heads + p.n_kv), dim3(p.hd / 2), 0, st, p);
 }
 
-int attn_chunks_per_split(int P, int n_kv) {
-    const int nch_p = (P + 1 + KCH - 1) / KCH;
-    int target = 256 / (n_kv > 0 ? n_kv : 1);
-    if (target > MAX_SPLITS - 3) target = MAX_SPLITS - 3;  // up to 3 more splits for <= 128 new rows
-    if (target < 1) target = 1;
-    if (target > nch_p) target = nch_p;
-    return (nch_p + target - 1) / target;
+static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
+
+AttnSplit attn_split(int P, int M, int n_kv) {
+    const int target = attn_target_splits(n_kv);
+    int kpw = (P + 1 + 4 * target - 1) / (4 * target);
+    kpw = kpw < 32 ? 32 : (kpw + 31) / 32 * 32;
+    const int T = P + M;
+    return AttnSplit{kpw, (T + 4 * kpw - 1) / (4 * kpw)};
 }
 
-int attn_num_splits(int P, int M, int cps) {
-    const int nchunks = (P + M + KCH - 1) / KCH;
-    return (nchunks + cps - 1) / cps;
+// 4 * kpw >= (P + 1) / target and 4 * kpw >= 128 >= M, so
+// nsplit = ceil((P + M) / (4 kpw)) <= target + 1
+int attn_max_splits(int n_kv) { return attn_target_splits(n_kv) + 3; }
+
+template <int HD>
+static void launch_attn_hd(const AttnParams &p, dim3 grid, int qt, hipStream_t st) {
+    if (qt == 1) hipLaunchKernelGGL((k_attn<HD, 1>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((k_attn<HD, 2>), grid, dim3(256), 0, st, p);
 }
 
 void launch_attention(const AttnParams &p, hipStream_t st) {
-    const int nsplit = attn_num_splits(p.P, p.M, p.cps);
-    const int nq = p.M * p.n_rep;
-    const int nqg = (nq + 16 * 4 * QPW - 1) / (16 * 4 * QPW);
-    const dim3 grid(p.n_kv, nsplit, nqg);
-    if (p.hd == 128) hipLaunchKernelGGL(k_attn_split<128>, grid, dim3(256), 0, st, p);
-    else if (p.hd == 64) hipLaunchKernelGGL(k_attn_split<64>, grid, dim3(256), 0, st, p);
+    if (p.keys_per_wave < 32 || p.keys_per_wave % 32) throw BackendError("attention: keys_per_wave");
+    if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
+    if (p.cap % 32 || (int64_t)p.P + p.M > p.cap) throw BackendError("attention: cache capacity");
+    if (p.mask_words < 1 || p.mask_words > 2 || p.M > 64 * p.mask_words) throw BackendError("attention: mask words");
+    // Query tiles per wave: at most 2 (two double-buffered 32-key operand
+    // sets and 2 tiles' accumulators fill the register file).  More query
+    // tiles become more workgroups along z; with the KV head as blockIdx.x
+    // and n_kv a multiple of the 8 XCDs, every workgroup of one head lands on
+    // the same XCD, so the query groups re-read that head's keys from its L2.
+    const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
+    const int qt = nqt <= 1 ? 1 : 2;
+    const dim3 grid(p.n_kv, p.nsplit, (nqt + qt - 1) / qt);
+    if (p.hd == 128) launch_attn_hd<128>(p, grid, qt, st);
+    else if (p.hd == 64) launch_attn_hd<64>(p, grid, qt, st);
     else throw BackendError("attention: head_dim must be 64 or 128");
-    if (nsplit > MAX_SPLITS) throw BackendError("attention: too many splits");
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p, nsplit);
+    if (p.nsplit > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p);
 }
 
 }  // namespace sd

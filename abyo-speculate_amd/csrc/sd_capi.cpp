@@ -372,8 +372,17 @@ sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t hea
         setdev(m);
         const uint16_t *base = m->model->kv + (((int64_t)layer * 2 + which) * c.n_kv_heads + head) * m->model->cap *
                                                   c.head_dim;
+        // copy the whole 32-position blocks covering the rows, then gather the
+        // rows out of the blocked layout (sd_common.hpp: kv_k_off / kv_v_off)
+        const int64_t b0 = (int64_t)pos0 / 32, b1 = ((int64_t)(pos0 + n) + 31) / 32;
+        std::vector<uint16_t> blk((size_t)(b1 - b0) * 32 * c.head_dim);
         SD_HIP_CHECK(hipStreamSynchronize(m->model->st));
-        SD_HIP_CHECK(hipMemcpy(out, base + pos0 * c.head_dim, n * c.head_dim * 2, hipMemcpyDeviceToHost));
+        if (!blk.empty())
+            SD_HIP_CHECK(hipMemcpy(blk.data(), base + b0 * 32 * c.head_dim, blk.size() * 2, hipMemcpyDeviceToHost));
+        const int64_t off0 = b0 * 32 * c.head_dim;
+        for (size_t j = 0; j < n; j++)
+            for (int d = 0; d < c.head_dim; d++)
+                out[j * c.head_dim + d] = blk[sd::kv_off(which, (int64_t)(pos0 + j), d, c.head_dim) - off0];
     });
 }
 

@@ -58,6 +58,27 @@ __host__ __device__ inline int frag_slot(int e) {
 }
 __host__ __device__ inline int64_t frag_index(int64_t k) { return (k & ~int64_t(255)) + frag_slot((int)(k & 255)); }
 
+// ---- KV cache layout ----------------------------------------------------
+// The cache holds, per (layer, K/V, kv head) "stream", cap positions x hd
+// fp16 values (cap a multiple of 32), blocked so that every MFMA operand the
+// attention kernel loads is one contiguous 16-byte piece per lane and 1 KiB
+// per wave:
+//   K: [pos / 16][d / 32][pos % 16][d % 32]  (A operand of S^T = K Q^T: a lane
+//      reads 8 consecutive d of one key)
+//   V: [pos / 32][d][slot(pos % 32)]         (A operand of O^T = V^T P^T: a lane
+//      reads the 8 keys its P^T fragment holds, {4g..4g+3, 16+4g..16+4g+3},
+//      as slots 8g..8g+7)
+__host__ __device__ inline int64_t kv_k_off(int64_t pos, int d, int hd) {
+    return (pos >> 4) * 16 * hd + (d >> 5) * 512 + (pos & 15) * 32 + (d & 31);
+}
+__host__ __device__ inline int kv_v_slot(int r) { return 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3); }
+__host__ __device__ inline int64_t kv_v_off(int64_t pos, int d, int hd) {
+    return (pos >> 5) * 32 * hd + d * 32 + kv_v_slot((int)(pos & 31));
+}
+__host__ __device__ inline int64_t kv_off(int which, int64_t pos, int d, int hd) {
+    return which ? kv_v_off(pos, d, hd) : kv_k_off(pos, d, hd);
+}
+
 // ---- fp16 bit helpers --------------------------------------------------
 __device__ inline float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ inline uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }

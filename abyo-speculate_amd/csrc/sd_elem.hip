@@ -160,20 +160,22 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float *x, int64_t ld,
 
 // ---- KV compaction: rows P + src[j] -> P + j, j = 1..n-1 (src[0] == 0) -------
 // grid (L * 2 * n_kv), block 256: each workgroup gathers its stream's rows into
-// LDS first, so the in-place move is race free.
-__global__ __launch_bounds__(256) void k_keep_kv_tail(uint16_t *kv, int64_t stream_stride, int hd, int P,
+// LDS first, so the in-place move is race free.  Streams alternate K, V every
+// n_kv streams; element places follow the blocked cache layout (kv_off).
+__global__ __launch_bounds__(256) void k_keep_kv_tail(uint16_t *kv, int64_t stream_stride, int n_kv, int hd, int P,
                                                       const int *src, int n) {
     extern __shared__ uint16_t buf[];
     uint16_t *base = kv + (int64_t)blockIdx.x * stream_stride;
+    const int which = (int)((blockIdx.x / n_kv) & 1);
     const int per = n * hd;
     for (int i = threadIdx.x; i < per; i += 256) {
         const int j = i / hd, d = i % hd;
-        buf[i] = base[(int64_t)(P + src[j]) * hd + d];
+        buf[i] = base[kv_off(which, P + src[j], d, hd)];
     }
     __syncthreads();
     for (int i = threadIdx.x; i < per; i += 256) {
         const int j = i / hd, d = i % hd;
-        base[(int64_t)(P + j) * hd + d] = buf[i];
+        base[kv_off(which, P + j, d, hd)] = buf[i];
     }
 }
 
@@ -200,10 +202,10 @@ void launch_argmax_reduce(const float *pv, const int *pi, int nwg, int M, int *o
 void launch_argmax_rows(const float *x, int64_t ld, int n, int M, int *out, hipStream_t st) {
     hipLaunchKernelGGL(k_argmax_rows, dim3(M), dim3(256), 0, st, x, ld, n, out);
 }
-void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int hd, int P, const int *src, int n,
-                         hipStream_t st) {
+void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int n_kv, int hd, int P, const int *src,
+                         int n, hipStream_t st) {
     const size_t lds = (size_t)n * hd * sizeof(uint16_t);
-    hipLaunchKernelGGL(k_keep_kv_tail, dim3(nstreams), dim3(256), lds, st, kv, stream_stride, hd, P, src, n);
+    hipLaunchKernelGGL(k_keep_kv_tail, dim3(nstreams), dim3(256), lds, st, kv, stream_stride, n_kv, hd, P, src, n);
 }
 
 }  // namespace sd

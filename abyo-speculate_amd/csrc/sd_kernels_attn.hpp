@@ -10,11 +10,21 @@ struct RopeKvParams {
     const int *pos;     // [M] absolute positions
     const float *cos_t, *sin_t;  // [ctx][hd/2]
     uint16_t *q16;      // [n_heads][M][hd] fp16 (rotated q)
-    uint16_t *kc, *vc;  // this layer's cache [n_kv][cap][hd]
+    uint16_t *kc, *vc;  // this layer's cache streams, [n_kv][cap * hd] in the blocked layout (kv_k_off / kv_v_off)
     int64_t cap;
     int P, M, n_heads, n_kv, hd;
     int interleaved;    // 1: rope_i pairs (2i, 2i+1) (Llama); 0: rope pairs (i, i+hd/2) (Qwen2)
 };
+
+// Work split of one attention call, a function of the prefix length P and the
+// head layout only (never of M), so a query's arithmetic does not depend on
+// how many other queries share the call.
+struct AttnSplit {
+    int keys_per_wave;  // multiple of 32; a workgroup covers 4 * keys_per_wave keys
+    int nsplit;         // workgroups along the keys (for T = P + M keys)
+};
+AttnSplit attn_split(int P, int M, int n_kv);
+int attn_max_splits(int n_kv);  // upper bound of nsplit over all P, M <= 128
 
 struct AttnParams {
     const uint16_t *q16;
@@ -23,7 +33,7 @@ struct AttnParams {
     const uint64_t *mask;  // [M][mask_words]
     int mask_words;
     int P, M, n_heads, n_kv, n_rep, hd;
-    int cps;               // 64-key chunks per split (a function of P only)
+    int keys_per_wave, nsplit;
     float scale;           // 1/sqrt(hd)
     float *part_o;         // [nsplit][n_heads][M][hd]
     float *part_ml;        // [nsplit][n_heads][M][2]
@@ -32,8 +42,6 @@ struct AttnParams {
 };
 
 void launch_rope_kv(const RopeKvParams &p, hipStream_t st);
-int attn_chunks_per_split(int P, int n_kv);
-int attn_num_splits(int P, int M, int cps);
 void launch_attention(const AttnParams &p, hipStream_t st);
 
 }  // namespace sd

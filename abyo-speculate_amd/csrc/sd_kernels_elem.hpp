@@ -15,7 +15,7 @@ void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uin
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st);
 void launch_argmax_reduce(const float *pv, const int *pi, int nwg, int M, int *out, hipStream_t st);
 void launch_argmax_rows(const float *x, int64_t ld, int n, int M, int *out, hipStream_t st);
-void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int hd, int P, const int *src, int n,
-                         hipStream_t st);
+void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int n_kv, int hd, int P, const int *src,
+                         int n, hipStream_t st);
 
 }  // namespace sd

@@ -101,21 +101,17 @@ __global__ void k_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int64_t n
     for (int e = 0; e < 256; e++) o[e] = deq_gguf(fmt, gg, e);
 }
 
-// h[m][k] = table[ids[m]][k] (Embedding over the dequantised token table):
-// one thread per (token, superblock)
-__global__ void k_embed(int fmt, const uint8_t *table, int64_t nsb, const int *ids, int M, float *h) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)M * nsb) return;
-    const int m = (int)(i / nsb);
-    const int64_t sb = i % nsb, row = ids[m];
-    float *o = h + (int64_t)m * nsb * 256 + sb * 256;
+// h[m][k] = table[ids[m]][k] (Embedding over the dequantised token table),
+// from the table's GGUF-order copy: grid (M, K/256), one thread per element
+__global__ __launch_bounds__(256) void k_embed(int fmt, const uint8_t *table, int64_t nsb, const int *ids, float *h) {
+    const int m = blockIdx.x, sb = blockIdx.y, e = threadIdx.x;
+    const int64_t row = ids[m];
+    float *o = h + ((int64_t)m * nsb + sb) * 256;
     if (fmt == F32) {
-        for (int e = 0; e < 256; e++) o[e] = ((const float *)table)[row * nsb * 256 + sb * 256 + e];
+        o[e] = ((const float *)table)[(row * nsb + sb) * 256 + e];
         return;
     }
-    uint8_t gg[272];
-    unpack_sb(fmt, table + ((row >> 4) * nsb + sb) * (int64_t)tile_block_bytes(fmt), (int)(row & 15), gg);
-    for (int e = 0; e < 256; e++) o[e] = deq_gguf(fmt, gg, e);
+    o[e] = deq_gguf(fmt, table + (row * nsb + sb) * (int64_t)fmt_sb_bytes(fmt), e);
 }
 
 // ---- launchers ----
@@ -135,8 +131,9 @@ void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y
     hipLaunchKernelGGL(k_dequant_dev, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, fmt, w, rows, nsb, y);
 }
 void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st) {
-    const int64_t nsb = K / 256, n = (int64_t)M * nsb;
-    hipLaunchKernelGGL(k_embed, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, st, fmt, table, nsb, ids, M, h);
+    if (!table) throw BackendError("embedding table not set");
+    const int64_t nsb = K / 256;
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)M, (unsigned)nsb), dim3(256), 0, st, fmt, table, nsb, ids, h);
 }
 
 }  // namespace sd

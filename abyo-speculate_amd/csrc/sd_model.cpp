@@ -66,7 +66,10 @@ Model::~Model() {
     };
     for (auto &L : lw)
         for (auto &t : L) F(t.d);
-    for (auto &t : gw) F(t.d);
+    for (auto &t : gw) {
+        F(t.d);
+        F(t.gguf);
+    }
     for (void *p : {(void *)kv, (void *)cos_t, (void *)sin_t, (void *)h, (void *)qkv, (void *)logits,
                     (void *)hidden_out, (void *)last_row, (void *)part_o, (void *)part_ml, (void *)amax_v,
                     (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids, (void *)d_pos,
@@ -81,7 +84,7 @@ Model::~Model() {
 void Model::alloc_buffers() {
     const ModelCfg &c = cfg;
     const int Mx = c.max_batch, Mp = 128 + 16;  // padded rows (16-token MFMA tiles + last-row slack)
-    cap = (int64_t)c.ctx_len + 128;
+    cap = ((int64_t)c.ctx_len + 128 + 31) / 32 * 32;  // whole 32-position blocks of the V layout
     kv = dalloc<uint16_t>((size_t)c.n_layers * 2 * c.n_kv_heads * cap * c.head_dim);
     // RoPE tables (quantized_llama_local.rs:189-205): host f32 powf/cosf/sinf
     {
@@ -109,7 +112,7 @@ void Model::alloc_buffers() {
     ap = dalloc<uint16_t>((size_t)Mp * ap_ld);
     act = dalloc<uint16_t>((size_t)Mp * act_ld);
     q16 = dalloc<uint16_t>((size_t)c.n_heads * Mx * c.head_dim);
-    nsplit_max = 256 / c.n_kv_heads + (Mx + 63) / 64 + 2;
+    nsplit_max = attn_max_splits(c.n_kv_heads);
     part_o = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * c.head_dim);
     part_ml = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * 2);
     logits = dalloc<float>((size_t)Mx * c.vocab);
@@ -176,6 +179,10 @@ void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t by
         SD_HIP_CHECK(hipFree(t.d));
         t.d = nullptr;
     }
+    if (t.gguf) {
+        SD_HIP_CHECK(hipFree(t.gguf));
+        t.gguf = nullptr;
+    }
     if ((size_t)dev_tensor_bytes(fmt, rows, K) >= ((size_t)1 << 31))
         throw UnsupportedError("a matrix must be smaller than 2 GiB (32-bit buffer offsets)");
     if (fmt != F32 && rows % 16) throw UnsupportedError("quantised matrices need a multiple of 16 rows");
@@ -191,7 +198,8 @@ void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t by
         SD_HIP_CHECK(hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice));
         launch_gguf_to_dev(fmt, tmp, t.d, rows, K, st);
         SD_HIP_CHECK(hipStreamSynchronize(st));
-        SD_HIP_CHECK(hipFree(tmp));
+        if (kind == K_TOK_EMBD) t.gguf = tmp;
+        else SD_HIP_CHECK(hipFree(tmp));
     }
 }
 
@@ -269,6 +277,8 @@ void Model::synthesize(int mix, uint64_t seed, float stdv) {
             throw UnsupportedError("a matrix must be smaller than 2 GiB (32-bit buffer offsets)");
         if (fmt != F32 && rows % 16) throw UnsupportedError("quantised matrices need a multiple of 16 rows");
         if (t.d) SD_HIP_CHECK(hipFree(t.d));
+        if (t.gguf) SD_HIP_CHECK(hipFree(t.gguf));
+        t.d = t.gguf = nullptr;
         t.fmt = fmt;
         t.rows = rows;
         t.K = K;
@@ -285,7 +295,8 @@ void Model::synthesize(int mix, uint64_t seed, float stdv) {
             launch_synth_quant(fmt, tmp, rows, K, ts, mult, st);
             launch_gguf_to_dev(fmt, tmp, t.d, rows, K, st);
             SD_HIP_CHECK(hipStreamSynchronize(st));
-            SD_HIP_CHECK(hipFree(tmp));
+            if (kind == K_TOK_EMBD) t.gguf = tmp;
+            else SD_HIP_CHECK(hipFree(tmp));
         }
     };
     make(-1, K_TOK_EMBD);
@@ -478,9 +489,9 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     stage_done();
 
     const int H = c.hidden, QD = c.q_dim(), KVD = c.kv_dim(), QKVD = QD + 2 * KVD;
-    launch_embed(gw[K_TOK_EMBD].fmt, gw[K_TOK_EMBD].d, H, d_ids, M, h, st);
-    const int cps = attn_chunks_per_split(P, c.n_kv_heads);
-    if (attn_num_splits(P, M, cps) > nsplit_max) throw BackendError("attention split count exceeds workspace");
+    launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), H, d_ids, M, h, st);
+    const AttnSplit split = attn_split(P, M, c.n_kv_heads);
+    if (split.nsplit > nsplit_max) throw BackendError("attention split count exceeds workspace");
     for (int l = 0; l < c.n_layers; l++) {
         auto &L = lw[l];
         launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
@@ -533,7 +544,8 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             a.n_kv = c.n_kv_heads;
             a.n_rep = c.n_heads / c.n_kv_heads;
             a.hd = c.head_dim;
-            a.cps = cps;
+            a.keys_per_wave = split.keys_per_wave;
+            a.nsplit = split.nsplit;
             a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
             a.part_o = part_o;
             a.part_ml = part_ml;
@@ -656,7 +668,7 @@ void Model::embed_rows(const int *ids, int n, float *out_host) {
         std::memcpy(h_stage, ids + r0, k * sizeof(int));
         SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, k * sizeof(int), hipMemcpyHostToDevice, st));
         stage_done();
-        launch_embed(gw[K_TOK_EMBD].fmt, gw[K_TOK_EMBD].d, c.hidden, d_ids, k, hidden_out, st);
+        launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), c.hidden, d_ids, k, hidden_out, st);
         SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.hidden, hidden_out, (size_t)k * c.hidden * 4,
                                     hipMemcpyDeviceToHost, st));
         SD_HIP_CHECK(hipStreamSynchronize(st));
@@ -671,7 +683,8 @@ void Model::compact_tail(int P, const std::vector<int> &src) {
     std::memcpy(h_stage, src.data(), n * sizeof(int));
     SD_HIP_CHECK(hipMemcpyAsync(d_src, h_stage, n * sizeof(int), hipMemcpyHostToDevice, st));
     stage_done();
-    launch_keep_kv_tail(kv, cfg.n_layers * 2 * cfg.n_kv_heads, cap * cfg.head_dim, cfg.head_dim, P, d_src, n, st);
+    launch_keep_kv_tail(kv, cfg.n_layers * 2 * cfg.n_kv_heads, cap * cfg.head_dim, cfg.n_kv_heads, cfg.head_dim, P, d_src,
+                        n, st);
 }
 
 // ===========================================================================

@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include "sd_common.hpp"
 #include "sd_kernels.hpp"
 #include "sd_kernels_attn.hpp"
 #include "sd_kernels_elem.hpp"
@@ -54,6 +55,10 @@ struct DevTensor {
     int rows = 0, K = 0;
     uint8_t *d = nullptr;
     size_t bytes = 0;
+    // token_embd only: a second copy in GGUF row order, read by the embedding
+    // gather (one row's superblocks are contiguous there, while the tile
+    // layout interleaves 16 rows); HBM is plentiful, the gather is on the path
+    uint8_t *gguf = nullptr;
     bool set() const { return d != nullptr; }
 };
 
@@ -136,6 +141,8 @@ class Model {
   private:
     void alloc_buffers();
     void run_gemm(GemmParams &p, int cls, double bytes);
+    // token table in GGUF row order (F32 tables are row-major either way)
+    const uint8_t *embed_table() const { return gw[K_TOK_EMBD].fmt == F32 ? gw[K_TOK_EMBD].d : gw[K_TOK_EMBD].gguf; }
     uint16_t *kc(int layer) const { return kv + (int64_t)layer * 2 * cfg.n_kv_heads * cap * cfg.head_dim; }
     uint16_t *vc(int layer) const { return kc(layer) + (int64_t)cfg.n_kv_heads * cap * cfg.head_dim; }
 };

@@ -180,7 +180,8 @@ __global__ void k_fill_f32(float *out, int64_t n, float v) {
 }
 
 // KV rows [0, P) of every (layer, K/V, head): fp16(N(0,1)-like), value index
-// (stream << 32) | (pos * hd + d) with stream = (layer*2 + kv)*n_kv + head.
+// (stream << 32) | (pos * hd + d) with stream = (layer*2 + kv)*n_kv + head,
+// stored at the element's place in the blocked cache layout (kv_off).
 __global__ void k_fill_kv(uint16_t *kv, int L, int n_kv, int64_t cap, int hd, int P, uint64_t seed, float mult) {
     const int64_t per_stream = (int64_t)P * hd;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -188,7 +189,8 @@ __global__ void k_fill_kv(uint16_t *kv, int L, int n_kv, int64_t cap, int hd, in
     if (i >= total) return;
     const int64_t stream = i / per_stream, r = i % per_stream;
     const uint64_t idx = ((uint64_t)stream << 32) | (uint64_t)r;
-    kv[stream * cap * hd + r] = f2h(synth_value(seed, idx, mult));
+    const int which = (int)((stream / n_kv) & 1);
+    kv[stream * cap * hd + kv_off(which, r / hd, (int)(r % hd), hd)] = f2h(synth_value(seed, idx, mult));
 }
 
 // ---- exact f32 dequantisation: one thread per 32 outputs ----------------
