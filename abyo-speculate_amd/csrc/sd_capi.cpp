@@ -308,6 +308,66 @@ sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint3
     });
 }
 
+sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t k, const float *q_rows,
+                                     const float *uniforms, size_t n_uniforms, float temperature, size_t max_commit,
+                                     uint32_t *commits, size_t *n_commit, size_t *n_accepted, size_t *n_used) {
+    return guard([&] {
+        need_weights(m);
+        if ((k && (!drafts || !q_rows)) || !uniforms || !commits || !n_commit || !n_accepted || !n_used)
+            throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_rejection_linear(drafts, k, q_rows, uniforms, n_uniforms, temperature, max_commit, commits,
+                                        n_commit, n_accepted, n_used);
+    });
+}
+
+sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                   const float *q_rows, size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
+                                   const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
+                                   size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
+                                   size_t *n_used) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents || !q_row_of || !uniforms || !path || !path_len || !token || !n_used ||
+            (q_rows_n && !q_rows))
+            throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_rejection_tree(tokens, parents, n, q_rows, q_rows_n, q_vocab, q_row_of, uniforms, n_uniforms,
+                                      temperature, use_t2d, max_commit, path, path_len, token, n_used);
+    });
+}
+
+sd_status sd_set_d2t(sd_model *m, const int64_t *d2t, size_t n) {
+    return guard([&] {
+        need(m);
+        if (!d2t) throw sd::ArgError("null d2t");
+        setdev(m);
+        m->dec->set_d2t(d2t, n);
+    });
+}
+
+sd_status sd_draft_to_target(sd_model *m, const uint32_t *draft_ids, size_t n, uint32_t *out) {
+    return guard([&] {
+        need(m);
+        if ((n && (!draft_ids || !out))) throw sd::ArgError("null argument");
+        const auto &d2t = m->dec->d2t_host;
+        if (d2t.empty()) throw sd::ArgError("no d2t table (sd_set_d2t)");
+        for (size_t i = 0; i < n; i++)
+            if (draft_ids[i] >= d2t.size())
+                throw sd::SamplingError("draft id " + std::to_string(draft_ids[i]) + " out of range (" +
+                                        std::to_string(d2t.size()) + ")");
+        for (size_t i = 0; i < n; i++) out[i] = (uint32_t)d2t[draft_ids[i]];
+    });
+}
+
+size_t sd_t2d_mask(const sd_model *m, uint8_t *out, size_t cap) {
+    if (!m || !m->dec || m->dec->t2d_host.empty()) return 0;
+    const auto &inv = m->dec->t2d_host;
+    const size_t n = std::min(cap, inv.size());
+    for (size_t i = 0; i < n && out; i++) out[i] = inv[i] >= 0 ? 1 : 0;
+    return inv.size();
+}
+
 sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n) {
     return guard([&] {
         need(m);

@@ -73,7 +73,9 @@ Model::~Model() {
     for (void *p : {(void *)kv, (void *)cos_t, (void *)sin_t, (void *)h, (void *)qkv, (void *)logits,
                     (void *)hidden_out, (void *)last_row, (void *)part_o, (void *)part_ml, (void *)amax_v,
                     (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids, (void *)d_pos,
-                    (void *)d_src, (void *)d_mask, (void *)xp, (void *)ap, (void *)act, (void *)q16})
+                    (void *)d_src, (void *)d_mask, (void *)xp, (void *)ap, (void *)act, (void *)q16,
+                    (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
+                    (void *)acc_out, (void *)t2d_inv})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -127,6 +129,12 @@ void Model::alloc_buffers() {
     d_pos = dalloc<int>(Mx);
     d_src = dalloc<int>(Mx);
     d_mask = dalloc<uint64_t>((size_t)Mx * 2);
+    acc_m = dalloc<float>(Mx);
+    acc_s = dalloc<float>(Mx);
+    acc_am = dalloc<int>(Mx);
+    acc_u = dalloc<float>(Mx);
+    acc_tree = dalloc<int>((size_t)3 * Mx);
+    acc_out = dalloc<int>((size_t)Mx + 4);
     h_stage_bytes = (size_t)Mx * (3 * sizeof(int) + 2 * sizeof(uint64_t)) + 256;
     SD_HIP_CHECK(hipHostMalloc((void **)&h_stage, h_stage_bytes, hipHostMallocDefault));
     SD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev, hipEventDisableTiming));
@@ -1073,6 +1081,168 @@ void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents
                 *bonus_node = (int32_t)c;
                 break;
             }
+}
+
+// ---- rejection sampling ------------------------------------------------------
+// EAGLE-3's d2t table (eagle3.rs:377-397): draft id -> absolute target id;
+// entries outside [0, vocab) are ignored; the inverse keeps the last writer.
+void Decoder::set_d2t(const int64_t *d2t, size_t n) {
+    Model &m = *model;
+    if (n == 0 || n > (size_t)INT32_MAX) throw ArgError("d2t: size out of range");
+    std::vector<int32_t> inv((size_t)m.cfg.vocab, -1);
+    for (size_t i = 0; i < n; i++)
+        if (d2t[i] >= 0 && d2t[i] < m.cfg.vocab) inv[(size_t)d2t[i]] = (int32_t)i;
+    SD_HIP_CHECK(hipSetDevice(m.cfg.device));
+    if (!m.t2d_inv) SD_HIP_CHECK(hipMalloc((void **)&m.t2d_inv, (size_t)m.cfg.vocab * sizeof(int) + 256));
+    SD_HIP_CHECK(hipMemcpyAsync(m.t2d_inv, inv.data(), inv.size() * sizeof(int), hipMemcpyHostToDevice, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    d2t_host.assign(d2t, d2t + n);
+    t2d_host = std::move(inv);
+    m.d2t_draft_vocab = (int)n;
+}
+
+void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
+                          size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature,
+                          int use_t2d, size_t max_commit, std::vector<int> &path, int &fin, size_t &used) {
+    Model &m = *model;
+    const ModelCfg &c = m.cfg;
+    if (m.logits_rows_last < n) throw BackendError("acceptance: fewer logits rows than tree nodes");
+    const size_t qn = q_rows_n * q_vocab;
+    if (qn > m.acc_q_cap) {
+        if (m.acc_q) SD_HIP_CHECK(hipFree(m.acc_q));
+        m.acc_q = nullptr;
+        m.acc_q_cap = 0;
+        SD_HIP_CHECK(hipMalloc((void **)&m.acc_q, qn * sizeof(float) + 256));
+        m.acc_q_cap = qn;
+    }
+    // parents | tokens | q_row_of, uniforms and draft rows: one copy each
+    std::vector<int> tree((size_t)3 * n);
+    std::memcpy(tree.data(), parents, n * sizeof(int));
+    std::memcpy(tree.data() + n, tokens, n * sizeof(int));
+    std::memcpy(tree.data() + 2 * n, q_row_of, n * sizeof(int));
+    SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, tree.data(), tree.size() * sizeof(int), hipMemcpyHostToDevice, m.st));
+    SD_HIP_CHECK(hipMemcpyAsync(m.acc_u, uniforms, n * sizeof(float), hipMemcpyHostToDevice, m.st));
+    if (qn) SD_HIP_CHECK(hipMemcpyAsync(m.acc_q, q_rows, qn * sizeof(float), hipMemcpyHostToDevice, m.st));
+    const bool greedy = temperature == 0.f;
+    const float inv_t = greedy ? 1.f : 1.0f / temperature;
+    const int *mask = use_t2d ? m.t2d_inv : nullptr;
+    launch_row_stats(m.logits, c.vocab, c.vocab, n, inv_t, mask, m.acc_m, m.acc_s, m.acc_am, m.st);
+    AcceptParams a{};
+    a.logits = m.logits;
+    a.ld = c.vocab;
+    a.V = c.vocab;
+    a.n = n;
+    a.parents = m.acc_tree;
+    a.tokens = m.acc_tree + n;
+    a.q_row_of = m.acc_tree + 2 * n;
+    a.row_m = m.acc_m;
+    a.row_s = m.acc_s;
+    a.row_am = m.acc_am;
+    a.inv_t = inv_t;
+    a.greedy = greedy ? 1 : 0;
+    a.t2d_inv = mask;
+    a.q = m.acc_q;
+    a.q_ld = (int64_t)q_vocab;
+    a.q_map = q_vocab == (size_t)c.vocab ? nullptr : m.t2d_inv;
+    a.uniforms = m.acc_u;
+    a.max_commit = (int)max_commit;
+    a.out_path = m.acc_out + 4;
+    a.out_info = m.acc_out;
+    launch_accept_walk(a, m.st);
+    std::vector<int> out((size_t)n + 4);
+    SD_HIP_CHECK(hipMemcpyAsync(out.data(), m.acc_out, out.size() * sizeof(int), hipMemcpyDeviceToHost, m.st));
+    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    const int status = out[3];
+    if (status == ACC_ERR_SOFTMAX) throw SamplingError("softmax produced a non-positive or non-finite sum");
+    if (status == ACC_ERR_ADJUSTED) throw SamplingError("adjusted distribution has non-positive mass");
+    if (status != ACC_OK) throw SamplingError("acceptance walk: too many rejections at one node");
+    const int plen = out[0];
+    if (plen < 1 || plen > n) throw BackendError("acceptance walk: bad path length");
+    path.assign(out.begin() + 4, out.begin() + 4 + plen);
+    fin = out[1];
+    used = (size_t)out[2];
+}
+
+static void check_temperature(float t) {
+    // softmax_with_temperature rejects these (tokens.rs:19-23)
+    if (!std::isfinite(t) || t < 0.f) throw SamplingError("invalid temperature");
+}
+
+void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const float *q_rows, const float *uniforms,
+                                      size_t n_uniforms, float temperature, size_t max_commit, uint32_t *commits,
+                                      size_t *n_commit, size_t *n_accepted, size_t *n_used) {
+    Model &m = *model;
+    check_temperature(temperature);
+    if (n_uniforms < k + 1) throw ArgError("rejection verify needs k + 1 uniforms");
+    if (k + 1 > (size_t)m.cfg.max_batch) throw ArgError("too many draft tokens for one verify pass");
+    if (history.empty()) throw SamplingError("batched_logits with empty history");
+    const uint32_t last = history.back();
+    batched_logits(drafts, k, nullptr);
+    if (k == 0) {
+        // next_logits left the row in last_row; the walk reads logits row 0
+        SD_HIP_CHECK(hipMemcpyAsync(m.logits, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToDevice, m.st));
+        m.logits_rows_last = 1;
+    }
+    const int n = (int)k + 1;
+    std::vector<int> parents(n), tokens(n), qrow(n);
+    for (int i = 0; i < n; i++) {
+        parents[i] = i - 1;
+        tokens[i] = (int)(i == 0 ? last : drafts[i - 1]);
+        qrow[i] = i < (int)k ? i : -1;
+    }
+    parents[0] = 0;
+    std::vector<int> path;
+    int fin;
+    size_t used;
+    accept_walk(parents.data(), tokens.data(), n, q_rows, k, m.cfg.vocab, qrow.data(), uniforms, temperature, 0,
+                max_commit, path, fin, used);
+    size_t nc = 0;
+    for (size_t i = 1; i < path.size(); i++) commits[nc++] = (uint32_t)tokens[path[i]];
+    if (fin >= 0) commits[nc++] = (uint32_t)fin;
+    *n_commit = nc;
+    *n_accepted = path.size() - 1;
+    *n_used = used;
+}
+
+void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *q_rows,
+                                    size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
+                                    const float *uniforms, size_t n_uniforms, float temperature, int use_t2d,
+                                    size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
+                                    size_t *n_used) {
+    Model &m = *model;
+    check_temperature(temperature);
+    if (history.empty()) throw SamplingError("tree_logits with empty history");
+    const DraftTreeC t = DraftTreeC::from_arrays(tokens, parents, n);
+    if (n_uniforms < n) throw ArgError("rejection verify needs one uniform per tree node");
+    if (q_vocab != (size_t)m.cfg.vocab && (q_vocab != (size_t)m.d2t_draft_vocab || !m.t2d_inv))
+        throw ArgError("draft rows must span the target vocabulary, or the d2t draft vocabulary after sd_set_d2t");
+    if (use_t2d && !m.t2d_inv) throw ArgError("t2d masking needs sd_set_d2t");
+    std::vector<bool> has_child(n, false);
+    std::vector<int> nchild(n, 0);
+    for (size_t i = 1; i < n; i++) {
+        has_child[t.parents[i]] = true;
+        if (++nchild[t.parents[i]] > 16) throw UnsupportedError("rejection walk: at most 16 children per node");
+    }
+    for (size_t i = 0; i < n; i++) {
+        if (has_child[i] && (q_row_of[i] < 0 || (size_t)q_row_of[i] >= q_rows_n))
+            throw ArgError("every node with children needs a draft row");
+    }
+    tree_logits_keep_kv(tokens, parents, n, nullptr, nullptr);
+    std::vector<int> par(n), tok(n), qr(n);
+    for (size_t i = 0; i < n; i++) {
+        par[i] = (int)t.parents[i];
+        tok[i] = (int)tokens[i];
+        qr[i] = has_child[i] ? q_row_of[i] : -1;
+    }
+    std::vector<int> p;
+    int fin;
+    size_t used;
+    accept_walk(par.data(), tok.data(), (int)n, q_rows, q_rows_n, q_vocab, qr.data(), uniforms, temperature, use_t2d,
+                max_commit, p, fin, used);
+    for (size_t i = 0; i < p.size(); i++) path[i] = (uint32_t)p[i];
+    *path_len = p.size();
+    *token = fin;
+    *n_used = used;
 }
 
 void Decoder::prime_synthetic(const uint32_t *ids, size_t n, uint64_t kv_seed) {

@@ -12,6 +12,7 @@
 #include "sd_common.hpp"
 #include "sd_kernels.hpp"
 #include "sd_kernels_attn.hpp"
+#include "sd_kernels_accept.hpp"
 #include "sd_kernels_elem.hpp"
 
 namespace sd {
@@ -126,6 +127,14 @@ class Model {
     float *part_o = nullptr, *part_ml = nullptr, *amax_v = nullptr, *collect_buf = nullptr;
     int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
     uint64_t *d_mask = nullptr;
+    // rejection-sampling acceptance: per-row softmax statistics, the tree,
+    // draft rows, uniforms and results (draft rows grow on demand)
+    float *acc_m = nullptr, *acc_s = nullptr, *acc_u = nullptr, *acc_q = nullptr;
+    size_t acc_q_cap = 0;  // floats
+    int *acc_am = nullptr, *acc_tree = nullptr, *acc_out = nullptr;
+    // d2t map of an EAGLE-3 draft (eagle3.rs:377-397): target id -> draft id or -1
+    int *t2d_inv = nullptr;
+    int d2t_draft_vocab = 0;
     uint16_t *xp = nullptr, *ap = nullptr, *act = nullptr, *q16 = nullptr;
     int xp_ld = 0, ap_ld = 0, act_ld = 0;
     int amax_ld = 0;
@@ -177,12 +186,29 @@ class Decoder {
     void verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, int strict,
                             uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node);
     void argmax_rows(int32_t *out, size_t n);
+    // batched_logits + the rejection walk of vanilla.rs:178-210 on the device
+    void verify_rejection_linear(const uint32_t *drafts, size_t k, const float *q_rows, const float *uniforms,
+                                 size_t n_uniforms, float temperature, size_t max_commit, uint32_t *commits,
+                                 size_t *n_commit, size_t *n_accepted, size_t *n_used);
+    // tree_logits_keep_kv + the tree rejection walk (sd_accept.hip)
+    void verify_rejection_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *q_rows,
+                               size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of, const float *uniforms,
+                               size_t n_uniforms, float temperature, int use_t2d, size_t max_commit, uint32_t *path,
+                               size_t *path_len, int32_t *token, size_t *n_used);
+    // EAGLE-3 vocabulary map (eagle3.rs:377-397, 476-513)
+    void set_d2t(const int64_t *d2t, size_t n);
+    std::vector<int64_t> d2t_host;
+    std::vector<int32_t> t2d_host;  // target id -> draft id or -1 (last writer wins, like the HashMap insert)
 
     // sets history and KV [0, n) to synthetic values (benchmarks, full-size tests)
     void prime_synthetic(const uint32_t *ids, size_t n, uint64_t kv_seed);
 
   private:
     void forward_advance(const uint32_t *tokens, size_t n, bool all_rows);
+    // the acceptance walk over logits rows [0, n) of the last pass
+    void accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
+                     size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature, int use_t2d,
+                     size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
     void truncate(size_t len);
     void tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden, int &prefix);
 };

@@ -137,6 +137,12 @@ def load_library(path: str = LIB_PATH):
         "sd_verify_greedy_linear": ([P, P, SZ, P, pSZ, pSZ], I32),
         "sd_verify_greedy_tree": ([P, P, P, SZ, I32, P, pSZ, P, P], I32),
         "sd_last_argmax": ([P, P, SZ], I32),
+        "sd_verify_rejection_linear": ([P, P, SZ, P, P, SZ, ctypes.c_float, SZ, P, pSZ, pSZ, pSZ], I32),
+        "sd_verify_rejection_tree": ([P, P, P, SZ, P, SZ, SZ, P, P, SZ, ctypes.c_float, I32, SZ, P, pSZ, P, pSZ],
+                                     I32),
+        "sd_set_d2t": ([P, P, SZ], I32),
+        "sd_draft_to_target": ([P, P, SZ, P], I32),
+        "sd_t2d_mask": ([P, P, SZ], SZ),
         "sd_prime_synthetic": ([P, P, SZ, U64], I32),
         "sd_profile_enable": ([P, I32], I32),
         "sd_profile_read": ([P, P, P, P, SZ], SZ),
@@ -359,6 +365,58 @@ class HipQuantDecoder:
         _check(_lib.sd_verify_greedy_tree(self._h, _ptr(t), _ptr(p), t.size, 1 if strict else 0, _ptr(path),
                                           ctypes.byref(plen), ctypes.byref(bonus), ctypes.byref(bnode)))
         return [int(v) for v in path[:plen.value]], int(bonus.value), int(bnode.value)
+
+    def verify_rejection_linear(self, drafts: Sequence[int], q_rows: np.ndarray, uniforms: Sequence[float],
+                                temperature: float, max_commit: int = 0):
+        """-> (commits, n_accepted, uniforms_used)."""
+        d = _u32(drafts)
+        q = np.ascontiguousarray(q_rows, np.float32)
+        if d.size and q.shape != (d.size, self.cfg.vocab):
+            raise ValueError("q_rows must be [k][vocab]")
+        u = np.ascontiguousarray(uniforms, np.float32)
+        commits = np.empty(d.size + 1, np.uint32)
+        nc, na, nu = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(_lib.sd_verify_rejection_linear(self._h, _ptr(d), d.size, _ptr(q), _ptr(u), u.size,
+                                               float(temperature), max_commit, _ptr(commits), ctypes.byref(nc),
+                                               ctypes.byref(na), ctypes.byref(nu)))
+        return [int(v) for v in commits[:nc.value]], int(na.value), int(nu.value)
+
+    def verify_rejection_tree(self, tree, q_rows: np.ndarray, q_row_of: Sequence[int], uniforms: Sequence[float],
+                              temperature: float, use_t2d: bool = False, max_commit: int = 0):
+        """-> (path node indices, final token or -1, uniforms_used)."""
+        t, p = tree_arrays(tree)
+        q = np.ascontiguousarray(q_rows, np.float32)
+        if q.ndim != 2:
+            raise ValueError("q_rows must be 2-D")
+        qr = np.ascontiguousarray(q_row_of, np.int32)
+        if qr.size != t.size:
+            raise ValueError("q_row_of needs one entry per node")
+        u = np.ascontiguousarray(uniforms, np.float32)
+        path = np.empty(t.size, np.uint32)
+        plen, nu = ctypes.c_size_t(), ctypes.c_size_t()
+        tok = ctypes.c_int32()
+        _check(_lib.sd_verify_rejection_tree(self._h, _ptr(t), _ptr(p), t.size, _ptr(q), q.shape[0], q.shape[1],
+                                             _ptr(qr), _ptr(u), u.size, float(temperature), 1 if use_t2d else 0,
+                                             max_commit, _ptr(path), ctypes.byref(plen), ctypes.byref(tok),
+                                             ctypes.byref(nu)))
+        return [int(v) for v in path[:plen.value]], int(tok.value), int(nu.value)
+
+    def set_d2t(self, d2t: Sequence[int]):
+        a = np.ascontiguousarray(d2t, np.int64)
+        _check(_lib.sd_set_d2t(self._h, _ptr(a), a.size))
+
+    def draft_to_target(self, ids: Sequence[int]):
+        a = _u32(ids)
+        out = np.empty(a.size, np.uint32)
+        _check(_lib.sd_draft_to_target(self._h, _ptr(a), a.size, _ptr(out)))
+        return [int(v) for v in out]
+
+    def t2d_mask(self) -> np.ndarray:
+        n = _lib.sd_t2d_mask(self._h, None, 0)
+        out = np.zeros(n, np.uint8)
+        if n:
+            _lib.sd_t2d_mask(self._h, _ptr(out), n)
+        return out.astype(bool)
 
     def last_argmax(self, n: int) -> np.ndarray:
         out = np.empty(n, np.int32)

@@ -185,6 +185,52 @@ sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint3
 /* First-max argmax of each row of the last verify pass (eagle.rs:626-637 fold). */
 sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n);
 
+/* batched_logits + the rejection-sampling walk of run_vanilla_sd
+ * (methods/vanilla.rs:178-210) on the device: for draft i, p = softmax of row i
+ * at `temperature` (sampling/tokens.rs:15-55), q = q_rows[i][drafts[i]];
+ * accept iff q <= 0 or uniforms[used++] <= min(1, p/q) (vanilla.rs:59-73); on
+ * the first rejection one token is drawn with uniforms[used++] from
+ * max(0, p - q_rows[i]) renormalised (vanilla.rs:83-106, tokens.rs:99-120)
+ * and the walk stops; after k accepted drafts the bonus is drawn from row k.
+ * max_commit (0 = none) stops after that many accepted drafts with no final
+ * draw (the max_new_tokens checks of vanilla.rs:190, 206).  q_rows [k][vocab]
+ * and uniforms (>= k + 1 values) are host arrays; commits has room for k + 1.
+ * State afterwards is that of sd_batched_logits; the caller re-anchors with
+ * sd_rollback_to(len + n_accepted) + sd_observe(commits + n_accepted)
+ * (vanilla.rs:219-223).  SD_ERR_SAMPLING for the reference's softmax /
+ * adjusted-distribution errors and invalid temperatures. */
+sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t k, const float *q_rows,
+                                     const float *uniforms, size_t n_uniforms, float temperature, size_t max_commit,
+                                     uint32_t *commits, size_t *n_commit, size_t *n_accepted, size_t *n_used);
+/* tree_logits_keep_kv + rejection sampling over the tree.  The reference has no
+ * tree rejection rule (run_eagle / run_eagle3 ignore the temperature,
+ * eagle.rs:739-740, eagle3.rs:789); this one reduces to the linear walk above
+ * on a chain: the children of a node are tested in BFS order with the rule of
+ * vanilla.rs:59-73 against the node's current distribution p (softmax of its
+ * row) and its draft row q = q_rows[q_row_of[node]]; a rejection replaces p by
+ * max(0, p - q) renormalised before the next sibling is tested; if no child is
+ * accepted the final token is drawn from the current p, after a leaf from the
+ * leaf's row.  q_rows has q_rows_n rows of q_vocab entries: q_vocab = vocab
+ * (target ids) or the draft vocabulary of sd_set_d2t (target id x reads entry
+ * t2d(x), 0 where unreachable).  use_t2d masks target entries unreachable
+ * through d2t to -inf first (mask_target_logits, eagle3.rs:498-513).
+ * uniforms: >= n values.  path receives the accepted node indices from the
+ * root (room for n), token the final draw or -1 (max_commit reached). */
+sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                   const float *q_rows, size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
+                                   const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
+                                   size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
+                                   size_t *n_used);
+/* EAGLE-3 vocabulary map (Eagle3DraftCandle's d2t, eagle3.rs:377-397): d2t[draft id]
+ * = absolute target id; entries outside [0, vocab) are skipped; the inverse
+ * keeps the last draft id of a target id (HashMap::insert). */
+sd_status sd_set_d2t(sd_model *m, const int64_t *d2t, size_t n);
+/* draft_to_target_token (eagle3.rs:476-484): SD_ERR_SAMPLING for an id past the table. */
+sd_status sd_draft_to_target(sd_model *m, const uint32_t *draft_ids, size_t n, uint32_t *out);
+/* t2d_mask (eagle3.rs:495-497): out[i] = 1 iff target id i is reachable; returns
+ * the mask length (vocab), 0 without a d2t table; copies min(cap, vocab). */
+size_t sd_t2d_mask(const sd_model *m, uint8_t *out, size_t cap);
+
 /* ---- synthetic state and measurement ---------------------------------------- */
 /* Sets history = ids and fills KV rows [0, n) with seeded N(0,1)-like fp16
  * values; the next-token logits cache is invalid afterwards. */

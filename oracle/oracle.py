@@ -749,6 +749,56 @@ def rejection_linear_accept(target_rows: Sequence[np.ndarray], q_rows: Sequence[
     return commits, n_acc, used
 
 
+def rejection_tree_accept(tree: "DraftTree", target_rows: Sequence[np.ndarray], q_rows: Sequence[np.ndarray],
+                          q_row_of: Sequence[int], uniforms: Sequence[float], temperature: float,
+                          t2d_mask: Optional[np.ndarray] = None, max_commit: Optional[int] = None):
+    """Tree rejection walk (a build extension: the reference has no tree rule,
+    eagle.rs:739-740 and eagle3.rs:789 ignore the temperature), made of the
+    reference's own steps: at the current node, children are tested in BFS
+    order with modified_rejection_step (vanilla.rs:59-73) against the node's
+    current distribution p (softmax_with_temperature of its row, tokens.rs:15-55)
+    and its draft row q = q_rows[q_row_of[node]] (target vocabulary); each
+    rejection sets p = adjusted_distribution(p, q) (vanilla.rs:83-106); the first
+    accepted child is descended into; with no child left the final token is
+    sample_from_distribution(p) (tokens.rs:99-120).  On a chain this is exactly
+    rejection_linear_accept.  t2d_mask (eagle3.rs:498-513) sets unreachable
+    target logits to -inf first.
+
+    Returns (path node indices, final token or None, uniforms used).
+    """
+    n = len(tree)
+    children = [[] for _ in range(n)]
+    for c in range(1, n):
+        children[tree.parent_of(c)].append(c)
+    used = 0
+    node = 0
+    path = [0]
+    while True:
+        if max_commit is not None and max_commit > 0 and len(path) - 1 >= max_commit:
+            return path, None, used
+        row = np.array(target_rows[node], np.float32)
+        if t2d_mask is not None:
+            row[~t2d_mask] = -np.inf
+        p = softmax_t(row, temperature)
+        accepted = None
+        for c in children[node]:
+            q = np.asarray(q_rows[q_row_of[node]], np.float32)
+            tok = tree.token_at(c)
+            u = uniforms[used]
+            used += 1
+            if rejection_step(float(q[tok]), float(p[tok]), u):
+                accepted = c
+                break
+            p = adjusted_distribution(p, q)
+        if accepted is not None:
+            path.append(accepted)
+            node = accepted
+            continue
+        tok = sample_u(p, uniforms[used])
+        used += 1
+        return path, tok, used
+
+
 def d2t_maps(d2t: Sequence[int], target_vocab: int):
     """eagle3.rs:386-397 -> (target_to_draft dict, t2d mask)."""
     t2d = np.zeros(target_vocab, bool)
