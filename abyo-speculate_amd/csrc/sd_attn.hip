@@ -33,6 +33,19 @@ namespace sd {
 #pragma clang fp contract(off)
 
 // ---- RoPE + KV append ------------------------------------------------------
+// projection output (m, col): the matmul's value, or its K-slice partials
+// added in slice order plus the bias
+__device__ __forceinline__ float qkv_at(const RopeKvParams &p, int m, int col) {
+    const int64_t at = (int64_t)m * p.ld_qkv + col;
+    if (p.nks <= 1) return p.qkv[at];
+    const int64_t stride = (int64_t)p.M * p.ld_qkv;
+    float v = p.part[at];
+    for (int k = 1; k < p.nks; k++) v += p.part[at + k * stride];
+    if (!p.bq) return v;
+    const int qd = p.n_heads * p.hd, kvd = p.n_kv * p.hd;
+    return v + (col < qd ? p.bq[col] : col < qd + kvd ? p.bk[col - qd] : p.bv[col - qd - kvd]);
+}
+
 // grid (M, n_heads + n_kv), block hd/2 threads
 __global__ void k_rope_kv(RopeKvParams p) {
     const int m = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
@@ -40,7 +53,6 @@ __global__ void k_rope_kv(RopeKvParams p) {
     if (i >= half) return;
     const int pos = p.pos[m];
     const float c = p.cos_t[(int64_t)pos * half + i], s = p.sin_t[(int64_t)pos * half + i];
-    const float *row = p.qkv + (int64_t)m * p.ld_qkv;
     int a, b;  // element pair
     if (p.interleaved) {
         a = 2 * i;
@@ -50,22 +62,21 @@ __global__ void k_rope_kv(RopeKvParams p) {
         b = i + half;
     }
     if (hh < p.n_heads) {
-        const float *x = row + hh * p.hd;
-        const float x0 = x[a], x1 = x[b];
+        const int c0 = hh * p.hd;
+        const float x0 = qkv_at(p, m, c0 + a), x1 = qkv_at(p, m, c0 + b);
         uint16_t *q = p.q16 + ((int64_t)hh * p.M + m) * p.hd;
         q[a] = f2h(x0 * c - x1 * s);
         q[b] = f2h(x0 * s + x1 * c);
     } else {
         const int h = hh - p.n_heads;
-        const float *xk = row + p.n_heads * p.hd + h * p.hd;
-        const float *xv = row + (p.n_heads + p.n_kv) * p.hd + h * p.hd;
+        const int ck = p.n_heads * p.hd + h * p.hd, cv = (p.n_heads + p.n_kv) * p.hd + h * p.hd;
         uint16_t *ks = p.kc + (int64_t)h * p.cap * p.hd, *vs = p.vc + (int64_t)h * p.cap * p.hd;
         const int64_t t = p.P + m;
-        const float k0 = xk[a], k1 = xk[b];
+        const float k0 = qkv_at(p, m, ck + a), k1 = qkv_at(p, m, ck + b);
         ks[kv_k_off(t, a, p.hd)] = f2h(k0 * c - k1 * s);
         ks[kv_k_off(t, b, p.hd)] = f2h(k0 * s + k1 * c);
-        vs[kv_v_off(t, a, p.hd)] = f2h(xv[a]);
-        vs[kv_v_off(t, b, p.hd)] = f2h(xv[b]);
+        vs[kv_v_off(t, a, p.hd)] = f2h(qkv_at(p, m, cv + a));
+        vs[kv_v_off(t, b, p.hd)] = f2h(qkv_at(p, m, cv + b));
     }
 }
 

@@ -16,17 +16,35 @@ namespace sd {
 // One workgroup (256 threads) per row.  Each thread keeps its K/256 values in
 // registers (vector loads, all issued before the first use), so the row is
 // read from memory once and there is one memory round trip, not K/256 of them.
+// With nks > 1 the residual matmul that produced x left K-slice partial sums
+// part[ks][M][K]: they are added to x in slice order first (and x is stored).
 template <int NV>  // float4 vectors per thread: K = 1024 * NV
-__global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *w, int K, float eps, uint16_t *out16,
-                                                 int ld16, float *out32) {
+__global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K, float eps, uint16_t *out16,
+                                                 int ld16, float *out32, const float *part, int nks,
+                                                 int64_t pstride) {
     const int m = blockIdx.x, t = threadIdx.x;
-    const float4 *row = (const float4 *)(x + (int64_t)m * K);
+    float4 *row = (float4 *)(x + (int64_t)m * K);
     const float4 *wv = (const float4 *)w;
     float4 v[NV], wr[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) v[i] = row[t + 256 * i];
 #pragma unroll
     for (int i = 0; i < NV; i++) wr[i] = wv[t + 256 * i];
+    if (nks > 1) {
+        for (int k = 0; k < nks; k++) {
+            const float4 *pr = (const float4 *)(part + k * pstride + (int64_t)m * K);
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const float4 a = pr[t + 256 * i];
+                v[i].x += a.x;
+                v[i].y += a.y;
+                v[i].z += a.z;
+                v[i].w += a.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) row[t + 256 * i] = v[i];
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
@@ -55,10 +73,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *w,
 }
 
 // generic K (multiple of 4): strided loop
-__global__ __launch_bounds__(256) void k_rmsnorm_any(const float *x, const float *w, int K, float eps, uint16_t *out16,
-                                                     int ld16, float *out32) {
+__global__ __launch_bounds__(256) void k_rmsnorm_any(float *x, const float *w, int K, float eps, uint16_t *out16,
+                                                     int ld16, float *out32, const float *part, int nks,
+                                                     int64_t pstride) {
     const int m = blockIdx.x;
-    const float *row = x + (int64_t)m * K;
+    float *row = x + (int64_t)m * K;
+    if (nks > 1) {
+        for (int k = threadIdx.x; k < K; k += 256) {
+            float v = row[k];
+            for (int s = 0; s < nks; s++) v += part[s * pstride + (int64_t)m * K + k];
+            row[k] = v;
+        }
+        __syncthreads();
+    }
     float ss = 0.f;
     for (int k = threadIdx.x; k < K; k += 256) ss += row[k] * row[k];
     __shared__ float red[256];
@@ -180,18 +207,20 @@ __global__ __launch_bounds__(256) void k_keep_kv_tail(uint16_t *kv, int64_t stre
 }
 
 // ---- launchers ----
-void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
-                    hipStream_t st) {
+void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
+                    hipStream_t st, const float *part, int nks) {
+    const int64_t ps = (int64_t)M * K;
+#define SD_RMS(KERN) hipLaunchKernelGGL(KERN, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32, part, nks, ps)
     switch (K) {
-    case 512: hipLaunchKernelGGL(k_rmsnorm_any, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 1024: hipLaunchKernelGGL(k_rmsnorm<1>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 2048: hipLaunchKernelGGL(k_rmsnorm<2>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 3072: hipLaunchKernelGGL(k_rmsnorm<3>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 4096: hipLaunchKernelGGL(k_rmsnorm<4>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 5120: hipLaunchKernelGGL(k_rmsnorm<5>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    case 8192: hipLaunchKernelGGL(k_rmsnorm<8>, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
-    default: hipLaunchKernelGGL(k_rmsnorm_any, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32); break;
+    case 1024: SD_RMS(k_rmsnorm<1>); break;
+    case 2048: SD_RMS(k_rmsnorm<2>); break;
+    case 3072: SD_RMS(k_rmsnorm<3>); break;
+    case 4096: SD_RMS(k_rmsnorm<4>); break;
+    case 5120: SD_RMS(k_rmsnorm<5>); break;
+    case 8192: SD_RMS(k_rmsnorm<8>); break;
+    default: SD_RMS(k_rmsnorm_any); break;
     }
+#undef SD_RMS
 }
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st) {
     hipLaunchKernelGGL(k_to_frag16, dim3((K + 255) / 256, M), dim3(256), 0, st, x, K, out16, ld16);

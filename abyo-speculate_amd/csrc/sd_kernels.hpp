@@ -51,11 +51,18 @@ struct GemmParams {
     float *amax_v;           // GM_LOGITS: per (token, workgroup) argmax partials
     int *amax_i;
     int amax_ld;             // = number of workgroups
+    // M > 16 only: with allow_split (GM_STORE / GM_RESID) the launch may split
+    // K into qgemm_slices(p) slices and then writes partial sums
+    // part[ks][M][ntiles * 16] instead of the output; the caller adds them.
+    int allow_split;
+    float *part;
+    int64_t part_cap;        // floats
 };
 
 // Launches y = x . W^T over all segments.  Chooses the tile shape from M.
 // Returns the number of workgroups launched (GM_LOGITS partial count).
 int launch_qgemm(const GemmParams &p, hipStream_t st);
 int qgemm_workgroups(const GemmParams &p);
+int qgemm_slices(const GemmParams &p);  // 1 when the output is written directly
 
 }  // namespace sd

@@ -14,6 +14,11 @@ struct RopeKvParams {
     int64_t cap;
     int P, M, n_heads, n_kv, hd;
     int interleaved;    // 1: rope_i pairs (2i, 2i+1) (Llama); 0: rope pairs (i, i+hd/2) (Qwen2)
+    // nks > 1: the QKV matmul left K-slice partial sums part[ks][M][ld_qkv]
+    // (no bias) instead of qkv; they are added in slice order, then the bias
+    const float *part;
+    int nks;
+    const float *bq, *bk, *bv;  // QKV biases (Qwen2) or null
 };
 
 // Work split of one attention call, a function of the prefix length P and the

@@ -10,8 +10,10 @@ namespace sd {
 // are dequantised on the fly, so no f32 copy of the table is kept)
 void launch_dequant_dev(int fmt, const uint8_t *w, int64_t rows, int K, float *y, hipStream_t st);
 void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, float *h, hipStream_t st);
-void launch_rmsnorm(const float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
-                    hipStream_t st);
+// x: [M][K]; with nks > 1, part[ks][M][K] (K-slice partial sums of the
+// residual matmul that produced x) are first added to x in slice order.
+void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
+                    hipStream_t st, const float *part = nullptr, int nks = 1);
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st);
 void launch_argmax_reduce(const float *pv, const int *pi, int nwg, int M, int *out, hipStream_t st);
 void launch_argmax_rows(const float *x, int64_t ld, int n, int M, int *out, hipStream_t st);

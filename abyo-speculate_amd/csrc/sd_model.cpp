@@ -75,7 +75,7 @@ Model::~Model() {
                     (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids, (void *)d_pos,
                     (void *)d_src, (void *)d_mask, (void *)xp, (void *)ap, (void *)act, (void *)q16,
                     (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
-                    (void *)acc_out, (void *)t2d_inv})
+                    (void *)acc_out, (void *)t2d_inv, (void *)qg_part})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -129,6 +129,8 @@ void Model::alloc_buffers() {
     d_pos = dalloc<int>(Mx);
     d_src = dalloc<int>(Mx);
     d_mask = dalloc<uint64_t>((size_t)Mx * 2);
+    qg_part_cap = std::max<int64_t>((int64_t)8 * Mx * std::max(qkvd, c.hidden), (int64_t)2 * Mx * 2 * c.ffn);
+    qg_part = dalloc<float>((size_t)qg_part_cap);
     acc_m = dalloc<float>(Mx);
     acc_s = dalloc<float>(Mx);
     acc_am = dalloc<int>(Mx);
@@ -396,6 +398,7 @@ void Model::qmatmul(int layer, int kind, const float *x, int M, float *y) {
     SD_HIP_CHECK(hipMemcpy(dx, x, (size_t)M * t.K * 4, hipMemcpyHostToDevice));
     launch_to_frag16(dx, M, t.K, dxp, t.K, st);
     GemmParams p{};
+    gemm_workspace(p);
     p.seg[0] = seg_of(t, 0, dy, t.rows, 0, nullptr);
     p.nseg = 1;
     p.ntiles = t.rows / 16;
@@ -422,6 +425,7 @@ double Model::bench_qmatmul(int layer, int kind, int M, int iters, double *bytes
     SD_HIP_CHECK(hipSetDevice(cfg.device));
     auto &L = lw[layer < 0 ? 0 : layer];
     GemmParams p{};
+    gemm_workspace(p);
     p.xp = xp;
     p.M = M;
     double wb = 0.0;
@@ -500,11 +504,18 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), H, d_ids, M, h, st);
     const AttnSplit split = attn_split(P, M, c.n_kv_heads);
     if (split.nsplit > nsplit_max) throw BackendError("attention split count exceeds workspace");
+    // M > 16 matmuls may leave K-slice partial sums in qg_part for the next
+    // kernel to add (rope for QKV, the following RMSNorm for the residual
+    // matmuls); not while per-layer hidden states are collected
+    const int split_ok = collect.empty() ? 1 : 0;
+    int pend = 1;  // K slices of the last residual matmul not yet added to h
     for (int l = 0; l < c.n_layers; l++) {
         auto &L = lw[l];
-        launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
+        launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
+        int nks_qkv;
         {
             GemmParams p{};
+            gemm_workspace(p);
             const bool bias = c.arch == 1;
             int t0 = 0;
             p.seg[0] = seg_of(L[K_ATTN_Q], t0, qkv, QKVD, 0, bias ? (const float *)L[K_BQ].d : nullptr);
@@ -519,7 +530,9 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = H;
             p.M = M;
             p.mode = GM_STORE;
+            p.allow_split = split_ok;
             run_gemm(p, PC_QKV, wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
+            nks_qkv = qgemm_slices(p);
         }
         {
             RopeKvParams r{};
@@ -538,6 +551,13 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             r.n_kv = c.n_kv_heads;
             r.hd = c.head_dim;
             r.interleaved = c.arch == 0;
+            r.part = qg_part;
+            r.nks = nks_qkv;
+            if (c.arch == 1) {
+                r.bq = (const float *)L[K_BQ].d;
+                r.bk = (const float *)L[K_BK].d;
+                r.bv = (const float *)L[K_BV].d;
+            }
             launch_rope_kv(r, st);
             AttnParams a{};
             a.q16 = q16;
@@ -571,6 +591,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         }
         {
             GemmParams p{};
+            gemm_workspace(p);
             p.seg[0] = seg_of(L[K_ATTN_O], 0, h, H, 0, nullptr);
             p.nseg = 1;
             p.ntiles = L[K_ATTN_O].rows / 16;
@@ -578,11 +599,14 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = QD;
             p.M = M;
             p.mode = GM_RESID;
+            p.allow_split = split_ok;
             run_gemm(p, PC_WO, wbytes(L[K_ATTN_O]));
+            pend = qgemm_slices(p);
         }
-        launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st);
+        launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         {
             GemmParams p{};
+            gemm_workspace(p);
             p.seg[0] = seg_of(L[K_FFN_GATE], 0, nullptr, 0, 0, nullptr);
             p.seg[1] = seg_of(L[K_FFN_UP], 0, nullptr, 0, 0, nullptr);
             p.nseg = 2;
@@ -598,6 +622,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         }
         {
             GemmParams p{};
+            gemm_workspace(p);
             p.seg[0] = seg_of(L[K_FFN_DOWN], 0, h, H, 0, nullptr);
             p.nseg = 1;
             p.ntiles = L[K_FFN_DOWN].rows / 16;
@@ -605,7 +630,9 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.K = c.ffn;
             p.M = M;
             p.mode = GM_RESID;
+            p.allow_split = split_ok;
             run_gemm(p, PC_DOWN, wbytes(L[K_FFN_DOWN]));
+            pend = qgemm_slices(p);
         }
         for (size_t ci = 0; ci < collect.size(); ci++)
             if (collect[ci] == l)
@@ -613,12 +640,13 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                                             hipMemcpyDeviceToDevice, st));
     }
     launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, xp, xp_ld, want_hidden ? hidden_out : nullptr,
-                   st);
+                   st, qg_part, pend);
     logits_rows_last = 0;
     if (logits_mode != 0) {
         const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
         const int rows = logits_mode == 1 ? 1 : M;
         GemmParams p{};
+        gemm_workspace(p);
         p.seg[0] = seg_of(W, 0, logits, c.vocab, 0, nullptr);
         p.nseg = 1;
         p.ntiles = W.rows / 16;
@@ -651,6 +679,7 @@ void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
                                     hipMemcpyHostToDevice, st));
         launch_to_frag16(hidden_out, n, c.hidden, xp, xp_ld, st);
         GemmParams p{};
+        gemm_workspace(p);
         p.seg[0] = seg_of(W, 0, logits, c.vocab, 0, nullptr);
         p.nseg = 1;
         p.ntiles = W.rows / 16;

@@ -127,6 +127,13 @@ class Model {
     float *part_o = nullptr, *part_ml = nullptr, *amax_v = nullptr, *collect_buf = nullptr;
     int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
     uint64_t *d_mask = nullptr;
+    // split-K partial sums of the M > 16 matmul (see GemmParams::allow_split)
+    float *qg_part = nullptr;
+    int64_t qg_part_cap = 0;
+    void gemm_workspace(GemmParams &p) const {
+        p.part = qg_part;
+        p.part_cap = qg_part_cap;
+    }
     // rejection-sampling acceptance: per-row softmax statistics, the tree,
     // draft rows, uniforms and results (draft rows grow on demand)
     float *acc_m = nullptr, *acc_s = nullptr, *acc_u = nullptr, *acc_q = nullptr;

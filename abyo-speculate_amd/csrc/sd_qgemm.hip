@@ -121,7 +121,15 @@ __device__ __forceinline__ void kquant_scales(const uintx4 &hdr, int g, float &s
 // Loads address one tile block: the wave-uniform part (tile, superblock) goes
 // in the scalar offset, the lane's fixed position inside the block in the
 // vector offset (see the tile-block layout in sd_layout.hip).
-__device__ __forceinline__ uint32_t tb_off(const WRow &w, int sb, int tbb) { return uni(w.base + (uint32_t)sb * tbb); }
+// A negative sb is a load that must not happen: its offset is pushed past any
+// resource size (a matrix is < 2 GiB), so the hardware range check returns
+// zeros without touching memory (the same trick as composable_kernel's
+// out-of-bounds buffer loads).  Loads can then be issued unconditionally,
+// which keeps the compiler's wait-count bookkeeping exact across loop turns.
+constexpr uint32_t kNoLoad = 0x80000000u;
+__device__ __forceinline__ uint32_t tb_off(const WRow &w, int sb, int tbb) {
+    return uni(sb < 0 ? kNoLoad : w.base + (uint32_t)sb * tbb);
+}
 
 template <> struct QFmt<Q4_K> {
     typedef LaneQ4K D;
@@ -236,21 +244,24 @@ template <> struct QFmt<Q8_0> {
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
 
 // --------------------------------------------------------------------------
-// Shared epilogue: v[rt] is the full sum for row tile rt (lane holds rows
-// rloc[rt] + 4g + i, token m).  Writes outputs and, for GM_LOGITS, the
-// per-workgroup argmax partial of every token (first max wins).
+// Epilogue of one wave's row tiles: v[rt] is the full sum of row tile rt (the
+// lane holds rows rloc[rt] + 4g + i of token m).  SWIGLU: tiles [0, RT/2) are
+// gate tiles and [RT/2, RT) the up tiles of the same features.  GM_LOGITS also
+// writes the tiles' argmax partial of every token (first max wins) to `slot`.
 // --------------------------------------------------------------------------
 template <int RT>
-__device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg &S, const int (&rloc)[RT],
-                                         floatx4 (&v)[RT], int m, int g) {
+__device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
+                                         const floatx4 (&v)[RT], int m, int g, int slot) {
     const bool live = m < p.M;
     if (p.mode == GM_SWIGLU) {
-        // v[0] = gate rows, v[RT-1] = up rows of the same output features
         if (live) {
             uint16_t *dst = p.act + (int64_t)m * p.act_ld;
-            const int n0 = rloc[0] + 4 * g;
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[frag_index(n0 + i)] = f2h(silu_f(v[0][i]) * v[RT - 1][i]);
+            for (int f = 0; f < RT / 2; f++) {
+                const int n0 = rloc[f] + 4 * g;
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[frag_index(n0 + i)] = f2h(silu_f(v[f][i]) * v[RT / 2 + f][i]);
+            }
         }
         return;
     }
@@ -260,19 +271,19 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg &S, 
     for (int rt = 0; rt < RT; rt++) {
         if (!live) continue;
         const int n0 = rloc[rt] + 4 * g;
-        float *o = S.out + (int64_t)m * S.ldo + S.col0 + n0;
+        float *o = S[rt].out + (int64_t)m * S[rt].ldo + S[rt].col0 + n0;
         floatx4 r = v[rt];
         if (p.mode == GM_RESID) {
             r += *(floatx4 *)o;
-        } else if (S.bias) {
-            r += *(const floatx4 *)(S.bias + n0);
+        } else if (S[rt].bias) {
+            r += *(const floatx4 *)(S[rt].bias + n0);
         }
         *(floatx4 *)o = r;
         if (p.mode == GM_LOGITS) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float x = r[i];
-                const int idx = S.col0 + n0 + i;
+                const int idx = S[rt].col0 + n0 + i;
                 if (x > -INFINITY && (x > bv || (x == bv && idx < bi))) {
                     bv = x;
                     bi = idx;
@@ -292,8 +303,8 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg &S, 
             }
         }
         if (g == 0 && live) {
-            p.amax_v[(int64_t)m * p.amax_ld + blockIdx.x] = bv;
-            p.amax_i[(int64_t)m * p.amax_ld + blockIdx.x] = bi;
+            p.amax_v[(int64_t)m * p.amax_ld + slot] = bv;
+            p.amax_i[(int64_t)m * p.amax_ld + slot] = bi;
         }
     }
 }
@@ -318,246 +329,536 @@ __device__ __forceinline__ WRow wrow(const GemmSeg &S, int K, int row0) {
 }
 
 // ==========================================================================
-// M <= 16
+// The kernel: a workgroup owns RT row tiles (a "row group") and KW waves that
+// split the K superblocks (wave w takes w, w + KW, ...); each wave multiplies
+// its RT tiles by CT token tiles, so every activation fragment it loads feeds
+// RT MFMAs and every dequantised weight fragment CT of them.
 // ==========================================================================
-template <int FMT>
-__device__ __forceinline__ void gemv_step(const typename QFmt<FMT>::D &d, rsrc_t xr, uint32_t xvo, int sb, int g,
-                                          floatx4 &acc) {
+// Vector-memory loads complete in issue order, so a wait on one load also
+// waits for every older one.  Each step therefore issues the loads it will
+// wait on first and the prefetch of the next step's operands after them.
+
+// One superblock of one token tile: the activations arrive with the weights
+// (both prefetched one step ahead, in two register sets).
+template <int FMT, int RT>
+__device__ __forceinline__ void qmm_step1(const typename QFmt<FMT>::D (&w)[RT], const uintx4 (&b)[8], int g,
+                                          floatx4 (&acc)[RT][1]) {
     typedef QFmt<FMT> F;
-    // activations of this superblock: issued before the dequantisation so
-    // their L2 latency overlaps it
-    uintx4 b[8];
+    typename F::S sc[RT];
 #pragma unroll
-    for (int c = 0; c < 8; c++) b[c] = bld16(xr, xvo + 64 * c, uni((uint32_t)sb * 512u));
-    const typename F::S sc = F::scales(d, g);
-    // all fragments first, then the MFMA chain: no MFMA waits on the VALU
-    // result it reads (the VALU -> MFMA operand hazard costs wait states)
-    half8 a[8];
+    for (int rt = 0; rt < RT; rt++) sc[rt] = F::scales(w[rt], g);
 #pragma unroll
-    for (int c = 0; c < 8; c++) a[c] = F::frag(d, sc, g, c);
+    for (int c = 0; c < 8; c++) {
+        half8 a[RT];
 #pragma unroll
-    for (int c = 0; c < 8; c++)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c], __builtin_bit_cast(half8, b[c]), acc, 0, 0, 0);
+        for (int rt = 0; rt < RT; rt++) a[rt] = F::frag(w[rt], sc[rt], g, c);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+            acc[rt][0] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt], __builtin_bit_cast(half8, b[c]), acc[rt][0], 0, 0, 0);
+    }
 }
 
-// Superblocks sb = ks, ks + KW, ... in order; the weights of the next two are
-// in flight (three register buffers in rotation) while one is computed.
-template <int FMT, int KW>
-__device__ __forceinline__ void gemv_body(const GemmParams &p, const WRow &row, int ks, floatx4 &acc) {
+// One superblock of CT token tiles: the superblock's activations are loaded
+// at the start of the step, before the next step's weights are requested.
+template <int FMT, int RT, int CT>
+__device__ __forceinline__ void qmm_stepn(const typename QFmt<FMT>::D (&w)[RT], const uintx4 (&b)[CT][8], int g,
+                                          floatx4 (&acc)[RT][CT]) {
+    typedef QFmt<FMT> F;
+    typename F::S sc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) sc[rt] = F::scales(w[rt], g);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        half8 a[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) a[rt] = F::frag(w[rt], sc[rt], g, c);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++)
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt], __builtin_bit_cast(half8, b[ct][c]),
+                                                                     acc[rt][ct], 0, 0, 0);
+    }
+}
+
+template <int CT>
+__device__ __forceinline__ void load_x(uintx4 (&b)[CT][8], rsrc_t xr, const uint32_t (&xvo)[CT], int sb) {
+    const uint32_t so = uni(sb < 0 ? kNoLoad : (uint32_t)sb * 512u);
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) b[ct][c] = bld16(xr, xvo[ct] + 64 * c, so);
+}
+
+// Superblocks in flight per wave (x + weights) for one token tile, 2 or 3:
+// measured equal on the verify shapes, and 2 leaves registers to spare.
+constexpr int kDepth1 = 2;
+
+// Superblocks sb = ks, ks + KW, ... in increasing order.
+template <int FMT, int RT, int CT, int KW>
+__device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT][CT]) {
     typedef QFmt<FMT> F;
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
     const int nsb = p.K >> 8;
-    // lanes of padding tokens (r16 >= M) read the last real token's row: the
-    // loads coalesce with that lane's and the padding columns are never stored
+    // token columns past M read the last real token's row: the loads coalesce
+    // with that lane's and the padding columns are never stored
     const rsrc_t xr = make_rsrc(p.xp, (uint32_t)p.M * (uint32_t)p.K * 2u);
-    const uint32_t xvo = ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u;
-    int sb = ks;
-    if (sb >= nsb) return;
-    typename F::D w0, w1, w2;
-    F::load(w0, row, nsb, sb, g);
-    if (sb + KW < nsb) F::load(w1, row, nsb, sb + KW, g);
-    while (true) {
-        if (sb + 2 * KW < nsb) F::load(w2, row, nsb, sb + 2 * KW, g);
-        gemv_step<FMT>(w0, xr, xvo, sb, g, acc);
-        sb += KW;
-        if (sb >= nsb) break;
-        if (sb + 2 * KW < nsb) F::load(w0, row, nsb, sb + 2 * KW, g);
-        gemv_step<FMT>(w1, xr, xvo, sb, g, acc);
-        sb += KW;
-        if (sb >= nsb) break;
-        if (sb + 2 * KW < nsb) F::load(w1, row, nsb, sb + 2 * KW, g);
-        gemv_step<FMT>(w2, xr, xvo, sb, g, acc);
-        sb += KW;
-        if (sb >= nsb) break;
+    uint32_t xvo[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) xvo[ct] = ((uint32_t)min(ct * 16 + r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u;
+    if (ks >= nsb) return;
+    const int nst = (nsb - ks + KW - 1) / KW;  // superblocks of this wave: ks + i * KW, i < nst
+    auto sbi = [&](int i) { return i < nst ? ks + i * KW : -1; };
+    typename F::D w0[RT], w1[RT];
+    if constexpr (CT == 1 && kDepth1 == 2) {
+        // x and weights of the next superblock in flight during this one
+        uintx4 b0[1][8], b1[1][8];
+        load_x<1>(b0, xr, xvo, sbi(0));
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        for (int i = 0;; i += 2) {
+            load_x<1>(b1, xr, xvo, sbi(i + 1));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
+            qmm_step1<FMT, RT>(w0, b0[0], g, acc);
+            if (i + 1 >= nst) break;
+            load_x<1>(b0, xr, xvo, sbi(i + 2));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
+            qmm_step1<FMT, RT>(w1, b1[0], g, acc);
+            if (i + 2 >= nst) break;
+        }
+    } else if constexpr (CT == 1) {
+        // x and weights of the next two superblocks in flight during this one
+        // (three register sets in rotation): at ~2.5 us loaded HBM latency a
+        // wave must keep about two superblocks requested to stream
+        uintx4 b0[1][8], b1[1][8], b2[1][8];
+        typename F::D w2[RT];
+        load_x<1>(b0, xr, xvo, sbi(0));
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        load_x<1>(b1, xr, xvo, sbi(1));
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(1), g);
+        for (int i = 0;; i += 3) {
+            load_x<1>(b2, xr, xvo, sbi(i + 2));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w2[rt], row[rt], nsb, sbi(i + 2), g);
+            qmm_step1<FMT, RT>(w0, b0[0], g, acc);
+            if (i + 1 >= nst) break;
+            load_x<1>(b0, xr, xvo, sbi(i + 3));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 3), g);
+            qmm_step1<FMT, RT>(w1, b1[0], g, acc);
+            if (i + 2 >= nst) break;
+            load_x<1>(b1, xr, xvo, sbi(i + 4));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 4), g);
+            qmm_step1<FMT, RT>(w2, b2[0], g, acc);
+            if (i + 3 >= nst) break;
+        }
+    } else {
+        // weights one superblock ahead; the activations of a superblock are
+        // requested before the next superblock's weights
+        uintx4 b[CT][8];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        for (int i = 0;; i += 2) {
+            load_x<CT>(b, xr, xvo, sbi(i));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
+            qmm_stepn<FMT, RT, CT>(w0, b, g, acc);
+            if (i + 1 >= nst) break;
+            load_x<CT>(b, xr, xvo, sbi(i + 1));
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
+            qmm_stepn<FMT, RT, CT>(w1, b, g, acc);
+            if (i + 2 >= nst) break;
+        }
     }
 }
 
-// Workgroup = NT row tiles x KW waves: wave w works on tile w / KW and on the
-// superblocks w % KW, w % KW + KW, ...  NT = 2 only in SWIGLU mode (gate tile,
-// up tile of the same 16 features).
-template <int NT, int KW>
-__global__ __launch_bounds__(64 * KW * NT) void k_qgemv(GemmParams p) {
+template <int RT, int CT, int KW>
+__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int t = wave / KW, ks = wave % KW;
-    GemmSeg S, St;
-    int rloc;
-    if (NT == 2) {
-        S = p.seg[0];
-        St = t == 0 ? p.seg[0] : p.seg[1];
-        rloc = (int)blockIdx.x * 16;
+    GemmSeg S[RT];
+    int rloc[RT];
+    if (p.mode == GM_SWIGLU) {
+        // feature tiles f0 .. f0 + RT/2 - 1: their gate tiles, then their up tiles
+        const int f0 = (int)blockIdx.x * (RT / 2);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            S[rt] = rt < RT / 2 ? p.seg[0] : p.seg[1];
+            rloc[rt] = (f0 + rt % (RT / 2)) * 16;
+        }
     } else {
-        S = seg_of_tile(p, blockIdx.x);
-        St = S;
-        rloc = ((int)blockIdx.x - S.tile0) * 16;
+        // RT consecutive tiles of one segment (segment sizes are multiples of RT)
+        const int t0 = (int)blockIdx.x * RT;
+        const GemmSeg s = seg_of_tile(p, t0);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            S[rt] = s;
+            rloc[rt] = (t0 - s.tile0 + rt) * 16;
+        }
     }
-    const WRow row = wrow(St, p.K, rloc);
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    switch (St.fmt) {
-    case Q4_K: gemv_body<Q4_K, KW>(p, row, ks, acc); break;
-    case Q5_K: gemv_body<Q5_K, KW>(p, row, ks, acc); break;
-    case Q6_K: gemv_body<Q6_K, KW>(p, row, ks, acc); break;
-    case Q8_0: gemv_body<Q8_0, KW>(p, row, ks, acc); break;
+    WRow row[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) row[rt] = wrow(S[rt], p.K, rloc[rt]);
+    floatx4 acc[RT][CT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    switch (S[0].fmt) {
+    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc); break;
+    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc); break;
+    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc); break;
+    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc); break;
     default: break;
     }
-    floatx4 v[NT];
-    if constexpr (KW * NT > 1) {
-        __shared__ floatx4 red[NT][KW][64];
-        red[t][ks][lane] = acc;
-        __syncthreads();
-        if (wave != 0) return;
+    // fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, one
+    // token tile at a time
 #pragma unroll
-        for (int tt = 0; tt < NT; tt++) {
-            floatx4 sum = red[tt][0][lane];
+    for (int ct = 0; ct < CT; ct++) {
+        floatx4 v[RT];
+        if constexpr (KW > 1) {
+            __shared__ floatx4 red[KW][RT][64];
+            __syncthreads();
 #pragma unroll
-            for (int w = 1; w < KW; w++) sum += red[tt][w][lane];
-            v[tt] = sum;
+            for (int rt = 0; rt < RT; rt++) red[wave][rt][lane] = acc[rt][ct];
+            __syncthreads();
+            if (wave != 0) continue;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                floatx4 s = red[0][rt][lane];
+#pragma unroll
+                for (int w = 1; w < KW; w++) s += red[w][rt][lane];
+                v[rt] = s;
+            }
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) v[rt] = acc[rt][ct];
         }
-    } else {
-        v[0] = acc;
+        epilogue<RT>(p, S, rloc, v, ct * 16 + r16, g, (int)blockIdx.x);
     }
-    int rl[NT];
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) rl[tt] = rloc;
-    epilogue<NT>(p, S, rl, v, r16, g);
 }
 
 // ==========================================================================
-// M > 16
+// M > 16 (tree and prefill shapes).  A workgroup of 4 waves owns a row block
+// -- 4 x RW row tiles, or for gate/up 4 features' gate and up tiles -- and one
+// K slice.  The slice's activations are staged superblock by superblock in
+// LDS, so each activation byte is fetched from L2 once per workgroup and read
+// by all 4 waves (reading them per wave from L1 made the M = 60 launches L2
+// bound); the weights stream into registers one superblock ahead.  With more
+// than one K slice the launch writes per-slice partial sums and the kernel
+// that consumes the output adds them (GM_STORE / GM_RESID callers only).
 // ==========================================================================
-template <int FMT, int CT, int KW>
-__device__ __forceinline__ void gemm_body(const GemmParams &p, const WRow &row, floatx4 (&acc)[CT]) {
+constexpr int XG_WAVES = 4;
+constexpr int XG_PITCH = 528;  // bytes per staged token row: 512 + 16 keeps ds_read_b128 conflict free
+
+template <int CT> struct XStage {
+    uintx4 v[2 * CT];  // CT*16 rows x 32 16-byte pieces over 256 threads
+};
+
+// the activations of superblock sb (a negative sb loads nothing)
+template <int CT>
+__device__ __forceinline__ void xg_load(XStage<CT> &st, rsrc_t xr, int M, int K, int sb) {
+    const uint32_t so = uni(sb < 0 ? kNoLoad : (uint32_t)sb * 512u);
+#pragma unroll
+    for (int i = 0; i < 2 * CT; i++) {
+        const int piece = (int)threadIdx.x + 256 * i, r = piece >> 5, col = piece & 31;
+        const uint32_t vo = r < M ? (uint32_t)r * (uint32_t)K * 2u + (uint32_t)col * 16u : kNoLoad;
+        st.v[i] = bld16(xr, vo, so);
+    }
+}
+template <int CT> __device__ __forceinline__ void xg_store(const XStage<CT> &st, uint8_t *buf) {
+#pragma unroll
+    for (int i = 0; i < 2 * CT; i++) {
+        const int piece = (int)threadIdx.x + 256 * i, r = piece >> 5, col = piece & 31;
+        *(uintx4 *)(buf + r * XG_PITCH + col * 16) = st.v[i];
+    }
+}
+
+template <int FMT, int RW, int CT>
+__device__ __forceinline__ void qgx_step(const typename QFmt<FMT>::D (&w)[RW], const uint8_t *xb,
+                                         const uint32_t (&boff)[CT], int g, floatx4 (&acc)[RW][CT]) {
     typedef QFmt<FMT> F;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r16 = lane & 15, g = lane >> 4;
-    const int K = p.K, nsb = K >> 8;
-    const rsrc_t xr = make_rsrc(p.xp, (uint32_t)(CT * 16) * (uint32_t)K * 2u);
-    const uint32_t xvo = ((uint32_t)r16 * (uint32_t)K + 8u * g) * 2u, xct = 16u * (uint32_t)K * 2u;
-    int sb = wave;
-    if (sb >= nsb) return;
-    typename F::D cur, nxt;
-    F::load(cur, row, nsb, sb, g);
-    for (; sb < nsb; sb += KW) {
-        const int nx = sb + KW < nsb ? sb + KW : sb;
-        F::load(nxt, row, nsb, nx, g);
-        uintx4 bf[CT][8];
+    typename F::S sc[RW];
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++)
+    for (int rt = 0; rt < RW; rt++) sc[rt] = F::scales(w[rt], g);
 #pragma unroll
-            for (int c = 0; c < 8; c++) bf[ct][c] = bld16(xr, xvo + ct * xct + 64 * c, uni((uint32_t)sb * 512u));
-        const typename F::S sc = F::scales(cur, g);
+    for (int c = 0; c < 8; c++) {
+        half8 b[CT];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const half8 a = F::frag(cur, sc, g, c);
+        for (int ct = 0; ct < CT; ct++) b[ct] = *(const half8 *)(xb + boff[ct] + 64 * c);
+#pragma unroll
+        for (int rt = 0; rt < RW; rt++) {
+            const half8 a = F::frag(w[rt], sc[rt], g, c);
 #pragma unroll
             for (int ct = 0; ct < CT; ct++)
-                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, bf[ct][c]), acc[ct], 0,
-                                                                 0, 0);
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[ct], acc[rt][ct], 0, 0, 0);
         }
-        cur = nxt;
     }
 }
 
-// One row tile per workgroup; in SWIGLU mode the workgroup computes the gate
-// tile and then the up tile of the same 16 output features.
-template <int CT, int KW>
-__global__ __launch_bounds__(64 * KW) void k_qgemm(GemmParams p) {
+// superblocks [sb0, sb1); every thread stages, waves with live = false only
+// keep the barriers
+template <int FMT, int RW, int CT>
+__device__ __forceinline__ void qgx_body(const GemmParams &p, const WRow (&row)[RW], bool live, int sb0, int sb1,
+                                         floatx4 (&acc)[RW][CT], uint8_t *lds) {
+    typedef QFmt<FMT> F;
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
+    const int nsb = p.K >> 8;
+    constexpr int STAGE = CT * 16 * XG_PITCH;
+    const rsrc_t xr = make_rsrc(p.xp, (uint32_t)p.M * (uint32_t)p.K * 2u);
+    uint32_t boff[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) boff[ct] = (uint32_t)min(ct * 16 + r16, p.M - 1) * XG_PITCH + 16u * g;
+    typename F::D w0[RW], w1[RW];
+    XStage<CT> xs;
+    auto wsb = [&](int sb) { return live && sb < sb1 ? sb : -1; };
+    xg_load<CT>(xs, xr, p.M, p.K, sb0);
+#pragma unroll
+    for (int rt = 0; rt < RW; rt++) F::load(w0[rt], row[rt], nsb, wsb(sb0), g);
+    xg_store<CT>(xs, lds);
+    __syncthreads();
+    for (int sb = sb0;; sb += 2) {
+        // next superblock: activations first (the LDS store below waits on
+        // them only), then weights
+        xg_load<CT>(xs, xr, p.M, p.K, sb + 1 < sb1 ? sb + 1 : -1);
+#pragma unroll
+        for (int rt = 0; rt < RW; rt++) F::load(w1[rt], row[rt], nsb, wsb(sb + 1), g);
+        if (live) qgx_step<FMT, RW, CT>(w0, lds, boff, g, acc);
+        if (sb + 1 >= sb1) break;
+        xg_store<CT>(xs, lds + STAGE);
+        __syncthreads();
+        xg_load<CT>(xs, xr, p.M, p.K, sb + 2 < sb1 ? sb + 2 : -1);
+#pragma unroll
+        for (int rt = 0; rt < RW; rt++) F::load(w0[rt], row[rt], nsb, wsb(sb + 2), g);
+        if (live) qgx_step<FMT, RW, CT>(w1, lds + STAGE, boff, g, acc);
+        if (sb + 2 >= sb1) break;
+        xg_store<CT>(xs, lds);
+        __syncthreads();
+    }
+}
+
+template <int RW, int CT>
+__global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
+    const int rb = (int)blockIdx.x / nks, ks = (int)blockIdx.x % nks;
     const bool swi = p.mode == GM_SWIGLU;
-    const int nt = swi ? 2 : 1;
-    const GemmSeg S = swi ? p.seg[0] : seg_of_tile(p, blockIdx.x);
-    const int rloc = swi ? (int)blockIdx.x * 16 : ((int)blockIdx.x - S.tile0) * 16;
-    floatx4 acc[2][CT];
-    for (int t = 0; t < nt; t++) {
-        const GemmSeg St = (swi && t == 1) ? p.seg[1] : S;
-        const WRow row = wrow(St, p.K, rloc);
+    const int nfeat = swi ? p.seg[0].rows / 16 : 0;
+    // this wave's row tiles and their place among the launch's output rows
+    GemmSeg S[RW];
+    int rloc[RW], grow[RW];
+    bool live;
+    if (swi) {
+        const int f = rb * XG_WAVES + wave;
+        live = f < nfeat;
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) acc[t][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-        switch (St.fmt) {
-        case Q4_K: gemm_body<Q4_K, CT, KW>(p, row, acc[t]); break;
-        case Q5_K: gemm_body<Q5_K, CT, KW>(p, row, acc[t]); break;
-        case Q6_K: gemm_body<Q6_K, CT, KW>(p, row, acc[t]); break;
-        case Q8_0: gemm_body<Q8_0, CT, KW>(p, row, acc[t]); break;
-        default: break;
+        for (int rt = 0; rt < RW; rt++) {
+            S[rt] = rt == 0 ? p.seg[0] : p.seg[1];
+            rloc[rt] = (live ? f : 0) * 16;
+            grow[rt] = rt * nfeat * 16 + rloc[rt];
+        }
+    } else {
+        const int t0 = (rb * XG_WAVES + wave) * RW;
+        live = t0 < p.ntiles;
+        const GemmSeg s = seg_of_tile(p, live ? t0 : 0);
+#pragma unroll
+        for (int rt = 0; rt < RW; rt++) {
+            S[rt] = s;
+            rloc[rt] = ((live ? t0 : s.tile0) - s.tile0 + rt) * 16;
+            grow[rt] = (live ? t0 : 0) * 16 + rt * 16;
         }
     }
-    // fixed-order cross-wave reduction through LDS, one token tile at a time
-    __shared__ floatx4 red[KW][2][64];
-    const int r2[2] = {rloc, rloc};
+    WRow row[RW];
+#pragma unroll
+    for (int rt = 0; rt < RW; rt++) row[rt] = wrow(S[rt], p.K, rloc[rt]);
+    const int nsb = p.K >> 8;
+    const int sb0 = ks * nsb / nks, sb1 = (ks + 1) * nsb / nks;
+    floatx4 acc[RW][CT];
+#pragma unroll
+    for (int rt = 0; rt < RW; rt++)
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    switch (S[0].fmt) {
+    case Q4_K: qgx_body<Q4_K, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
+    case Q5_K: qgx_body<Q5_K, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
+    case Q6_K: qgx_body<Q6_K, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
+    case Q8_0: qgx_body<Q8_0, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
+    default: break;
+    }
+    const int slot = rb * XG_WAVES + wave;  // argmax partial slot of this wave
+    if (!live) {
+        // padding waves of the last row block leave a neutral argmax partial
+        if (p.mode == GM_LOGITS && g == 0)
+            for (int m = r16; m < p.M; m += 16) {
+                p.amax_v[(int64_t)m * p.amax_ld + slot] = -INFINITY;
+                p.amax_i[(int64_t)m * p.amax_ld + slot] = 0x7fffffff;
+            }
+        if (nks == 1) return;
+    }
+    if (nks == 1) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) {
+            floatx4 v[RW];
+#pragma unroll
+            for (int rt = 0; rt < RW; rt++) v[rt] = acc[rt][ct];
+            epilogue<RW>(p, S, rloc, v, ct * 16 + r16, g, slot);
+        }
+        return;
+    }
+    // K slices: partial sums [ks][M][R] (R = output rows of the launch); the
+    // consumer of the output adds them in slice order (an in-kernel reduction
+    // by the last workgroup needs agent-scope fences, i.e. L2 write-back and
+    // invalidation on every XCD, which measured slower than the split saved)
+    if (!live) return;
+    const int R = p.ntiles * 16;
+#pragma unroll
     for (int ct = 0; ct < CT; ct++) {
-        __syncthreads();
-        for (int t = 0; t < nt; t++) red[wave][t][lane] = acc[t][ct];
-        __syncthreads();
-        if (wave != 0) continue;
-        floatx4 v[2];
-        for (int t = 0; t < nt; t++) {
-            floatx4 s = red[0][t][lane];
-            for (int w = 1; w < KW; w++) s += red[w][t][lane];
-            v[t] = s;
-        }
         const int m = ct * 16 + r16;
-        if (swi) {
-            epilogue<2>(p, S, r2, v, m, g);
-        } else {
-            const int r1[1] = {rloc};
-            floatx4 v1[1] = {v[0]};
-            epilogue<1>(p, S, r1, v1, m, g);
-        }
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int rt = 0; rt < RW; rt++)
+            *(floatx4 *)(p.part + ((int64_t)ks * p.M + m) * R + grow[rt] + 4 * g) = acc[rt][ct];
     }
 }
 
 // --------------------------------------------------------------------------
-// Launch policy.  KW (waves splitting K) is a function of the matrix only:
-// the smallest power of two that puts >= 2048 waves on the chip for the M <= 16
-// kernel, capped at 8 and at the number of superblocks.
+// Launch policy.  KW (waves splitting K) is a function of the matrix only --
+// the smallest power of two that reaches the policy's wave count, capped at 8
+// (two waves per SIMD keep the register file) and at the number of
+// superblocks -- so row i of an M-row call equals the M=1 call bit for bit.  RT depends on M only through
+// the register budget and changes which tiles share a wave, not any sum.
 // --------------------------------------------------------------------------
-static int tiles_per_row_group(const GemmParams &p) { return p.mode == GM_SWIGLU ? p.seg[0].rows / 16 : p.ntiles; }
+static int swiglu_features(const GemmParams &p) { return p.seg[0].rows / 16; }
+static int total_rows(const GemmParams &p) {
+    int r = 0;
+    for (int i = 0; i < p.nseg; i++) r += p.seg[i].rows;
+    return r;
+}
+
+// Row tiles per wave and the wave count K is split towards, per matrix:
+// outputs of up to 4096 rows (wo, ffn_down at the 8B shapes) stream best as
+// 1 tile per wave and >= 2048 waves, wider ones (fused QKV, gate/up, lm_head)
+// as 2 tiles per wave and >= 1024 waves (measured on MI355X; a wave's start-up
+// latency is paid once per K range, so few long waves beat many short ones
+// once the grid covers the chip).
+static int policy_rt(const GemmParams &p) { return p.mode == GM_SWIGLU ? 2 : total_rows(p) <= 4096 ? 1 : 2; }
 
 int qgemm_kw(const GemmParams &p) {
     const int nsb = p.K / 256;
-    const int groups = tiles_per_row_group(p);  // row groups (16 rows, or gate+up pairs)
+    const int rt = policy_rt(p);
+    const int groups = p.mode == GM_SWIGLU ? swiglu_features(p) : p.ntiles / rt;
+    const int target = rt == 1 ? 2048 : 1024;
     int kw = 1;
-    while (kw < 8 && groups * kw < 2048) kw *= 2;
+    while (kw < 8 && groups * kw < target) kw *= 2;
     while (kw > 1 && kw > nsb) kw /= 2;
-    if (p.mode == GM_SWIGLU && kw > 4) kw = 4;  // 2 x 8 waves would exceed 128 VGPRs per lane
     return kw;
 }
 
-int qgemm_workgroups(const GemmParams &p) {
-    if (p.mode == GM_SWIGLU) return p.seg[0].rows / 16;
-    return p.ntiles;
+static int token_tiles(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+
+// Row tiles of a wave: the policy's for up to two token tiles, else 1 (gate/up
+// pairs always 2); shrunk until every segment splits evenly.
+static int qgemm_rt(const GemmParams &p) {
+    if (p.mode == GM_SWIGLU) return 2;
+    int rt = token_tiles(p.M) <= 2 ? policy_rt(p) : 1;
+    for (; rt > 1; rt /= 2) {
+        bool ok = p.ntiles % rt == 0;
+        for (int i = 0; i < p.nseg; i++) ok = ok && (p.seg[i].rows / 16) % rt == 0;
+        if (ok) break;
+    }
+    return rt;
 }
 
-template <int NT, int KW>
-static void launch_gemv(const GemmParams &p, int nwg, hipStream_t st) {
-    hipLaunchKernelGGL((k_qgemv<NT, KW>), dim3(nwg), dim3(64 * KW * NT), 0, st, p);
+// ---- M > 16: row blocks of 4 waves, K slices towards one workgroup per CU ----
+static int xg_rw(const GemmParams &p) {
+    if (p.mode == GM_SWIGLU) return 2;
+    if (token_tiles(p.M) > 4) return 1;
+    for (int i = 0; i < p.nseg; i++)
+        if ((p.seg[i].rows / 16) % 2) return 1;
+    return 2;
 }
-template <int CT, int KW>
-static void launch_gemm(const GemmParams &p, int nwg, hipStream_t st) {
-    hipLaunchKernelGGL((k_qgemm<CT, KW>), dim3(nwg), dim3(64 * KW), 0, st, p);
+static int xg_row_blocks(const GemmParams &p) {
+    const int units = p.mode == GM_SWIGLU ? swiglu_features(p) : p.ntiles / xg_rw(p);
+    return (units + XG_WAVES - 1) / XG_WAVES;
+}
+// K slices: only when the caller finalises them (allow_split), towards 192
+// workgroups, up to 8 slices and the partial-sum buffer
+int qgemm_slices(const GemmParams &p) {
+    if (p.M <= 16 || !p.allow_split || (p.mode != GM_STORE && p.mode != GM_RESID)) return 1;
+    const int rb = xg_row_blocks(p), nsb = p.K / 256;
+    const int64_t R = 16LL * p.ntiles;
+    int ks = 1;
+    while (ks < 8 && rb * ks < 192 && 2 * ks <= nsb && (int64_t)2 * ks * p.M * R <= p.part_cap) ks *= 2;
+    return ks;
+}
+
+// argmax partial slots of a GM_LOGITS launch (= amax_ld)
+int qgemm_workgroups(const GemmParams &p) {
+    if (p.M > 16) return xg_row_blocks(p) * XG_WAVES;
+    const int rt = qgemm_rt(p);
+    return p.mode == GM_SWIGLU ? swiglu_features(p) / (rt / 2) : p.ntiles / rt;
+}
+
+template <int RW, int CT>
+static void launch_qgx(const GemmParams &p, hipStream_t st) {
+    const int rb = xg_row_blocks(p), nks = qgemm_slices(p);
+    const size_t lds = 2 * CT * 16 * XG_PITCH;
+    hipLaunchKernelGGL((k_qgx<RW, CT>), dim3(rb * nks), dim3(64 * XG_WAVES), lds, st, p, nks);
+}
+
+template <int RT, int CT, int KW>
+static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st) {
+    hipLaunchKernelGGL((k_qmm<RT, CT, KW>), dim3(nwg), dim3(64 * KW), 0, st, p);
+}
+
+template <int RT, int CT>
+static bool launch_kw(const GemmParams &p, int kw, int nwg, hipStream_t st) {
+    switch (kw) {
+    case 1: launch_qmm<RT, CT, 1>(p, nwg, st); return true;
+    case 2: launch_qmm<RT, CT, 2>(p, nwg, st); return true;
+    case 4: launch_qmm<RT, CT, 4>(p, nwg, st); return true;
+    case 8: launch_qmm<RT, CT, 8>(p, nwg, st); return true;
+    default: return false;
+    }
 }
 
 int launch_qgemm(const GemmParams &p, hipStream_t st) {
     if (p.M < 1 || p.M > 128) throw BackendError("qgemm: M out of range");
-    const int kw = qgemm_kw(p);
-    const int nwg = qgemm_workgroups(p);
-    if (p.M <= 16) {
-        const int nt = p.mode == GM_SWIGLU ? 2 : 1;
-#define SD_GEMV(T, W) if (nt == T && kw == W) { launch_gemv<T, W>(p, nwg, st); return nwg; }
-        SD_GEMV(1, 1) SD_GEMV(1, 2) SD_GEMV(1, 4) SD_GEMV(1, 8)
-        SD_GEMV(2, 1) SD_GEMV(2, 2) SD_GEMV(2, 4) SD_GEMV(2, 8)
-#undef SD_GEMV
-        throw BackendError("qgemv: unsupported launch shape");
+    if (p.K % 256) throw BackendError("qgemm: K must be a multiple of 256");
+    if (p.mode == GM_SWIGLU && (p.nseg != 2 || p.seg[0].rows != p.seg[1].rows || p.seg[0].fmt != p.seg[1].fmt))
+        throw BackendError("qgemm: gate/up segments must match");
+    if (p.mode != GM_SWIGLU)
+        for (int i = 1; i < p.nseg; i++)
+            if (p.seg[i].tile0 != p.seg[i - 1].tile0 + p.seg[i - 1].rows / 16)
+                throw BackendError("qgemm: segments must be consecutive");
+    const int ct = token_tiles(p.M);
+    if (ct > 1) {
+        if (qgemm_slices(p) > 1 && !p.part) throw BackendError("qgemm: split-K workspace missing");
+        const int rw = xg_rw(p);
+        if (rw == 2 && ct == 2) launch_qgx<2, 2>(p, st);
+        else if (rw == 2 && ct == 4) launch_qgx<2, 4>(p, st);
+        else if (rw == 2 && ct == 8) launch_qgx<2, 8>(p, st);
+        else if (rw == 1 && ct == 2) launch_qgx<1, 2>(p, st);
+        else if (rw == 1 && ct == 4) launch_qgx<1, 4>(p, st);
+        else launch_qgx<1, 8>(p, st);
+        return qgemm_workgroups(p);
     }
-    const int ct = p.M <= 32 ? 2 : p.M <= 64 ? 4 : 8;
-#define SD_GEMM(C, W) if (ct == C && kw == W) { launch_gemm<C, W>(p, nwg, st); return nwg; }
-    SD_GEMM(2, 1) SD_GEMM(2, 2) SD_GEMM(2, 4) SD_GEMM(2, 8)
-    SD_GEMM(4, 1) SD_GEMM(4, 2) SD_GEMM(4, 4) SD_GEMM(4, 8)
-    SD_GEMM(8, 1) SD_GEMM(8, 2) SD_GEMM(8, 4) SD_GEMM(8, 8)
-#undef SD_GEMM
-    throw BackendError("qgemm: unsupported launch shape");
+    const int kw = qgemm_kw(p), rt = qgemm_rt(p);
+    const int nwg = qgemm_workgroups(p);
+    bool ok = false;
+    if (rt == 2) ok = launch_kw<2, 1>(p, kw, nwg, st);
+    else if (rt == 1 && p.mode != GM_SWIGLU) ok = launch_kw<1, 1>(p, kw, nwg, st);
+    if (!ok) throw BackendError("qgemm: unsupported launch shape");
+    return nwg;
 }
 
 }  // namespace sd

@@ -130,19 +130,29 @@ def test_tree_keep_kv_verify_and_commit(hip):
     assert rel_err(a, b) < TOL
 
 
-def test_strict_root_row_is_m_invariant(hip):
-    """Row 0 of a tree pass equals the single-token pass bit for bit, so the
-    strict (GEMV-root) mode changes nothing."""
+def test_strict_root_row(hip):
+    """tree_logits (strict, quantized_llama.rs:262-325) takes row 0 from a
+    single-token pass, bit for bit the next_logits row; the fast path's row 0
+    comes from the tree-shaped pass and agrees to rounding; every other row is
+    the same tree pass in both."""
     od, hd, prefix = make_pair(hip)
     chain = greedy_chain(od, 3)
     tree = O.build_cartesian_tree(prefix[-1], _tree_with_chain(chain, 32000))
-    nl = hd.next_logits()
+    nl = hd.next_logits()  # cached by the 128-row observe pass
     strict = hd.tree_logits(tree)
     assert hd.cache_len() == len(prefix)
     fast, _ = hd.tree_logits_keep_kv(tree)
-    assert np.array_equal(strict[0].view(np.uint32), nl.view(np.uint32))
-    assert np.array_equal(fast[0].view(np.uint32), nl.view(np.uint32))
+    for row in (strict[0], fast[0]):
+        # different row counts take different K splits; fp16 activations carry
+        # the rounding differences through the layers
+        assert rel_err(row, nl.astype(np.float64)) < 2e-3
+        if safe(nl):
+            assert int(np.argmax(row)) == int(np.argmax(nl))  # tree_logits_consistency.rs:74-122
     assert np.array_equal(strict[1:].view(np.uint32), fast[1:].view(np.uint32))
+    # the strict row is exactly the single-token (M = 1) pass of the root
+    hd.rollback_to(len(prefix) - 1)
+    hd.observe([prefix[-1]])
+    assert np.array_equal(strict[0].view(np.uint32), hd.next_logits().view(np.uint32))
 
 
 def test_error_semantics_keep_state(hip):

@@ -83,14 +83,22 @@ def test_qmatmul_vs_oracle(hip, mix, layer, kind, M):
 @pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q6_k", O.K_FFN_DOWN), ("q8_0", O.K_FFN_UP),
                                       ("q5_k", O.K_ATTN_V)])
 def test_qmatmul_m_invariant(hip, mix, kind):
-    """Row i of an M-row product equals the single-row product bit for bit, for
-    every M (tile shape changes at 16/32/64 rows)."""
+    """Up to 16 rows (the linear-verify shapes) row i of an M-row product equals
+    the single-row product bit for bit: the K split is a function of the
+    matrix only.  Past 16 rows the activation-staged kernel sums K in other
+    slices, so rows agree to f32 rounding (the reference's own GEMV and GEMM
+    paths differ the same way, which is why its strict root mode exists)."""
     ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
     K = ocfg.shape(kind)[1]
     x = np.random.default_rng(11).standard_normal((128, K)).astype(np.float32)
-    singles = [dec.qmatmul(0, kind, x[i:i + 1])[0] for i in (0, 3, 15, 16, 63, 64, 127)]
-    for M in (5, 16, 17, 60, 64, 65, 128):
+    picks = (0, 3, 15, 16, 63, 64, 127)
+    singles = [dec.qmatmul(0, kind, x[i:i + 1])[0] for i in picks]
+    for M in (5, 9, 16, 17, 60, 64, 65, 128):
         y = dec.qmatmul(0, kind, x[:M])
-        for j, i in enumerate((0, 3, 15, 16, 63, 64, 127)):
-            if i < M:
+        for j, i in enumerate(picks):
+            if i >= M:
+                continue
+            if M <= 16:
                 assert np.array_equal(y[i].view(np.uint32), singles[j].view(np.uint32)), (M, i)
+            else:
+                assert rel_err(y[i], singles[j].astype(np.float64)) < 1e-5, (M, i)
