@@ -59,9 +59,16 @@ struct GemmParams {
     int64_t part_cap;        // floats
 };
 
+// Optional timing of one launch: with both events set the kernel goes through
+// hipExtLaunchKernel, which stamps the events with the dispatch's own start and
+// end (the kernel's duration, without the queue gaps around it).
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
 // Launches y = x . W^T over all segments.  Chooses the tile shape from M.
 // Returns the number of workgroups launched (GM_LOGITS partial count).
-int launch_qgemm(const GemmParams &p, hipStream_t st);
+int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm = LaunchTiming{});
 int qgemm_workgroups(const GemmParams &p);
 int qgemm_slices(const GemmParams &p);  // 1 when the output is written directly
 

@@ -329,14 +329,18 @@ void Model::fill_kv_synthetic(int P, uint64_t seed) {
 
 void Model::prof_reset() { prof.clear(); }
 
-int Model::prof_begin() {
+int Model::prof_events() {
     const size_t need = 2 * (prof.size() + 1);
     while (ev_pool.size() < need) {
         hipEvent_t e;
         SD_HIP_CHECK(hipEventCreate(&e));
         ev_pool.push_back(e);
     }
-    const int ev = (int)(2 * prof.size());
+    return (int)(2 * prof.size());
+}
+
+int Model::prof_begin() {
+    const int ev = prof_events();
     SD_HIP_CHECK(hipEventRecord(ev_pool[ev], st));
     return ev;
 }
@@ -363,9 +367,10 @@ static double gemm_bytes(const GemmParams &p, double wbytes) {
 void Model::run_gemm(GemmParams &p, int cls, double bytes) {
     bytes = gemm_bytes(p, bytes);
     if (prof_on) {
-        const int ev = prof_begin();
-        launch_qgemm(p, st);
-        prof_end(ev, cls, bytes);
+        // the events carry the dispatch's own start / end timestamps
+        const int ev = prof_events();
+        launch_qgemm(p, st, LaunchTiming{ev_pool[ev], ev_pool[ev + 1]});
+        prof.push_back(ProfEntry{cls, bytes, ev});
     } else {
         launch_qgemm(p, st);
     }

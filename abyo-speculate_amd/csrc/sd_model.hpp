@@ -116,6 +116,7 @@ class Model {
     std::vector<ProfEntry> prof;
     std::vector<hipEvent_t> ev_pool;
     void prof_reset();
+    int prof_events();                             // index of a free (start, stop) event pair
     int prof_begin();                              // records a start event, returns its index
     void prof_end(int ev, int cls, double bytes);  // records the stop event
 

@@ -28,6 +28,8 @@
 // (0x5400 | q << 4 == 64 + q), and v_fma_mix evaluates
 // round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m): the f32
 // value s*q - m rounded once to fp16.
+#include <hip/hip_ext.h>
+
 #include "sd_common.hpp"
 #include "sd_kernels.hpp"
 #include "sd_qcodes.hpp"
@@ -808,30 +810,37 @@ int qgemm_workgroups(const GemmParams &p) {
     return p.mode == GM_SWIGLU ? swiglu_features(p) / (rt / 2) : p.ntiles / rt;
 }
 
+template <typename Kern, typename... Args>
+static void launch_timed(Kern kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, const LaunchTiming &tm,
+                         Args... args) {
+    if (tm.start && tm.stop) hipExtLaunchKernelGGL(kern, grid, block, lds, st, tm.start, tm.stop, 0, args...);
+    else hipLaunchKernelGGL(kern, grid, block, lds, st, args...);
+}
+
 template <int RW, int CT>
-static void launch_qgx(const GemmParams &p, hipStream_t st) {
+static void launch_qgx(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
     const int rb = xg_row_blocks(p), nks = qgemm_slices(p);
     const size_t lds = 2 * CT * 16 * XG_PITCH;
-    hipLaunchKernelGGL((k_qgx<RW, CT>), dim3(rb * nks), dim3(64 * XG_WAVES), lds, st, p, nks);
+    launch_timed(k_qgx<RW, CT>, dim3(rb * nks), dim3(64 * XG_WAVES), lds, st, tm, p, nks);
 }
 
 template <int RT, int CT, int KW>
-static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st) {
-    hipLaunchKernelGGL((k_qmm<RT, CT, KW>), dim3(nwg), dim3(64 * KW), 0, st, p);
+static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st, const LaunchTiming &tm) {
+    launch_timed(k_qmm<RT, CT, KW>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
 }
 
 template <int RT, int CT>
-static bool launch_kw(const GemmParams &p, int kw, int nwg, hipStream_t st) {
+static bool launch_kw(const GemmParams &p, int kw, int nwg, hipStream_t st, const LaunchTiming &tm) {
     switch (kw) {
-    case 1: launch_qmm<RT, CT, 1>(p, nwg, st); return true;
-    case 2: launch_qmm<RT, CT, 2>(p, nwg, st); return true;
-    case 4: launch_qmm<RT, CT, 4>(p, nwg, st); return true;
-    case 8: launch_qmm<RT, CT, 8>(p, nwg, st); return true;
+    case 1: launch_qmm<RT, CT, 1>(p, nwg, st, tm); return true;
+    case 2: launch_qmm<RT, CT, 2>(p, nwg, st, tm); return true;
+    case 4: launch_qmm<RT, CT, 4>(p, nwg, st, tm); return true;
+    case 8: launch_qmm<RT, CT, 8>(p, nwg, st, tm); return true;
     default: return false;
     }
 }
 
-int launch_qgemm(const GemmParams &p, hipStream_t st) {
+int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
     if (p.M < 1 || p.M > 128) throw BackendError("qgemm: M out of range");
     if (p.K % 256) throw BackendError("qgemm: K must be a multiple of 256");
     if (p.mode == GM_SWIGLU && (p.nseg != 2 || p.seg[0].rows != p.seg[1].rows || p.seg[0].fmt != p.seg[1].fmt))
@@ -844,19 +853,19 @@ int launch_qgemm(const GemmParams &p, hipStream_t st) {
     if (ct > 1) {
         if (qgemm_slices(p) > 1 && !p.part) throw BackendError("qgemm: split-K workspace missing");
         const int rw = xg_rw(p);
-        if (rw == 2 && ct == 2) launch_qgx<2, 2>(p, st);
-        else if (rw == 2 && ct == 4) launch_qgx<2, 4>(p, st);
-        else if (rw == 2 && ct == 8) launch_qgx<2, 8>(p, st);
-        else if (rw == 1 && ct == 2) launch_qgx<1, 2>(p, st);
-        else if (rw == 1 && ct == 4) launch_qgx<1, 4>(p, st);
-        else launch_qgx<1, 8>(p, st);
+        if (rw == 2 && ct == 2) launch_qgx<2, 2>(p, st, tm);
+        else if (rw == 2 && ct == 4) launch_qgx<2, 4>(p, st, tm);
+        else if (rw == 2 && ct == 8) launch_qgx<2, 8>(p, st, tm);
+        else if (rw == 1 && ct == 2) launch_qgx<1, 2>(p, st, tm);
+        else if (rw == 1 && ct == 4) launch_qgx<1, 4>(p, st, tm);
+        else launch_qgx<1, 8>(p, st, tm);
         return qgemm_workgroups(p);
     }
     const int kw = qgemm_kw(p), rt = qgemm_rt(p);
     const int nwg = qgemm_workgroups(p);
     bool ok = false;
-    if (rt == 2) ok = launch_kw<2, 1>(p, kw, nwg, st);
-    else if (rt == 1 && p.mode != GM_SWIGLU) ok = launch_kw<1, 1>(p, kw, nwg, st);
+    if (rt == 2) ok = launch_kw<2, 1>(p, kw, nwg, st, tm);
+    else if (rt == 1 && p.mode != GM_SWIGLU) ok = launch_kw<1, 1>(p, kw, nwg, st, tm);
     if (!ok) throw BackendError("qgemm: unsupported launch shape");
     return nwg;
 }

@@ -24,8 +24,13 @@ in + out, per launch).
 
 The CPU baseline times the oracle's C dequant-matmul (f32 dequantisation,
 f64 accumulation, OpenMP over output rows) on a bounded sample of the same
-step -- one Q6_K-mix layer, one Q4_K layer and the lm_head at M=5 -- and
-scales it to a whole verify step (16 layers of each kind + lm_head).
+step -- one Q6_K-mix layer, one Q4_K layer and the lm_head at M=5, repeated
+for about 12 s -- and scales the mean to a whole verify step (16 layers of
+each kind + lm_head).
+
+roofline.traffic is read from profiles/k1_hbm_traffic_llama8b_q4km.json: the
+HBM bytes per launch that rocprofv3's FETCH_SIZE and WRITE_SIZE counters gave
+for this workload, scaled by the same counters on a copy kernel.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -92,6 +97,21 @@ def summarize(prof):
     return out
 
 
+CPU_SAMPLE_S = 12.0
+TRAFFIC_FILE =os.path.join(ROOT, "profiles", "k1_hbm_traffic_llama8b_q4km.json")
+
+
+def measured_traffic(leg: str):
+    """HBM bytes per dequant-matmul launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes over this workload (copy-kernel calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(t[leg]["traffic_bytes_per_launch"]), os.path.relpath(TRAFFIC_FILE, ROOT)
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def cpu_baseline():
     """Oracle CPU dequant-matmul on a bounded sample, scaled to one M=5 verify step."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -104,27 +124,38 @@ def cpu_baseline():
     x = np.random.default_rng(1).standard_normal((5, cfg.ffn)).astype(np.float32)
     L = O.lib()
 
-    def time_matrix(layer, kind):
+    def prepare(layer, kind):
         fmt, raw = O.synth_tensor(cfg, layer, kind)
         N, K = cfg.shape(kind)
-        y = np.empty((5, N), np.float32)
-        xs = np.ascontiguousarray(x[:, :K])
+        return fmt, raw, N, K, np.ascontiguousarray(x[:, :K]), np.empty((5, N), np.float32)
+
+    def run(mats):
         t0 = time.perf_counter()
-        L.or_qmatmul(fmt, O._p(raw), N, K, O._p(xs), 5, O._p(y))
+        for fmt, raw, N, K, xs, y in mats:
+            L.or_qmatmul(fmt, O._p(raw), N, K, O._p(xs), 5, O._p(y))
         return time.perf_counter() - t0
 
     kinds = (O.K_ATTN_Q, O.K_ATTN_K, O.K_ATTN_V, O.K_ATTN_O, O.K_FFN_GATE, O.K_FFN_UP, O.K_FFN_DOWN)
-    t_q6 = sum(time_matrix(0, k) for k in kinds)      # layer 0: Q6_K attn_v / ffn_down
-    log(f"cpu baseline: Q6_K-mix layer {t_q6:.2f} s")
-    t_q4 = sum(time_matrix(4, k) for k in kinds)      # layer 4: all Q4_K
-    log(f"cpu baseline: Q4_K layer {t_q4:.2f} s")
-    t_lm = time_matrix(-1, O.K_OUTPUT)
-    log(f"cpu baseline: lm_head {t_lm:.2f} s")
+    q6 = [prepare(0, k) for k in kinds]   # layer 0: Q6_K attn_v / ffn_down
+    q4 = [prepare(4, k) for k in kinds]   # layer 4: all Q4_K
+    lm = [prepare(-1, O.K_OUTPUT)]
+    # repeat the sample until about 12 s of CPU work, report the mean per repetition
+    reps, t_q6, t_q4, t_lm = 0, 0.0, 0.0, 0.0
+    t_start = time.perf_counter()
+    while reps < 2 or time.perf_counter() - t_start < CPU_SAMPLE_S:
+        t_q6 += run(q6)
+        t_q4 += run(q4)
+        t_lm += run(lm)
+        reps += 1
+    t_q6, t_q4, t_lm = t_q6 / reps, t_q4 / reps, t_lm / reps
+    log(f"cpu baseline: {reps} repetitions; Q6_K-mix layer {t_q6 * 1e3:.1f} ms, Q4_K layer {t_q4 * 1e3:.1f} ms, "
+        f"lm_head {t_lm * 1e3:.1f} ms")
     n_q6 = sum(1 for i in range(cfg.n_layers) if O.use_more_bits(i, cfg.n_layers))
     step_s = n_q6 * t_q6 + (cfg.n_layers - n_q6) * t_q4 + t_lm
     return {"value": round(step_s * 1e6, 1), "unit": "us/verify (M=5)", "cores": threads, "kind": "port",
-            "sample": "oracle C dequant-matmul (f32 dequant, f64 accumulate, OpenMP over rows) at M=5 on one "
-                      "Q6_K-mix layer, one Q4_K layer and the Q4_K lm_head of the same synthetic weights, scaled to "
+            "sample": f"oracle C dequant-matmul (f32 dequant, f64 accumulate, OpenMP over rows) at M=5 on one "
+                      f"Q6_K-mix layer, one Q4_K layer and the Q4_K lm_head of the same synthetic weights, "
+                      f"{reps} repetitions ({time.perf_counter() - t_start:.1f} s), mean scaled to "
                       f"{n_q6}+{cfg.n_layers - n_q6} layers + lm_head; attention and norms not included"}
 
 
@@ -186,6 +217,7 @@ def main():
     achieved = per_launch_bytes / avg_launch_s / 1e9
     step_bytes = gb / args.steps + sum(e[1] for e in prof if e[0] == "attn") / args.steps
     log(f"K1 dequant-matmul: {achieved:.0f} GB/s over {len(gem)} launches")
+    traffic, traffic_src = measured_traffic("m5")
 
     result = {
         "metric": METRIC, "value": round(t_lin * 1e6, 1), "unit": "us", "n_gpus": 1, "steps": args.steps,
@@ -201,9 +233,11 @@ def main():
         "step_hbm_gbps": round(step_bytes / t_lin / 1e9, 1),
         "step_algorithmic_bytes": int(step_bytes),
         "kernels": summarize(prof),
-        "roofline": {"bound": "hbm", "kernel": "k_qgemm (fused dequant-matmul, all 129 launches of a step)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_qmm (K1 fused dequant-matmul for M<=16, all 129 launches of a step)",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "bytes_per_launch": int(per_launch_bytes), "avg_launch_us": round(avg_launch_s * 1e6, 2)},
     }
 
@@ -245,6 +279,10 @@ def main():
                             "tokens_per_s": round((plen / args.steps) / t_tree, 1),
                             "k1_gbps": round(tb / tt / 1e9, 1),
                             "k1_frac": round(tb / tt / 1e9 / PEAK_HBM_GBPS, 4),
+                            "k1_kernel": "k_qgx (K1 for M>16)",
+                            "k1_bytes_per_launch": int(tb / len(tg)),
+                            "k1_avg_launch_us": round(tt / len(tg) * 1e6, 2),
+                            "k1_traffic": measured_traffic("tree60")[0],
                             "kernels": summarize(tprof)}
     dec.close()
 
