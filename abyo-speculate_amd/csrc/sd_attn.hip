@@ -18,13 +18,14 @@
 // are computed transposed, S^T = K Q^T (16 keys x 16 queries per MFMA tile),
 // so a lane's accumulator already holds the P^T operand of O^T = V^T P^T.
 //
-// Grid (kv head, key split, query group).  A workgroup's 4 waves take 4
-// consecutive key ranges of keys_per_wave keys and all query tiles of the
-// group (the n_rep query heads of the KV head times the M tokens, 16 per
-// tile); their partial softmax states are merged in LDS in a fixed order, and
-// the splits by a combine kernel (skipped when one split covers all keys).
+// Grid (kv head, key split, query tile).  A workgroup's 4 waves take 4
+// consecutive key ranges of keys_per_wave keys and one query tile (16 of the
+// n_rep query heads of the KV head times the M tokens); their partial softmax
+// states are merged in LDS in a fixed order, and the splits by a combine
+// kernel (skipped when one split covers all keys).  Up to 16 tokens,
 // keys_per_wave and the split boundaries depend on P only, so a query's
 // result does not depend on how many other queries share the call.
+#include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels_attn.hpp"
 
@@ -88,20 +89,33 @@ template <int HD> struct KvStep {
     uintx4 v[HD / 16];     // O^T A operands: HD/16 d-tiles x 32 key slots
 };
 
-// 32 keys [kk, kk+32) of one stream: 16-byte pieces, 1 KiB per wave each
+// One KV head's K and V streams as buffer resources and the lane's fixed byte
+// offset inside a 32-key block, (r16 * 32 + g * 8) * 2 in both layouts; the
+// block's offset kk * HD * 2 is wave-uniform and goes in a scalar register.
+struct KvSrc {
+    rsrc_t k, v;
+    uint32_t lane;
+};
+// A load that must not happen gets an offset past the resource (a stream is
+// < 2 GiB), which reads zeros without touching memory; loads are then issued
+// unconditionally and the compiler's wait counts stay exact across the loop.
+constexpr uint32_t kNoKv = 0x80000000u;
+__device__ __forceinline__ uint32_t kv_so(int kk, int HD) { return uni(kk < 0 ? kNoKv : (uint32_t)kk * HD * 2u); }
+
+// 32 keys [kk, kk+32) of one stream (kk < 0: none): 16-byte pieces, 1 KiB per wave each
 template <int HD>
-__device__ __forceinline__ void kv_load_k(KvStep<HD> &b, const uint16_t *kb, int kk, int r16, int g) {
+__device__ __forceinline__ void kv_load_k(KvStep<HD> &b, const KvSrc &s, int kk) {
+    const uint32_t so = kv_so(kk, HD);
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-        for (int dc = 0; dc < HD / 32; dc++)
-            b.k[kt][dc] = *(const uintx4 *)(kb + (int64_t)((kk >> 4) + kt) * 16 * HD + dc * 512 + r16 * 32 + g * 8);
+        for (int dc = 0; dc < HD / 32; dc++) b.k[kt][dc] = bld16(s.k, s.lane + kt * 32 * HD + dc * 1024, so);
 }
 template <int HD>
-__device__ __forceinline__ void kv_load_v(KvStep<HD> &b, const uint16_t *vb, int kk, int r16, int g) {
+__device__ __forceinline__ void kv_load_v(KvStep<HD> &b, const KvSrc &s, int kk) {
+    const uint32_t so = kv_so(kk, HD);
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++)
-        b.v[dt] = *(const uintx4 *)(vb + (int64_t)(kk >> 5) * 32 * HD + (dt * 16 + r16) * 32 + g * 8);
+    for (int dt = 0; dt < HD / 16; dt++) b.v[dt] = bld16(s.v, s.lane + dt * 1024, so);
 }
 
 template <int HD, int QT> struct AttnState {
@@ -117,13 +131,21 @@ __device__ __forceinline__ int slot_key(int g, int j) { return j < 4 ? 4 * g + j
 // One 32-key step for all query tiles: scores and softmax first, then the
 // next step's V loads are issued (the current K is dead by then, so the two
 // register buffers never hold four operand sets at once), then O^T += V^T P^T.
+//
+// The running max of a query moves only when a score exceeds it by more than
+// 8 (base 2).  Probabilities exp2(s - m) then stay below 256, which fp16 and
+// f32 hold with full relative precision, and the rescale of the accumulators
+// (a read-modify-write of 32 registers per query tile) is skipped by the whole
+// wave unless one of its queries moved.  The final normalisation divides by
+// the sum taken against the same maxima, so the result is the softmax.
 template <int HD, int QT>
-__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const uint16_t *vb,
-                                          int kk, int k1, int P, int T, float sl2, int r16, int g) {
+__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const KvSrc &src,
+                                          int kk, int k1, int P, int T, float sl2, int g) {
     constexpr int NDC = HD / 32, NDT = HD / 16;
     const bool full = kk + 32 <= P;  // every key of the step is visible to every query
     half8 bp[QT];
     float alpha[QT];
+    bool moved = false;
 #pragma unroll
     for (int t = 0; t < QT; t++) {
         floatx4 st[2];
@@ -155,9 +177,11 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
             }
         cm = fmaxf(cm, __shfl_xor(cm, 16));
         cm = fmaxf(cm, __shfl_xor(cm, 32));
-        const float mnew = fmaxf(S.m[t], cm);
+        const bool up = cm > S.m[t] + 8.f;  // -inf + 8 == -inf: the first finite score always moves it
+        const float mnew = up ? cm : S.m[t];
+        alpha[t] = up ? __builtin_amdgcn_exp2f(S.m[t] - mnew) : 1.f;
+        moved = moved || up;
         const float muse = mnew == -INFINITY ? 0.f : mnew;
-        alpha[t] = exp2f(S.m[t] - muse);
         float ps = 0.f;
         uint32_t pk[4];
 #pragma unroll
@@ -165,7 +189,7 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
             float e[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                e[i] = exp2f(st[kt][i] - muse);
+                e[i] = __builtin_amdgcn_exp2f(st[kt][i] - muse);
                 ps += e[i];
             }
             pk[2 * kt] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
@@ -178,7 +202,7 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
         const uintx4 bu = {pk[0], pk[1], pk[2], pk[3]};
         bp[t] = __builtin_bit_cast(half8, bu);
     }
-    if (kk + 32 < k1) kv_load_v<HD>(nb, vb, kk + 32, r16, g);
+    kv_load_v<HD>(nb, src, kk + 32 < k1 ? kk + 32 : -1);
     if (kk + 32 > T) {
         // keys >= T hold stale cache rows: their P^T entries are 0, and their V
         // entries are zeroed so that nothing but finite values meets the MFMA
@@ -195,18 +219,22 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
             b.v[dt].w &= keep[3];
         }
     }
+    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+        for (int t = 0; t < QT; t++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) S.o[t][dt] *= alpha[t];
+    }
 #pragma unroll
     for (int t = 0; t < QT; t++)
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            S.o[t][dt] *= alpha[t];
+        for (int dt = 0; dt < NDT; dt++)
             S.o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b.v[dt]), bp[t], S.o[t][dt],
                                                                 0, 0, 0);
-        }
 }
 
 template <int HD, int QT>
-__global__ __launch_bounds__(256) void k_attn(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnParams p) {
     constexpr int NDC = HD / 32, NDT = HD / 16;
     const int h = blockIdx.x, s = blockIdx.y, qg = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -215,8 +243,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams p) {
     const int T = p.P + p.M;
     const int k0 = (s * 4 + wave) * p.keys_per_wave;
     const int k1 = min(k0 + p.keys_per_wave, T);
-    const uint16_t *kb = p.kc + (int64_t)h * p.cap * HD;
-    const uint16_t *vb = p.vc + (int64_t)h * p.cap * HD;
+    const uint32_t stream_bytes = (uint32_t)p.cap * HD * 2u;
+    KvSrc src;
+    src.k = make_rsrc(p.kc + (int64_t)h * p.cap * HD, stream_bytes);
+    src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
+    src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
 
     AttnState<HD, QT> S;
 #pragma unroll
@@ -244,17 +275,15 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams p) {
     // (K at the start of a step, V once the step's scores are done)
     KvStep<HD> b0, b1;
     int kk = k0;
-    if (kk < k1) {
-        kv_load_k<HD>(b0, kb, kk, r16, g);
-        kv_load_v<HD>(b0, vb, kk, r16, g);
-    }
+    kv_load_k<HD>(b0, src, kk < k1 ? kk : -1);
+    kv_load_v<HD>(b0, src, kk < k1 ? kk : -1);
     while (kk < k1) {
-        if (kk + 32 < k1) kv_load_k<HD>(b1, kb, kk + 32, r16, g);
-        attn_step<HD, QT>(S, b0, b1, vb, kk, k1, p.P, T, sl2, r16, g);
+        kv_load_k<HD>(b1, src, kk + 32 < k1 ? kk + 32 : -1);
+        attn_step<HD, QT>(S, b0, b1, src, kk, k1, p.P, T, sl2, g);
         kk += 32;
         if (kk >= k1) break;
-        if (kk + 32 < k1) kv_load_k<HD>(b0, kb, kk + 32, r16, g);
-        attn_step<HD, QT>(S, b1, b0, vb, kk, k1, p.P, T, sl2, r16, g);
+        kv_load_k<HD>(b0, src, kk + 32 < k1 ? kk + 32 : -1);
+        attn_step<HD, QT>(S, b1, b0, src, kk, k1, p.P, T, sl2, g);
         kk += 32;
     }
 
@@ -280,7 +309,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams p) {
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const float mw = sml[w][t][r16][0];
-            const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+            const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
             L += sml[w][t][r16][1] * f;
             if (w == wave) fme = f;
         }
@@ -371,39 +400,43 @@ void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
 
 static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
 
-AttnSplit attn_split(int P, int M, int n_kv) {
+// Up to 16 rows (a linear verify or a decode step) the key ranges are a
+// function of P alone, so each row's arithmetic is the same as in a one-row
+// call.  Above, the splits shrink as query tiles grow, towards 2 resident
+// waves per SIMD (512 workgroups of 4 waves).
+AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
     const int target = attn_target_splits(n_kv);
-    int kpw = (P + 1 + 4 * target - 1) / (4 * target);
+    int want = target;
+    if (M > 16) {
+        const int nqt = (M * n_rep + 15) / 16;
+        want = 512 / (n_kv * nqt);
+        want = want < 1 ? 1 : want > target ? target : want;
+    }
+    int kpw = (P + 1 + 4 * want - 1) / (4 * want);
     kpw = kpw < 32 ? 32 : (kpw + 31) / 32 * 32;
     const int T = P + M;
     return AttnSplit{kpw, (T + 4 * kpw - 1) / (4 * kpw)};
 }
 
-// 4 * kpw >= (P + 1) / target and 4 * kpw >= 128 >= M, so
-// nsplit = ceil((P + M) / (4 kpw)) <= target + 1
+// 4 * kpw >= (P + 1) / want, want <= target, and 4 * kpw >= 128 >= M, so
+// nsplit = ceil((P + M) / (4 kpw)) <= target + 2
 int attn_max_splits(int n_kv) { return attn_target_splits(n_kv) + 3; }
-
-template <int HD>
-static void launch_attn_hd(const AttnParams &p, dim3 grid, int qt, hipStream_t st) {
-    if (qt == 1) hipLaunchKernelGGL((k_attn<HD, 1>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((k_attn<HD, 2>), grid, dim3(256), 0, st, p);
-}
 
 void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.keys_per_wave < 32 || p.keys_per_wave % 32) throw BackendError("attention: keys_per_wave");
     if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
     if (p.cap % 32 || (int64_t)p.P + p.M > p.cap) throw BackendError("attention: cache capacity");
     if (p.mask_words < 1 || p.mask_words > 2 || p.M > 64 * p.mask_words) throw BackendError("attention: mask words");
-    // Query tiles per wave: at most 2 (two double-buffered 32-key operand
-    // sets and 2 tiles' accumulators fill the register file).  More query
-    // tiles become more workgroups along z; with the KV head as blockIdx.x
-    // and n_kv a multiple of the 8 XCDs, every workgroup of one head lands on
-    // the same XCD, so the query groups re-read that head's keys from its L2.
+    // One query tile per wave keeps a wave within 256 registers (two
+    // double-buffered 32-key operand sets and its accumulators), so two waves
+    // share each SIMD.  Query tiles become workgroups along z; with the KV head
+    // as blockIdx.x and n_kv a multiple of the 8 XCDs, every workgroup of one
+    // head lands on the same XCD, so the query tiles re-read that head's keys
+    // from its L2.
     const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
-    const int qt = nqt <= 1 ? 1 : 2;
-    const dim3 grid(p.n_kv, p.nsplit, (nqt + qt - 1) / qt);
-    if (p.hd == 128) launch_attn_hd<128>(p, grid, qt, st);
-    else if (p.hd == 64) launch_attn_hd<64>(p, grid, qt, st);
+    const dim3 grid(p.n_kv, p.nsplit, nqt);
+    if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, p);
+    else if (p.hd == 64) hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, p);
     else throw BackendError("attention: head_dim must be 64 or 128");
     if (p.nsplit > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p);
 }

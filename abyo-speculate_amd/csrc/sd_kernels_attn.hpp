@@ -28,7 +28,7 @@ struct AttnSplit {
     int keys_per_wave;  // multiple of 32; a workgroup covers 4 * keys_per_wave keys
     int nsplit;         // workgroups along the keys (for T = P + M keys)
 };
-AttnSplit attn_split(int P, int M, int n_kv);
+AttnSplit attn_split(int P, int M, int n_kv, int n_rep);
 int attn_max_splits(int n_kv);  // upper bound of nsplit over all P, M <= 128
 
 struct AttnParams {

@@ -424,10 +424,42 @@ void Model::qmatmul(int layer, int kind, const float *x, int M, float *y) {
 // matrix kind, or BENCH_QKV / BENCH_GATE_UP for the fused launches of a layer.
 double Model::bench_qmatmul(int layer, int kind, int M, int iters, double *bytes_out) {
     if (M < 1 || M > cfg.max_batch) throw ArgError("M out of range");
-    if (layer < -1 || layer >= cfg.n_layers) throw ArgError("layer out of range");
-    if ((kind == BENCH_QKV || kind == BENCH_GATE_UP) && layer < 0) throw ArgError("fused launches need a layer");
+    if (layer < BENCH_ALL_LAYERS || layer >= cfg.n_layers) throw ArgError("layer out of range");
+    if ((kind == BENCH_QKV || kind == BENCH_GATE_UP) && layer == -1) throw ArgError("fused launches need a layer");
+    if (layer == BENCH_ALL_LAYERS && !(kind == BENCH_QKV || kind == BENCH_GATE_UP || kind == K_ATTN_Q ||
+                                       kind == K_ATTN_K || kind == K_ATTN_V || kind == K_ATTN_O || kind == K_FFN_GATE ||
+                                       kind == K_FFN_UP || kind == K_FFN_DOWN))
+        throw ArgError("cycling over the layers needs a per-layer matrix");
     if (iters < 1) throw ArgError("iters must be positive");
     SD_HIP_CHECK(hipSetDevice(cfg.device));
+    // one launch description per layer when cycling (each launch then reads
+    // weights that the previous launches have not left in the caches)
+    std::vector<GemmParams> ps;
+    double bytes = 0.0;
+    const int l0 = layer == BENCH_ALL_LAYERS ? 0 : layer;
+    const int l1 = layer == BENCH_ALL_LAYERS ? cfg.n_layers : layer + 1;
+    for (int l = l0; l < l1; l++) {
+        double b = 0.0;
+        ps.push_back(bench_params(l, kind, M, &b));
+        bytes += b;
+    }
+    if (bytes_out) *bytes_out = bytes / (double)ps.size();
+    hipEvent_t a, b;
+    SD_HIP_CHECK(hipEventCreate(&a));
+    SD_HIP_CHECK(hipEventCreate(&b));
+    for (auto &p : ps) launch_qgemm(p, st);  // warm
+    SD_HIP_CHECK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) launch_qgemm(ps[i % ps.size()], st);
+    SD_HIP_CHECK(hipEventRecord(b, st));
+    SD_HIP_CHECK(hipEventSynchronize(b));
+    float ms = 0.f;
+    SD_HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return (double)ms * 1e3 / iters;
+}
+
+GemmParams Model::bench_params(int layer, int kind, int M, double *bytes_out) {
     auto &L = lw[layer < 0 ? 0 : layer];
     GemmParams p{};
     gemm_workspace(p);
@@ -472,19 +504,7 @@ double Model::bench_qmatmul(int layer, int kind, int M, int iters, double *bytes
     if (p.K > xp_ld && kind != K_FFN_DOWN) throw ArgError("activation buffer too narrow");
     if (kind == K_FFN_DOWN) p.xp = act;
     if (bytes_out) *bytes_out = gemm_bytes(p, wb);
-    hipEvent_t a, b;
-    SD_HIP_CHECK(hipEventCreate(&a));
-    SD_HIP_CHECK(hipEventCreate(&b));
-    launch_qgemm(p, st);  // warm
-    SD_HIP_CHECK(hipEventRecord(a, st));
-    for (int i = 0; i < iters; i++) launch_qgemm(p, st);
-    SD_HIP_CHECK(hipEventRecord(b, st));
-    SD_HIP_CHECK(hipEventSynchronize(b));
-    float ms = 0.f;
-    SD_HIP_CHECK(hipEventElapsedTime(&ms, a, b));
-    hipEventDestroy(a);
-    hipEventDestroy(b);
-    return (double)ms * 1e3 / iters;
+    return p;
 }
 
 void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P,
@@ -507,7 +527,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
 
     const int H = c.hidden, QD = c.q_dim(), KVD = c.kv_dim(), QKVD = QD + 2 * KVD;
     launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), H, d_ids, M, h, st);
-    const AttnSplit split = attn_split(P, M, c.n_kv_heads);
+    const AttnSplit split = attn_split(P, M, c.n_kv_heads, c.n_heads / c.n_kv_heads);
     if (split.nsplit > nsplit_max) throw BackendError("attention split count exceeds workspace");
     // M > 16 matmuls may leave K-slice partial sums in qg_part for the next
     // kernel to add (rope for QKV, the following RMSNorm for the residual

@@ -98,8 +98,9 @@ class Model {
     // raw matmul (test entry): y[M][N] = x[M][K] . W^T (x rounded to fp16)
     void qmatmul(int layer, int kind, const float *x, int M, float *y);
     // microbenchmark of one dequant-matmul launch: microseconds per launch
-    enum { BENCH_QKV = 100, BENCH_GATE_UP = 101 };
+    enum { BENCH_QKV = 100, BENCH_GATE_UP = 101, BENCH_ALL_LAYERS = -2 };
     double bench_qmatmul(int layer, int kind, int M, int iters, double *bytes_out);
+    GemmParams bench_params(int layer, int kind, int M, double *bytes_out);
 
     // forward of M tokens at cache positions [P, P+M); mask words per token.
     // logits_mode: 0 none, 1 last row only (into logits row 0), 2 all rows.

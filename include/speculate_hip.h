@@ -248,8 +248,11 @@ sd_status sd_synchronize(sd_model *m);
  * matrix kind, SD_BENCH_QKV (fused Q/K/V) or SD_BENCH_GATE_UP (fused gate/up +
  * SiLU), at `rows` activation rows; *us = mean microseconds per launch over
  * `iters` back-to-back launches timed with HIP events, *bytes = algorithmic
- * bytes per launch (weight blocks + activations in + outputs). */
-enum { SD_BENCH_QKV = 100, SD_BENCH_GATE_UP = 101 };
+ * bytes per launch (weight blocks + activations in + outputs).  layer =
+ * SD_BENCH_ALL_LAYERS cycles the launches over every layer's matrix, so each
+ * launch streams weights the previous ones did not leave in the caches (the
+ * situation inside a forward pass). */
+enum { SD_BENCH_QKV = 100, SD_BENCH_GATE_UP = 101, SD_BENCH_ALL_LAYERS = -2 };
 sd_status sd_bench_qmatmul(sd_model *m, int32_t layer, int32_t kind, size_t rows, int32_t iters, double *us,
                            double *bytes);
 /* Copies n fp16 cache rows [pos0, pos0+n) of one (layer, K=0/V=1, kv head):
