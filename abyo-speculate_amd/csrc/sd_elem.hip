@@ -103,6 +103,35 @@ __global__ __launch_bounds__(256) void k_rmsnorm_any(float *x, const float *w, i
     }
 }
 
+// Input of a matmul with the RMSNorm fused into it (M <= 16): u = fp16(x * w)
+// in fragment order and, per 16-element tile, the sum of x^2 (the matmul's
+// epilogue applies 1 / sqrt(sum / K + eps)).  grid M, block 256; K % 16 == 0.
+__global__ __launch_bounds__(256) void k_norm_u(const float *x, const float *w, int K, uint16_t *out16, int ld16,
+                                                float *ssq) {
+    const int m = blockIdx.x;
+    const float *row = x + (int64_t)m * K;
+    for (int t = threadIdx.x; t < K / 16; t += 256) {
+        float4 v[4], wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j] = ((const float4 *)(row + 16 * t))[j];
+            wv[j] = ((const float4 *)(w + 16 * t))[j];
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+            const int k = 16 * t + 4 * j;
+            uint16_t *dst = out16 + (int64_t)m * ld16 + frag_index(k);  // slots of k, k+2, k+1, k+3
+            dst[0] = f2h(v[j].x * wv[j].x);
+            dst[1] = f2h(v[j].z * wv[j].z);
+            dst[2] = f2h(v[j].y * wv[j].y);
+            dst[3] = f2h(v[j].w * wv[j].w);
+        }
+        ssq[(int64_t)m * (K / 16) + t] = s;
+    }
+}
+
 // f32 rows -> fp16 fragment layout (hidden states handed to apply_lm_head)
 __global__ void k_to_frag16(const float *x, int K, uint16_t *out16, int ld16) {
     const int m = blockIdx.y;
@@ -221,6 +250,11 @@ void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t 
     default: SD_RMS(k_rmsnorm_any); break;
     }
 #undef SD_RMS
+}
+void launch_norm_u(const float *x, const float *w, int M, int K, uint16_t *out16, int ld16, float *ssq,
+                   hipStream_t st) {
+    if (K % 16) throw BackendError("norm_u: K must be a multiple of 16");
+    hipLaunchKernelGGL(k_norm_u, dim3(M), dim3(256), 0, st, x, w, K, out16, ld16, ssq);
 }
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st) {
     hipLaunchKernelGGL(k_to_frag16, dim3((K + 255) / 256, M), dim3(256), 0, st, x, K, out16, ld16);

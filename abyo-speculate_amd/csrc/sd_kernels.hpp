@@ -38,6 +38,20 @@ struct GemmSeg {
     const float *bias; // optional per-row bias (GM_STORE)
 };
 
+// RoPE and KV append in the epilogue of the fused Q/K/V launch (M <= 16):
+// the launch's columns are q (n_heads heads) | k (n_kv) | v (n_kv), hd each.
+// Rotated q goes to q16[head][M][hd] (fp16), rotated k and v to the layer's
+// cache streams at position P + m (blocked layout, kv_k_off / kv_v_off).
+struct RopeOut {
+    const int *pos;              // [M] absolute positions
+    const float *cos_t, *sin_t;  // [ctx][hd/2]
+    uint16_t *q16;
+    uint16_t *kc, *vc;
+    int64_t cap;
+    int P, n_heads, n_kv, hd;
+    int interleaved;             // 1: pairs (2i, 2i+1); 0: pairs (i, i + hd/2)
+};
+
 struct GemmParams {
     GemmSeg seg[4];
     int nseg;
@@ -57,6 +71,23 @@ struct GemmParams {
     int allow_split;
     float *part;
     int64_t part_cap;        // floats
+    // ---- M <= 16 fused RMSNorm (RmsNorm::forward applied around the matmul) ----
+    // Input side (norm_ssq set): the activations are u = fp16(h * w_norm) and
+    // every output of token m is scaled by 1 / sqrt(S_m / K + norm_eps), with
+    // S_m = sum over t < norm_parts of norm_ssq[m * norm_parts + t] (sum of h^2).
+    const float *norm_ssq;
+    int norm_parts;
+    float norm_eps;
+    // Output side (GM_RESID, next_w set): with the new residual row h also
+    // next_u[m][frag(n)] = fp16(h[n] * next_w[n]) and, for each 16-row tile,
+    // next_ssq[m * ntiles + tile] = sum of h^2 over the tile: the input of the
+    // next normalised matmul.
+    const float *next_w;
+    uint16_t *next_u;
+    int next_ld;
+    float *next_ssq;
+    // GM_STORE with rope.q16 set: RoPE + KV append instead of storing the output
+    RopeOut rope;
 };
 
 // Optional timing of one launch: with both events set the kernel goes through

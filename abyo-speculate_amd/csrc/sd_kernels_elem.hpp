@@ -15,6 +15,10 @@ void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, f
 void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
                     hipStream_t st, const float *part = nullptr, int nks = 1);
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st);
+// u = fp16(x * w) in fragment order + per-16-element sums of x^2 (ssq [M][K/16])
+// for a matmul with the RMSNorm fused into its epilogue
+void launch_norm_u(const float *x, const float *w, int M, int K, uint16_t *out16, int ld16, float *ssq,
+                   hipStream_t st);
 void launch_argmax_reduce(const float *pv, const int *pi, int nwg, int M, int *out, hipStream_t st);
 void launch_argmax_rows(const float *x, int64_t ld, int n, int M, int *out, hipStream_t st);
 void launch_keep_kv_tail(uint16_t *kv, int nstreams, int64_t stream_stride, int n_kv, int hd, int P, const int *src,

@@ -131,6 +131,7 @@ void Model::alloc_buffers() {
     d_mask = dalloc<uint64_t>((size_t)Mx * 2);
     qg_part_cap = std::max<int64_t>((int64_t)8 * Mx * std::max(qkvd, c.hidden), (int64_t)2 * Mx * 2 * c.ffn);
     qg_part = dalloc<float>((size_t)qg_part_cap);
+    ssq = dalloc<float>((size_t)16 * (c.hidden / 16));
     acc_m = dalloc<float>(Mx);
     acc_s = dalloc<float>(Mx);
     acc_am = dalloc<int>(Mx);
@@ -534,9 +535,18 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     // matmuls); not while per-layer hidden states are collected
     const int split_ok = collect.empty() ? 1 : 0;
     int pend = 1;  // K slices of the last residual matmul not yet added to h
+    // Up to 16 rows the RMSNorms and RoPE live in the matmul epilogues: the
+    // residual matmuls (wo, ffn_down) also write u = fp16(h * w_next_norm)
+    // and per-tile sums of h^2, the next matmul scales its outputs by
+    // 1/rms, and the fused Q/K/V launch rotates q, k and appends k, v to the
+    // cache.  Nine launches per layer become five (four with one key split).
+    const bool fused = M <= 16 && H % 256 == 0 && H / 16 <= 256 && (c.head_dim == 64 || c.head_dim == 128);
+    const int np = H / 16;
+    if (fused) launch_norm_u(h, (const float *)lw[0][K_ATTN_NORM].d, M, H, xp, xp_ld, ssq, st);
     for (int l = 0; l < c.n_layers; l++) {
         auto &L = lw[l];
-        launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
+        if (!fused)
+            launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         int nks_qkv;
         {
             GemmParams p{};
@@ -556,6 +566,24 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.M = M;
             p.mode = GM_STORE;
             p.allow_split = split_ok;
+            if (fused) {
+                p.norm_ssq = ssq;
+                p.norm_parts = np;
+                p.norm_eps = c.rms_eps;
+                RopeOut &R = p.rope;
+                R.pos = d_pos;
+                R.cos_t = cos_t;
+                R.sin_t = sin_t;
+                R.q16 = q16;
+                R.kc = kc(l);
+                R.vc = vc(l);
+                R.cap = cap;
+                R.P = P;
+                R.n_heads = c.n_heads;
+                R.n_kv = c.n_kv_heads;
+                R.hd = c.head_dim;
+                R.interleaved = c.arch == 0;
+            }
             run_gemm(p, PC_QKV, wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
             nks_qkv = qgemm_slices(p);
         }
@@ -583,7 +611,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 r.bk = (const float *)L[K_BK].d;
                 r.bv = (const float *)L[K_BV].d;
             }
-            launch_rope_kv(r, st);
+            if (!fused) launch_rope_kv(r, st);
             AttnParams a{};
             a.q16 = q16;
             a.kc = kc(l);
@@ -625,10 +653,17 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.M = M;
             p.mode = GM_RESID;
             p.allow_split = split_ok;
+            if (fused) {
+                p.next_w = (const float *)L[K_FFN_NORM].d;
+                p.next_u = xp;
+                p.next_ld = xp_ld;
+                p.next_ssq = ssq;
+            }
             run_gemm(p, PC_WO, wbytes(L[K_ATTN_O]));
             pend = qgemm_slices(p);
         }
-        launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
+        if (!fused)
+            launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         {
             GemmParams p{};
             gemm_workspace(p);
@@ -642,6 +677,11 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.mode = GM_SWIGLU;
             p.act = act;
             p.act_ld = act_ld;
+            if (fused) {
+                p.norm_ssq = ssq;
+                p.norm_parts = np;
+                p.norm_eps = c.rms_eps;
+            }
             if (L[K_FFN_GATE].fmt != L[K_FFN_UP].fmt) throw UnsupportedError("ffn_gate and ffn_up must share a format");
             run_gemm(p, PC_GATE_UP, wbytes(L[K_FFN_GATE]) + wbytes(L[K_FFN_UP]));
         }
@@ -656,6 +696,12 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.M = M;
             p.mode = GM_RESID;
             p.allow_split = split_ok;
+            if (fused) {
+                p.next_w = (const float *)(l + 1 < c.n_layers ? lw[l + 1][K_ATTN_NORM] : gw[K_OUTPUT_NORM]).d;
+                p.next_u = xp;
+                p.next_ld = xp_ld;
+                p.next_ssq = ssq;
+            }
             run_gemm(p, PC_DOWN, wbytes(L[K_FFN_DOWN]));
             pend = qgemm_slices(p);
         }
@@ -664,8 +710,11 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 SD_HIP_CHECK(hipMemcpyAsync(collect_buf + ci * H, h + (size_t)(M - 1) * H, H * 4,
                                             hipMemcpyDeviceToDevice, st));
     }
-    launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, xp, xp_ld, want_hidden ? hidden_out : nullptr,
-                   st, qg_part, pend);
+    if (!fused)
+        launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, xp, xp_ld,
+                       want_hidden ? hidden_out : nullptr, st, qg_part, pend);
+    else if (want_hidden)  // the final-norm hidden rows only; the lm_head input is already in xp
+        launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, nullptr, 0, hidden_out, st);
     logits_rows_last = 0;
     if (logits_mode != 0) {
         const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
@@ -681,6 +730,11 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         p.mode = GM_LOGITS;
         p.amax_v = amax_v;
         p.amax_i = amax_i;
+        if (fused) {
+            p.norm_ssq = ssq + (logits_mode == 1 ? (size_t)(M - 1) * np : 0);
+            p.norm_parts = np;
+            p.norm_eps = c.rms_eps;
+        }
         if (xp_ld != H) throw UnsupportedError("lm_head needs hidden == q_dim activations stride");
         p.amax_ld = qgemm_workgroups(p);
         if (p.amax_ld > amax_ld) throw BackendError("argmax workspace too small");

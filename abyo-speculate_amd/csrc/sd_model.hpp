@@ -132,6 +132,8 @@ class Model {
     // split-K partial sums of the M > 16 matmul (see GemmParams::allow_split)
     float *qg_part = nullptr;
     int64_t qg_part_cap = 0;
+    // fused RMSNorm (M <= 16): per-16-row-tile sums of h^2, [16][hidden / 16]
+    float *ssq = nullptr;
     void gemm_workspace(GemmParams &p) const {
         p.part = qg_part;
         p.part_cap = qg_part_cap;

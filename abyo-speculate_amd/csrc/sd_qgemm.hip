@@ -222,10 +222,136 @@ __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)
 // gate tiles and [RT/2, RT) the up tiles of the same features.  GM_LOGITS also
 // writes the tiles' argmax partial of every token (first max wins) to `slot`.
 // --------------------------------------------------------------------------
+// four fp16 values to one 8-byte store
+__device__ __forceinline__ void st4h(uint16_t *dst, float a, float b, float c, float d) {
+    *(uintx2 *)dst = uintx2{(uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16), (uint32_t)f2h(c) | ((uint32_t)f2h(d) << 16)};
+}
+
+// Operands the epilogue reads besides the accumulators, requested when the
+// kernel starts so that they arrive during the main loop instead of costing a
+// memory round trip after it: the residual rows (GM_RESID), the next norm's
+// weights, the bias and, for RoPE, the position and its cos/sin entries.
+template <int RT> struct EpiPre {
+    floatx4 o[RT], w[RT], b[RT];
+    int pos;
+    float cs[4], sn[4];
+};
+
+// RoPE geometry of a lane (RT == 2): tile 0 holds elements d..d+3 of a head
+// (d < hd/2), tile 1 elements d+hd/2..; which = 0 q, 1 k, 2 v
+struct RopeLane {
+    int which, head, d;
+};
+template <int RT>
+__device__ __forceinline__ RopeLane rope_lane(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
+                                              int g) {
+    const RopeOut &R = p.rope;
+    const int qd = R.n_heads * R.hd, kvd = R.n_kv * R.hd;
+    const int col = S[0].col0 + rloc[0] + 4 * g;
+    RopeLane L;
+    L.which = col < qd ? 0 : col < qd + kvd ? 1 : 2;
+    const int rel = col - (L.which == 0 ? 0 : L.which == 1 ? qd : qd + kvd);
+    L.head = rel / R.hd;
+    L.d = rel % R.hd;
+    return L;
+}
+
+// all loads unconditional (padding tokens read the last real token's data)
+template <int RT>
+__device__ __forceinline__ void epi_prefetch(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
+                                             int m, int g, EpiPre<RT> &e) {
+    const int ml = min(m, p.M - 1);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int n0 = rloc[rt] + 4 * g;
+        if (p.mode == GM_RESID) e.o[rt] = *(const floatx4 *)(S[rt].out + (int64_t)ml * S[rt].ldo + S[rt].col0 + n0);
+        if (p.next_w) e.w[rt] = *(const floatx4 *)(p.next_w + S[rt].col0 + n0);
+        if (S[rt].bias) e.b[rt] = *(const floatx4 *)(S[rt].bias + n0);
+    }
+    if (p.rope.q16) e.pos = p.rope.pos[ml];
+}
+// after the position has arrived (called once the weight prologue is in flight)
+template <int RT>
+__device__ __forceinline__ void epi_prefetch_rope(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
+                                                  int g, EpiPre<RT> &e) {
+    if (!p.rope.q16) return;
+    const RopeOut &R = p.rope;
+    const RopeLane L = rope_lane<RT>(p, S, rloc, g);
+    const int half = R.hd / 2;
+    const float *ct = R.cos_t + (int64_t)e.pos * half, *sn = R.sin_t + (int64_t)e.pos * half;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // rope_i: pair index (d + rt * hd/2 + 2j) / 2 for slot i = 2 rt + j; rope: d + i
+        const int f = R.interleaved ? (L.d + (i >> 1) * half + 2 * (i & 1)) >> 1 : L.d + i;
+        e.cs[i] = ct[f];
+        e.sn[i] = sn[f];
+    }
+}
+
+// RoPE + KV append of one lane's rows (RT == 2).  Rotation as
+// LayerWeights::rope_at_positions (quantized_llama_local.rs:94-105,
+// quantized_qwen2_local.rs:98-109): (x0 c - x1 s, x0 s + x1 c) on the pairs
+// (2i, 2i+1) inside a tile (rope_i) or (i, i + hd/2) across the two (rope).
+template <int RT>
+__device__ __forceinline__ void rope_epilogue(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
+                                              const floatx4 (&v)[RT], const EpiPre<RT> &e, int m, int g) {
+    if constexpr (RT == 2) {
+        const RopeOut &R = p.rope;
+        const int hd = R.hd, half = hd / 2;
+        const RopeLane L = rope_lane<RT>(p, S, rloc, g);
+        float x[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            floatx4 r = v[rt];
+            if (S[rt].bias) r += e.b[rt];
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[rt][i] = r[i];
+        }
+        const int64_t t = (int64_t)R.P + m;
+        if (L.which < 2) {
+            float y[2][4];
+            if (R.interleaved) {
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2) {
+                        const float c = e.cs[2 * rt + i / 2], s = e.sn[2 * rt + i / 2];
+                        y[rt][i] = x[rt][i] * c - x[rt][i + 1] * s;
+                        y[rt][i + 1] = x[rt][i] * s + x[rt][i + 1] * c;
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float c = e.cs[i], s = e.sn[i];
+                    y[0][i] = x[0][i] * c - x[1][i] * s;
+                    y[1][i] = x[0][i] * s + x[1][i] * c;
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const int dd = L.d + rt * half;
+                uint16_t *dst = L.which == 0 ? R.q16 + ((int64_t)L.head * p.M + m) * hd + dd
+                                             : R.kc + (int64_t)L.head * R.cap * hd + kv_k_off(t, dd, hd);
+                st4h(dst, y[rt][0], y[rt][1], y[rt][2], y[rt][3]);
+            }
+        } else {
+            uint16_t *vs = R.vc + (int64_t)L.head * R.cap * hd;
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) vs[kv_v_off(t, L.d + rt * half + i, hd)] = f2h(x[rt][i]);
+        }
+    }
+}
+
 template <int RT>
 __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
-                                         const floatx4 (&v)[RT], int m, int g, int slot) {
+                                         const floatx4 (&v)[RT], const EpiPre<RT> &e, int m, int g, int slot) {
     const bool live = m < p.M;
+    if (p.rope.q16) {
+        if (live) rope_epilogue<RT>(p, S, rloc, v, e, m, g);
+        return;
+    }
     if (p.mode == GM_SWIGLU) {
         if (live) {
             uint16_t *dst = p.act + (int64_t)m * p.act_ld;
@@ -240,18 +366,28 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)
     }
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    float ss[RT];  // next_w: this lane's share of the tile's sum of squares
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
+        ss[rt] = 0.f;
         if (!live) continue;
         const int n0 = rloc[rt] + 4 * g;
         float *o = S[rt].out + (int64_t)m * S[rt].ldo + S[rt].col0 + n0;
         floatx4 r = v[rt];
         if (p.mode == GM_RESID) {
-            r += *(floatx4 *)o;
+            r += e.o[rt];
         } else if (S[rt].bias) {
-            r += *(const floatx4 *)(S[rt].bias + n0);
+            r += e.b[rt];
         }
         *(floatx4 *)o = r;
+        if (p.next_w) {
+            // features n .. n+3 sit in fragment slots f, f+2, f+1, f+3 (frag_slot)
+            const int n = S[rt].col0 + n0;
+            const floatx4 w = e.w[rt];
+            st4h(p.next_u + (int64_t)m * p.next_ld + frag_index(n), r[0] * w[0], r[2] * w[2], r[1] * w[1],
+                 r[3] * w[3]);
+            ss[rt] = (r[0] * r[0] + r[1] * r[1]) + (r[2] * r[2] + r[3] * r[3]);
+        }
         if (p.mode == GM_LOGITS) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -262,6 +398,16 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)
                     bi = idx;
                 }
             }
+        }
+    }
+    if (p.next_w) {
+        // per tile: the 4 lanes of a token (g = 0..3) add their rows in a fixed order
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            float s = ss[rt];
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (g == 0 && live) p.next_ssq[(int64_t)m * p.ntiles + (S[rt].col0 + rloc[rt]) / 16] = s;
         }
     }
     if (p.mode == GM_LOGITS) {
@@ -368,9 +514,42 @@ __device__ __forceinline__ void load_x(uintx4 (&b)[CT][8], rsrc_t xr, const uint
 // measured equal on the verify shapes, and 2 leaves registers to spare.
 constexpr int kDepth1 = 2;
 
-// Superblocks sb = ks, ks + KW, ... in increasing order.
-template <int FMT, int RT, int CT, int KW>
-__device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT][CT]) {
+// ---- fused RMSNorm, input side ------------------------------------------------
+// The sums of squares of token m arrive as norm_parts partials (one per
+// 16-row tile of the residual matmul that produced h, or of the RMSNorm
+// kernel).  Lane (r16, g) adds the quarter g of token r16's partials, the four
+// quarters meet by xor-shuffles: the same fixed order in every workgroup.  The
+// loads are issued before the weight prologue and consumed after it, so
+// waiting for them does not wait for the weights (loads retire in order).
+constexpr int kNormMaxParts = 256;  // hidden <= 4096
+struct NormLoads {
+    floatx4 v[kNormMaxParts / 16];
+};
+__device__ __forceinline__ void norm_issue(const GemmParams &p, NormLoads &nl) {
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
+    const int np = p.norm_parts;
+    // no norm: an empty resource, every load reads zero without a memory access
+    const rsrc_t r = make_rsrc(p.norm_ssq, p.norm_ssq ? (uint32_t)(p.M * np * 4) : 0u);
+    const int m = min(r16, p.M - 1);
+    const uint32_t vo = (uint32_t)(m * np + g * (np / 4)) * 4u;
+#pragma unroll
+    for (int j = 0; j < kNormMaxParts / 16; j++)
+        nl.v[j] = __builtin_bit_cast(floatx4, bld16(r, vo + 16u * j, uni(16 * j < np ? 0u : kNoLoad)));
+}
+__device__ __forceinline__ float norm_finish(const GemmParams &p, const NormLoads &nl) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormMaxParts / 16; j++) s += (nl.v[j].x + nl.v[j].y) + (nl.v[j].z + nl.v[j].w);
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    return p.norm_ssq ? 1.0f / sqrtf(s / (float)p.K + p.norm_eps) : 1.0f;
+}
+
+// Superblocks sb = ks, ks + KW, ... in increasing order;
+// `after_prologue` runs once the first superblock's loads are in flight.
+template <int FMT, int RT, int CT, int KW, typename Hook>
+__device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT][CT],
+                                         Hook &&after_prologue) {
     typedef QFmt<FMT> F;
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
@@ -391,6 +570,7 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
         load_x<1>(b0, xr, xvo, sbi(0));
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        after_prologue();
         for (int i = 0;; i += 2) {
             load_x<1>(b1, xr, xvo, sbi(i + 1));
 #pragma unroll
@@ -415,6 +595,7 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
         load_x<1>(b1, xr, xvo, sbi(1));
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(1), g);
+        after_prologue();
         for (int i = 0;; i += 3) {
             load_x<1>(b2, xr, xvo, sbi(i + 2));
 #pragma unroll
@@ -438,6 +619,7 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
         uintx4 b[CT][8];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        after_prologue();
         for (int i = 0;; i += 2) {
             load_x<CT>(b, xr, xvo, sbi(i));
 #pragma unroll
@@ -468,13 +650,21 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
             rloc[rt] = (f0 + rt % (RT / 2)) * 16;
         }
     } else {
-        // RT consecutive tiles of one segment (segment sizes are multiples of RT)
-        const int t0 = (int)blockIdx.x * RT;
+        // RT consecutive tiles of one segment (segment sizes are multiples of
+        // RT).  With RoPE in the epilogue (RT == 2) the pair is instead tiles j
+        // and j + hd/32 of one head, so the lane holding element d of a head
+        // also holds d + hd/2, the partner of the half rotation.
+        int t0 = (int)blockIdx.x * RT, tstep = 1;
+        if (RT == 2 && p.rope.q16) {
+            const int half = p.rope.hd / 32;
+            t0 = ((int)blockIdx.x / half) * 2 * half + (int)blockIdx.x % half;
+            tstep = half;
+        }
         const GemmSeg s = seg_of_tile(p, t0);
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             S[rt] = s;
-            rloc[rt] = (t0 - s.tile0 + rt) * 16;
+            rloc[rt] = (t0 - s.tile0 + rt * tstep) * 16;
         }
     }
     WRow row[RT];
@@ -485,11 +675,27 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Wave 0 runs the epilogue: it requests the epilogue's operands and the
+    // fused-norm sums first, and consumes the sums (and requests the RoPE
+    // table entries, which need the position) once its weights are in flight.
+    float inv = 1.0f;  // fused RMSNorm scale of this lane's token
+    EpiPre<RT> e;
+    NormLoads nl;
+    if (wave == 0) {
+        epi_prefetch<RT>(p, S, rloc, r16, g, e);
+        norm_issue(p, nl);
+    }
+    auto after_prologue = [&]() {
+        if (wave == 0) {
+            inv = norm_finish(p, nl);
+            epi_prefetch_rope<RT>(p, S, rloc, g, e);
+        }
+    };
     switch (S[0].fmt) {
-    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc); break;
-    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc); break;
-    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc); break;
-    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc); break;
+    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
+    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
+    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
+    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
     default: break;
     }
     // fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, one
@@ -515,7 +721,9 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) v[rt] = acc[rt][ct];
         }
-        epilogue<RT>(p, S, rloc, v, ct * 16 + r16, g, (int)blockIdx.x);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
+        epilogue<RT>(p, S, rloc, v, e, ct * 16 + r16, g, (int)blockIdx.x);
     }
 }
 
@@ -683,7 +891,9 @@ __global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
             floatx4 v[RW];
 #pragma unroll
             for (int rt = 0; rt < RW; rt++) v[rt] = acc[rt][ct];
-            epilogue<RW>(p, S, rloc, v, ct * 16 + r16, g, slot);
+            EpiPre<RW> e;
+            epi_prefetch<RW>(p, S, rloc, ct * 16 + r16, g, e);
+            epilogue<RW>(p, S, rloc, v, e, ct * 16 + r16, g, slot);
         }
         return;
     }
@@ -723,7 +933,10 @@ static int total_rows(const GemmParams &p) {
 // as 2 tiles per wave and >= 1024 waves (measured on MI355X; a wave's start-up
 // latency is paid once per K range, so few long waves beat many short ones
 // once the grid covers the chip).
-static int policy_rt(const GemmParams &p) { return p.mode == GM_SWIGLU ? 2 : total_rows(p) <= 4096 ? 1 : 2; }
+static int policy_rt(const GemmParams &p) {
+    if (p.mode == GM_SWIGLU || p.rope.q16) return 2;  // gate/up pairs; RoPE pairs (j, j + hd/32)
+    return total_rows(p) <= 4096 ? 1 : 2;
+}
 
 int qgemm_kw(const GemmParams &p) {
     const int nsb = p.K / 256;
@@ -820,6 +1033,21 @@ int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
         for (int i = 1; i < p.nseg; i++)
             if (p.seg[i].tile0 != p.seg[i - 1].tile0 + p.seg[i - 1].rows / 16)
                 throw BackendError("qgemm: segments must be consecutive");
+    // the fused RMSNorm and RoPE epilogues exist in the M <= 16 kernel only
+    if ((p.norm_ssq || p.next_w || p.rope.q16) && p.M > 16) throw BackendError("qgemm: fused epilogues need M <= 16");
+    if (p.norm_ssq && (p.norm_parts < 16 || p.norm_parts > 256 || p.norm_parts % 16))
+        throw BackendError("qgemm: norm partial count");
+    if (p.next_w && (p.mode != GM_RESID || !p.next_u || !p.next_ssq)) throw BackendError("qgemm: next-norm outputs");
+    if (p.rope.q16) {
+        const RopeOut &R = p.rope;
+        if (p.mode != GM_STORE || p.nseg != 3 || (R.hd != 64 && R.hd != 128))
+            throw BackendError("qgemm: RoPE epilogue needs the fused Q/K/V launch");
+        if (p.seg[0].rows != R.n_heads * R.hd || p.seg[1].rows != R.n_kv * R.hd || p.seg[2].rows != R.n_kv * R.hd)
+            throw BackendError("qgemm: RoPE head layout");
+        if (p.seg[1].col0 != p.seg[0].rows || p.seg[2].col0 != p.seg[0].rows + p.seg[1].rows || p.seg[0].col0 != 0)
+            throw BackendError("qgemm: RoPE column layout");
+        if (R.cap % 32 || (int64_t)R.P + p.M > R.cap) throw BackendError("qgemm: RoPE cache capacity");
+    }
     const int ct = token_tiles(p.M);
     if (ct > 1) {
         if (qgemm_slices(p) > 1 && !p.part) throw BackendError("qgemm: split-K workspace missing");
