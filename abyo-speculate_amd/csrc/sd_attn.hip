@@ -128,97 +128,133 @@ template <int HD, int QT> struct AttnState {
 // key of P^T / V^T slot j (0..7) of lane group g within a 32-key step
 __device__ __forceinline__ int slot_key(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
 
-// One 32-key step for all query tiles: scores and softmax first, then the
-// next step's V loads are issued (the current K is dead by then, so the two
-// register buffers never hold four operand sets at once), then O^T += V^T P^T.
-//
-// The running max of a query moves only when a score exceeds it by more than
-// 8 (base 2).  Probabilities exp2(s - m) then stay below 256, which fp16 and
-// f32 hold with full relative precision, and the rescale of the accumulators
-// (a read-modify-write of 32 registers per query tile) is skipped by the whole
-// wave unless one of its queries moved.  The final normalisation divides by
-// the sum taken against the same maxima, so the result is the softmax.
+// The 4 lanes of one query (lane groups g = 0..3 of a 16x16 MFMA layout)
+// combined with lane ^ 16 and lane ^ 32: two VALU swaps instead of LDS
+// permutes.  Every lane ends with the same value (the operations commute).
+__device__ __forceinline__ float xmax4(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xsum4(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Query fragment of lane (r16 = query row, g): 8 dims of dc-chunk, scaled by
+// scale * log2(e) so that scores come out in base-2 softmax units.
 template <int HD, int QT>
-__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const KvSrc &src,
-                                          int kk, int k1, int P, int T, float sl2, int g) {
-    constexpr int NDC = HD / 32, NDT = HD / 16;
-    const bool full = kk + 32 <= P;  // every key of the step is visible to every query
-    half8 bp[QT];
-    float alpha[QT];
-    bool moved = false;
+__device__ __forceinline__ void load_query(AttnState<HD, QT> &S, int t, const AttnParams &p, int h, int q, int g,
+                                           float sl2) {
+    constexpr int NDC = HD / 32;
+    const int nq = p.M * p.n_rep;
+    const bool live = q < nq;
+    const int m = live ? q / p.n_rep : 0, r = live ? q % p.n_rep : 0;
+    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + r) * p.M + m) * HD;
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
-        floatx4 st[2];
+    for (int dc = 0; dc < NDC; dc++) {
+        half8 v = half8{};
+        if (live) v = __builtin_bit_cast(half8, *(const uintx4 *)(qr + dc * 32 + g * 8));
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 8; i++) v[i] = (_Float16)((float)v[i] * sl2);
+        S.qf[t][dc] = v;
+    }
+    S.mk0[t] = p.mask[(int64_t)m * p.mask_words];
+    S.mk1[t] = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
 #pragma unroll
-            for (int dc = 0; dc < NDC; dc++)
-                st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b.k[kt][dc]), S.qf[t][dc],
-                                                                st[kt], 0, 0, 0);
-        }
-        float cm = -INFINITY;
+    for (int dt = 0; dt < HD / 16; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    S.m[t] = -INFINITY;
+    S.l[t] = 0.f;
+}
+
+// Softmax of one 32-key step for query tile t: st holds the lane's 8 scores
+// (keys kk + 16 kt + 4g + i) in base-2 units; returns the P^T fragment.
+//
+// The running max m of a query (the same in its 4 lanes) moves only when a
+// score exceeds it by more than 8: probabilities exp2(s - m) then stay below
+// 256, which fp16 and f32 hold with full relative precision.  Each lane keeps
+// its own partial sum l of the probabilities it produced; the 4 partials of a
+// query are added once, at the end.  So the common step has no cross-lane
+// traffic at all: the max is only gathered (and the accumulators rescaled by
+// alpha) when some lane of the wave sees a score above its m + 8.
+// Keys at or past lim (<= T) belong to another range and are masked.
+template <int HD, int QT>
+__device__ __forceinline__ half8 step_softmax(AttnState<HD, QT> &S, int t, floatx4 (&st)[2], int kk, int P, int T,
+                                              int lim, int g, float &alpha, bool &moved) {
+    const bool full = kk + 32 <= P && kk + 32 <= lim;  // every key of the step is visible to every query
+    float lmax = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float v = st[kt][i] * sl2;
-                if (!full) {
-                    const int key = kk + kt * 16 + 4 * g + i;
-                    bool vis = key < P;
-                    if (!vis && key < T) {
-                        const int tt = key - P;
-                        vis = (((tt < 64 ? S.mk0[t] : S.mk1[t]) >> (tt & 63)) & 1ull) != 0;
-                    }
-                    v = vis ? v : -INFINITY;
+        for (int i = 0; i < 4; i++) {
+            float v = st[kt][i];
+            if (!full) {
+                const int key = kk + kt * 16 + 4 * g + i;
+                bool vis = key < P && key < lim;
+                if (!vis && key < lim) {
+                    const int tt = key - P;
+                    vis = (((tt < 64 ? S.mk0[t] : S.mk1[t]) >> (tt & 63)) & 1ull) != 0;
                 }
-                st[kt][i] = v;
-                cm = fmaxf(cm, v);
+                v = vis ? v : -INFINITY;
             }
-        cm = fmaxf(cm, __shfl_xor(cm, 16));
-        cm = fmaxf(cm, __shfl_xor(cm, 32));
-        const bool up = cm > S.m[t] + 8.f;  // -inf + 8 == -inf: the first finite score always moves it
-        const float mnew = up ? cm : S.m[t];
-        alpha[t] = up ? __builtin_amdgcn_exp2f(S.m[t] - mnew) : 1.f;
-        moved = moved || up;
-        const float muse = mnew == -INFINITY ? 0.f : mnew;
-        float ps = 0.f;
-        uint32_t pk[4];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            float e[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                e[i] = __builtin_amdgcn_exp2f(st[kt][i] - muse);
-                ps += e[i];
-            }
-            pk[2 * kt] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
-            pk[2 * kt + 1] = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
+            st[kt][i] = v;
+            lmax = fmaxf(lmax, v);
         }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        S.l[t] = S.l[t] * alpha[t] + ps;
-        S.m[t] = mnew;
-        const uintx4 bu = {pk[0], pk[1], pk[2], pk[3]};
-        bp[t] = __builtin_bit_cast(half8, bu);
-    }
-    kv_load_v<HD>(nb, src, kk + 32 < k1 ? kk + 32 : -1);
-    if (kk + 32 > T) {
-        // keys >= T hold stale cache rows: their P^T entries are 0, and their V
-        // entries are zeroed so that nothing but finite values meets the MFMA
-        uint32_t keep[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-            keep[w] = (kk + slot_key(g, 2 * w) < T ? 0x0000ffffu : 0u) |
-                      (kk + slot_key(g, 2 * w + 1) < T ? 0xffff0000u : 0u);
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            b.v[dt].x &= keep[0];
-            b.v[dt].y &= keep[1];
-            b.v[dt].z &= keep[2];
-            b.v[dt].w &= keep[3];
+    alpha = 1.f;
+    // -inf + 8 == -inf: the first finite score always moves the max
+    if (__builtin_amdgcn_ballot_w64(lmax > S.m[t] + 8.f) != 0) {
+        const float cm = xmax4(lmax);
+        if (cm > S.m[t] + 8.f) {  // the same decision in the query's 4 lanes
+            alpha = __builtin_amdgcn_exp2f(S.m[t] - cm);
+            S.m[t] = cm;
+            moved = true;
         }
     }
+    const float muse = S.m[t] == -INFINITY ? 0.f : S.m[t];
+    float ps = 0.f;
+    uint32_t pk[4];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            e[i] = __builtin_amdgcn_exp2f(st[kt][i] - muse);
+            ps += e[i];
+        }
+        pk[2 * kt] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
+        pk[2 * kt + 1] = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
+    }
+    S.l[t] = S.l[t] * alpha + ps;
+    const uintx4 bu = {pk[0], pk[1], pk[2], pk[3]};
+    return __builtin_bit_cast(half8, bu);
+}
+
+// keys >= T hold stale cache rows: their P^T entries are 0, and their V entries
+// are zeroed so that nothing but finite values meets the MFMA
+template <int NDT>
+__device__ __forceinline__ void zero_stale_v(uintx4 (&v)[NDT], int kk, int T, int g) {
+    if (kk + 32 <= T) return;
+    uint32_t keep[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+        keep[w] = (kk + slot_key(g, 2 * w) < T ? 0x0000ffffu : 0u) | (kk + slot_key(g, 2 * w + 1) < T ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        v[dt].x &= keep[0];
+        v[dt].y &= keep[1];
+        v[dt].z &= keep[2];
+        v[dt].w &= keep[3];
+    }
+}
+
+// O^T += V^T P^T for the live tiles, after the rescale the step asked for
+template <int HD, int QT>
+__device__ __forceinline__ void step_pv(AttnState<HD, QT> &S, const uintx4 (&v)[HD / 16], const half8 (&bp)[QT],
+                                        const float (&alpha)[QT], bool moved, const bool (&tl)[QT]) {
+    constexpr int NDT = HD / 16;
     if (__builtin_amdgcn_ballot_w64(moved) != 0) {
 #pragma unroll
         for (int t = 0; t < QT; t++)
@@ -226,16 +262,87 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
             for (int dt = 0; dt < NDT; dt++) S.o[t][dt] *= alpha[t];
     }
 #pragma unroll
-    for (int t = 0; t < QT; t++)
+    for (int t = 0; t < QT; t++) {
+        if (!tl[t]) continue;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
-            S.o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b.v[dt]), bp[t], S.o[t][dt],
-                                                                0, 0, 0);
+            S.o[t][dt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, v[dt]), bp[t], S.o[t][dt], 0, 0, 0);
+    }
+}
+
+// S^T = K Q^T for the live tiles
+template <int HD, int QT>
+__device__ __forceinline__ void step_scores(const AttnState<HD, QT> &S, const uintx4 (&k)[2][HD / 32], int t,
+                                            floatx4 (&st)[2]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+        st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dc = 0; dc < HD / 32; dc++)
+            st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, k[kt][dc]), S.qf[t][dc], st[kt],
+                                                            0, 0, 0);
+    }
+}
+
+// One 32-key step from registers for all query tiles: scores and softmax,
+// then the next step's V loads are issued (the current K is dead by then, so
+// the two register buffers never hold four operand sets at once), then PV.
+template <int HD, int QT>
+__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const KvSrc &src,
+                                          int kk, int k1, int P, int T, int g) {
+    half8 bp[QT];
+    float alpha[QT];
+    bool tl[QT];
+    bool moved = false;
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        tl[t] = true;
+        floatx4 st[2];
+        step_scores<HD, QT>(S, b.k, t, st);
+        bp[t] = step_softmax<HD, QT>(S, t, st, kk, P, T, T, g, alpha[t], moved);
+    }
+    kv_load_v<HD>(nb, src, kk + 32 < k1 ? kk + 32 : -1);
+    zero_stale_v<HD / 16>(b.v, kk, T, g);
+    step_pv<HD, QT>(S, b.v, bp, alpha, moved, tl);
+}
+
+// Result of one query (lane (r16, g) holds d = dt*16 + 4g + i): with one
+// split the normalised row goes straight into the wo input (fp16, fragment
+// order); otherwise o / l as fp16 and (m, l) for the combine kernel, which
+// weighs split s by l_s * exp2(m_s - max m).
+template <int HD>
+__device__ __forceinline__ void attn_emit(const AttnParams &p, int s, int head, int m, int g,
+                                          const floatx4 (&o)[HD / 16], float mq, float l) {
+    const float inv = 1.0f / l;
+    if (p.nsplit == 1) {
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t k = (int64_t)head * HD + dt * 16 + 4 * g + i;
+                p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(o[dt][i] * inv);
+            }
+        return;
+    }
+    const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
+    uint16_t *po = (uint16_t *)p.part_o + pi * HD;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) {
+        const float w = l > 0.f ? inv : 0.f;  // a query that saw no key of this split has l = 0
+        *(uintx2 *)(po + dt * 16 + 4 * g) =
+            uintx2{(uint32_t)f2h(o[dt][0] * w) | ((uint32_t)f2h(o[dt][1] * w) << 16),
+                   (uint32_t)f2h(o[dt][2] * w) | ((uint32_t)f2h(o[dt][3] * w) << 16)};
+    }
+    if (g == 0) {
+        p.part_ml[2 * pi] = mq;
+        p.part_ml[2 * pi + 1] = l;
+    }
 }
 
 template <int HD, int QT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnParams p) {
-    constexpr int NDC = HD / 32, NDT = HD / 16;
+    constexpr int NDT = HD / 16;
     const int h = blockIdx.x, s = blockIdx.y, qg = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
@@ -249,43 +356,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
     src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
 
-    AttnState<HD, QT> S;
-#pragma unroll
-    for (int t = 0; t < QT; t++) {
-        const int q = (qg * QT + t) * 16 + r16;
-        const bool live = q < nq;
-        const int m = live ? q / p.n_rep : 0, r = live ? q % p.n_rep : 0;
-        const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + r) * p.M + m) * HD;
-#pragma unroll
-        for (int dc = 0; dc < NDC; dc++) {
-            uintx4 v = {0u, 0u, 0u, 0u};
-            if (live) v = *(const uintx4 *)(qr + dc * 32 + g * 8);
-            S.qf[t][dc] = __builtin_bit_cast(half8, v);
-        }
-        S.mk0[t] = p.mask[(int64_t)m * p.mask_words];
-        S.mk1[t] = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        S.m[t] = -INFINITY;
-        S.l[t] = 0.f;
-    }
-    const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
-
     // two register buffers: the next 32 keys load while the current ones compute
     // (K at the start of a step, V once the step's scores are done)
     KvStep<HD> b0, b1;
     int kk = k0;
     kv_load_k<HD>(b0, src, kk < k1 ? kk : -1);
     kv_load_v<HD>(b0, src, kk < k1 ? kk : -1);
+
+    AttnState<HD, QT> S;
+    const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
+#pragma unroll
+    for (int t = 0; t < QT; t++) load_query<HD, QT>(S, t, p, h, (qg * QT + t) * 16 + r16, g, sl2);
+
     while (kk < k1) {
         kv_load_k<HD>(b1, src, kk + 32 < k1 ? kk + 32 : -1);
-        attn_step<HD, QT>(S, b0, b1, src, kk, k1, p.P, T, sl2, g);
+        attn_step<HD, QT>(S, b0, b1, src, kk, k1, p.P, T, g);
         kk += 32;
         if (kk >= k1) break;
         kv_load_k<HD>(b0, src, kk + 32 < k1 ? kk + 32 : -1);
-        attn_step<HD, QT>(S, b1, b0, src, kk, k1, p.P, T, sl2, g);
+        attn_step<HD, QT>(S, b1, b0, src, kk, k1, p.P, T, g);
         kk += 32;
     }
+#pragma unroll
+    for (int t = 0; t < QT; t++) S.l[t] = xsum4(S.l[t]);  // the query's 4 partial sums
 
     // ---- merge the 4 waves' states: rescale to the common max, then
     // (o0 + o2) + (o1 + o3) through LDS ----
@@ -345,55 +438,211 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int t = 0; t < QT; t++) {
         const int q = (qg * QT + t) * 16 + r16;
         if (q >= nq) continue;
-        const int m = q / p.n_rep, r = q % p.n_rep;
-        const int head = h * p.n_rep + r;
-        if (p.nsplit == 1) {
-            const float inv = 1.0f / Lt[t];
+        floatx4 y[NDT];
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-                const floatx4 y = S.o[t][dt] + sob[0][t][dt][lane];
+        for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] + sob[0][t][dt][lane];
+        attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
+    }
+}
+
+// ---- many queries (tree verify): query tiles across waves, keys shared in LDS ----
+// Grid (kv head, key split, query block).  A workgroup has kTKS key groups of
+// 4 waves; the 4 waves of a group own kTQW query tiles each (the workgroup's
+// 4 * kTQW * 16 queries of one KV head) and walk the group's part of the split
+// together: each 32-key block of K and V (contiguous in the blocked cache
+// layout) is copied once into LDS by the group's 256 threads and read there by
+// its 4 waves, so the cache leaves L2 once per query block instead of once per
+// query tile.  Copies run kTStages blocks ahead through registers (as many LDS
+// stages, one barrier per block).  The key groups merge through LDS at the
+// end (fixed order), the splits in the combine kernel.
+constexpr int kTQW = 2;
+constexpr int kTKS = 2;
+constexpr int kTStages = 3;
+constexpr int kTMaxSplits = 16;
+
+// a thread's 16-byte pieces of one 32-key block: K (64 * HD bytes) then V
+template <int HD> struct TileCopy {
+    uintx4 r[HD / 32];
+};
+template <int HD>
+__device__ __forceinline__ void tile_fetch(TileCopy<HD> &c, const KvSrc &src, int kk, int tid) {  // kk < 0: none
+    const uint32_t so = kv_so(kk, HD);
+    const uint32_t t16 = (uint32_t)tid * 16u;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int64_t k = (int64_t)head * HD + dt * 16 + 4 * g + i;
-                    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(y[i] * inv);
-                }
-            }
-        } else {
-            const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
-            float *po = p.part_o + pi * HD;
+    for (int i = 0; i < HD / 32; i++) {
+        const uint32_t b = (uint32_t)i * 4096u + t16;
+        c.r[i] = i < HD / 64 ? bld16(src.k, b, so) : bld16(src.v, b - 64u * HD, so);
+    }
+}
+// In LDS each 1 KiB chunk (the 64 16-byte pieces one MFMA operand load reads,
+// piece r * 4 + g for lane (r16 = r, g)) is stored with the pieces of a row r
+// permuted, g -> g ^ ((r >> 1) & 3): the 8 lanes of one LDS pass (same g,
+// r = 8q .. 8q+7) then touch 8 different 4-bank groups instead of 2.
+__device__ __forceinline__ int lds_swz(int piece) {
+    const int w = piece & 63, r = w >> 2;
+    return (piece & ~63) + r * 4 + ((w & 3) ^ ((r >> 1) & 3));
+}
+template <int HD>
+__device__ __forceinline__ void tile_store(uintx4 *stage, const TileCopy<HD> &c, int tid) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) *(floatx4 *)(po + dt * 16 + 4 * g) = S.o[t][dt] + sob[0][t][dt][lane];
-            if (g == 0) {
-                p.part_ml[2 * pi] = Mt[t];
-                p.part_ml[2 * pi + 1] = Lt[t];
-            }
+    for (int i = 0; i < HD / 32; i++) stage[lds_swz(i * 256 + tid)] = c.r[i];
+}
+
+// One 32-key block from LDS for the wave's query tiles (dead tiles skipped)
+// (lp: the lane's swizzled piece inside a chunk, lds_swz(r16 * 4 + g))
+template <int HD, int QT>
+__device__ __forceinline__ void tile_step(AttnState<HD, QT> &S, const uintx4 *stage, int lp, const bool (&tl)[QT],
+                                          int kk, int P, int T, int lim, int g) {
+    constexpr int NDC = HD / 32, NDT = HD / 16;
+    uintx4 kop[2][NDC];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int dc = 0; dc < NDC; dc++) kop[kt][dc] = stage[kt * 2 * HD + dc * 64 + lp];
+    half8 bp[QT];
+    float alpha[QT];
+    bool moved = false;
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        alpha[t] = 1.f;
+        bp[t] = half8{};
+        if (!tl[t]) continue;
+        floatx4 st[2];
+        step_scores<HD, QT>(S, kop, t, st);
+        bp[t] = step_softmax<HD, QT>(S, t, st, kk, P, T, lim, g, alpha[t], moved);
+    }
+    uintx4 vop[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) vop[dt] = stage[4 * HD + dt * 64 + lp];
+    zero_stale_v<NDT>(vop, kk, T, g);
+    step_pv<HD, QT>(S, vop, bp, alpha, moved, tl);
+}
+
+template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTKS * kTStages * 8 * HD * 16; }
+
+template <int HD>
+__global__ __launch_bounds__(256 * kTKS) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {
+    constexpr int NDT = HD / 16, QT = kTQW, SW = 8 * HD;  // SW: 16-byte pieces of one stage
+    extern __shared__ uintx4 lds[];
+    const int h = blockIdx.x, s = blockIdx.y, qb = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kg = wave >> 2, qw = wave & 3, tid = threadIdx.x & 255;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int nq = p.M * p.n_rep;
+    const int T = p.P + p.M;
+    const int kps = 4 * p.keys_per_wave, kpg = kps / kTKS;  // keys of the split, of a group
+    const int s0 = s * kps;
+    const int k0 = s0 + kg * kpg, lim = min(k0 + kpg, T);   // this group's keys [k0, lim)
+    const int nb = (min(s0 + kpg, T) - s0 + 31) / 32;       // blocks of group 0 (>= group 1's)
+    const uint32_t stream_bytes = (uint32_t)p.cap * HD * 2u;
+    KvSrc src;
+    src.k = make_rsrc(p.kc + (int64_t)h * p.cap * HD, stream_bytes);
+    src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
+    src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
+    uintx4 *stg = lds + kg * kTStages * SW;
+    const int lp = lds_swz(r16 * 4 + g);
+    auto blk = [&](int j) { return k0 + 32 * j < lim ? k0 + 32 * j : -1; };
+
+    // the first blocks' copies go out before anything else
+    TileCopy<HD> c0, c1, c2;
+    tile_fetch<HD>(c0, src, blk(0), tid);
+    tile_fetch<HD>(c1, src, blk(1), tid);
+    tile_fetch<HD>(c2, src, blk(2), tid);
+
+    AttnState<HD, QT> S;
+    bool tl[QT];
+    const float sl2 = p.scale * 1.4426950408889634f;
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        const int tile = (qb * 4 + qw) * QT + t;
+        tl[t] = tile * 16 < nq;  // wave-uniform: the tile holds a live query
+        load_query<HD, QT>(S, t, p, h, tile * 16 + r16, g, sl2);
+    }
+
+    // block j lives in stage j % 3; it is written after every wave passed the
+    // barrier of block j - 1, i.e. finished block j - 2 and so block j - 3.
+    // Blocks past a group's range load nothing and are fully masked.
+    for (int j = 0; j < nb; j += 3) {
+        tile_store<HD>(stg, c0, tid);
+        tile_fetch<HD>(c0, src, blk(j + 3), tid);
+        __syncthreads();
+        tile_step<HD, QT>(S, stg, lp, tl, k0 + 32 * j, p.P, T, lim, g);
+        if (j + 1 >= nb) break;
+        tile_store<HD>(stg + SW, c1, tid);
+        tile_fetch<HD>(c1, src, blk(j + 4), tid);
+        __syncthreads();
+        tile_step<HD, QT>(S, stg + SW, lp, tl, k0 + 32 * (j + 1), p.P, T, lim, g);
+        if (j + 2 >= nb) break;
+        tile_store<HD>(stg + 2 * SW, c2, tid);
+        tile_fetch<HD>(c2, src, blk(j + 5), tid);
+        __syncthreads();
+        tile_step<HD, QT>(S, stg + 2 * SW, lp, tl, k0 + 32 * (j + 2), p.P, T, lim, g);
+    }
+#pragma unroll
+    for (int t = 0; t < QT; t++) S.l[t] = xsum4(S.l[t]);  // the query's 4 partial sums
+
+    // key group 1 hands its state to group 0 through LDS (the stages are free
+    // once every wave passed this barrier)
+    static_assert(kTKS == 2, "the merge below pairs two key groups");
+    floatx4 *mo = (floatx4 *)lds;                               // [qw][t][dt][lane]
+    float *mml = (float *)(lds + 4 * QT * NDT * 64);            // [qw][t][lane][2]
+    __syncthreads();
+    if (kg == 1) {
+#pragma unroll
+        for (int t = 0; t < QT; t++) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) mo[((qw * QT + t) * NDT + dt) * 64 + lane] = S.o[t][dt];
+            mml[((qw * QT + t) * 64 + lane) * 2] = S.m[t];
+            mml[((qw * QT + t) * 64 + lane) * 2 + 1] = S.l[t];
         }
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        const int q = ((qb * 4 + qw) * QT + t) * 16 + r16;
+        if (q >= nq) continue;
+        const float m1 = mml[((qw * QT + t) * 64 + lane) * 2], l1 = mml[((qw * QT + t) * 64 + lane) * 2 + 1];
+        const float mx = fmaxf(S.m[t], m1);
+        const float f0 = S.m[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(S.m[t] - mx);
+        const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
+        floatx4 y[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] * f0 + mo[((qw * QT + t) * NDT + dt) * 64 + lane] * f1;
+        attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, mx, S.l[t] * f0 + l1 * f1);
     }
 }
 
 // ---- combine splits -> fp16 fragment-layout input of wo ----------------------
-// grid (n_heads, M), block hd threads; splits are merged in index order.
+// grid (n_heads, M), block hd threads; splits are merged in index order:
+// out = sum_s w_s o_s / sum_s w_s, w_s = l_s * exp2(m_s - max m).
 __global__ __launch_bounds__(128) void k_attn_combine(AttnParams p) {
     const int head = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const int HD = p.hd, ns = p.nsplit;
     const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
     const int64_t pi0 = (int64_t)head * p.M + m;
+    const uint16_t *po = (const uint16_t *)p.part_o;
     float mx = -INFINITY;
     for (int s = 0; s < ns; s++) mx = fmaxf(mx, p.part_ml[2 * (pi0 + s * stride)]);
-    float L = 0.f, acc = 0.f;
+    float W = 0.f, acc = 0.f;
 #pragma unroll 4
     for (int s = 0; s < ns; s++) {
         const int64_t pi = pi0 + s * stride;
         const float ms = p.part_ml[2 * pi];
-        const float f = ms == -INFINITY ? 0.f : exp2f(ms - mx);
-        L += p.part_ml[2 * pi + 1] * f;
-        acc += p.part_o[pi * HD + d] * f;
+        const float w = ms == -INFINITY ? 0.f : p.part_ml[2 * pi + 1] * exp2f(ms - mx);
+        W += w;
+        acc += h2f(po[pi * HD + d]) * w;
     }
     const int64_t k = (int64_t)head * HD + d;
-    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / L);
+    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / W);
 }
 
 // ---- host launchers ----------------------------------------------------------
+#define SD_ATTN_CHECK(x)                                                                           \
+    do {                                                                                           \
+        const hipError_t e_ = (x);                                                                 \
+        if (e_ != hipSuccess) throw BackendError(std::string("attention: ") + hipGetErrorString(e_)); \
+    } while (0)
 void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
     hipLaunchKernelGGL(k_rope_kv, dim3(p.M, p.n_heads + p.n_kv), dim3(p.hd / 2), 0, st, p);
 }
@@ -405,39 +654,63 @@ static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
 // call.  Above, the splits shrink as query tiles grow, towards 2 resident
 // waves per SIMD (512 workgroups of 4 waves).
 AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
-    const int target = attn_target_splits(n_kv);
-    int want = target;
+    const int T = P + M;
     if (M > 16) {
-        const int nqt = (M * n_rep + 15) / 16;
-        want = 512 / (n_kv * nqt);
-        want = want < 1 ? 1 : want > target ? target : want;
+        // k_attn_t: splits of kps keys (a multiple of 128), towards 256
+        // workgroups over the query blocks
+        const int nqt = (M * n_rep + 15) / 16, nqb = (nqt + 4 * kTQW - 1) / (4 * kTQW);
+        int want = 256 / (n_kv * nqb);
+        want = want < 1 ? 1 : want > kTMaxSplits ? kTMaxSplits : want;
+        int kps = (P + 1 + want - 1) / want;
+        kps = kps < 128 ? 128 : (kps + 127) / 128 * 128;
+        return AttnSplit{kps / 4, (T + kps - 1) / kps};
     }
+    const int want = attn_target_splits(n_kv);
     int kpw = (P + 1 + 4 * want - 1) / (4 * want);
     kpw = kpw < 32 ? 32 : (kpw + 31) / 32 * 32;
-    const int T = P + M;
     return AttnSplit{kpw, (T + 4 * kpw - 1) / (4 * kpw)};
 }
 
-// 4 * kpw >= (P + 1) / want, want <= target, and 4 * kpw >= 128 >= M, so
-// nsplit = ceil((P + M) / (4 kpw)) <= target + 2
-int attn_max_splits(int n_kv) { return attn_target_splits(n_kv) + 3; }
+// split size >= (P + 1) / want and >= 128 >= M, so
+// nsplit = ceil((P + M) / size) <= want + 1
+int attn_max_splits(int n_kv) {
+    const int t = attn_target_splits(n_kv);
+    return (t > kTMaxSplits ? t : kTMaxSplits) + 3;
+}
 
 void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.keys_per_wave < 32 || p.keys_per_wave % 32) throw BackendError("attention: keys_per_wave");
     if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
+    if ((int64_t)(p.nsplit - 1) * 4 * p.keys_per_wave >= (int64_t)p.P + p.M) throw BackendError("attention: empty split");
     if (p.cap % 32 || (int64_t)p.P + p.M > p.cap) throw BackendError("attention: cache capacity");
     if (p.mask_words < 1 || p.mask_words > 2 || p.M > 64 * p.mask_words) throw BackendError("attention: mask words");
-    // One query tile per wave keeps a wave within 256 registers (two
-    // double-buffered 32-key operand sets and its accumulators), so two waves
-    // share each SIMD.  Query tiles become workgroups along z; with the KV head
-    // as blockIdx.x and n_kv a multiple of the 8 XCDs, every workgroup of one
-    // head lands on the same XCD, so the query tiles re-read that head's keys
-    // from its L2.
+    if (p.hd != 128 && p.hd != 64) throw BackendError("attention: head_dim must be 64 or 128");
     const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
-    const dim3 grid(p.n_kv, p.nsplit, nqt);
-    if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, p);
-    else if (p.hd == 64) hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, p);
-    else throw BackendError("attention: head_dim must be 64 or 128");
+    if (p.M > 16) {
+        // query blocks of 4 waves x kTQW tiles sharing each key block through LDS
+        const dim3 grid(p.n_kv, p.nsplit, (nqt + 4 * kTQW - 1) / (4 * kTQW));
+        if (p.keys_per_wave * 4 % (32 * kTKS)) throw BackendError("attention: split size");
+        static bool lds_set = false;  // LDS beyond the 64 KiB default, once per process
+        if (!lds_set) {
+            SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)attn_t_lds<128>()));
+            SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)attn_t_lds<64>()));
+            lds_set = true;
+        }
+        if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(256 * kTKS), attn_t_lds<128>(), st, p);
+        else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(256 * kTKS), attn_t_lds<64>(), st, p);
+    } else {
+        // One query tile per wave keeps a wave within 256 registers (two
+        // double-buffered 32-key operand sets and its accumulators), so two
+        // waves share each SIMD.  Query tiles become workgroups along z; with the
+        // KV head as blockIdx.x and n_kv a multiple of the 8 XCDs, every
+        // workgroup of one head lands on the same XCD, so the query tiles re-read
+        // that head's keys from its L2.
+        const dim3 grid(p.n_kv, p.nsplit, nqt);
+        if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, p);
+    }
     if (p.nsplit > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p);
 }
 
