@@ -232,7 +232,8 @@ __device__ __forceinline__ void st4h(uint16_t *dst, float a, float b, float c, f
 // memory round trip after it: the residual rows (GM_RESID), the next norm's
 // weights, the bias and, for RoPE, the position and its cos/sin entries.
 template <int RT> struct EpiPre {
-    floatx4 o[RT], w[RT], b[RT];
+    floatx4 a[RT];  // GM_RESID: the residual rows; otherwise the bias
+    floatx4 w[RT];  // GM_RESID with next_w: the next norm's weights
     int pos;
     float cs[4], sn[4];
 };
@@ -264,9 +265,12 @@ __device__ __forceinline__ void epi_prefetch(const GemmParams &p, const GemmSeg 
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int n0 = rloc[rt] + 4 * g;
-        if (p.mode == GM_RESID) e.o[rt] = *(const floatx4 *)(S[rt].out + (int64_t)ml * S[rt].ldo + S[rt].col0 + n0);
-        if (p.next_w) e.w[rt] = *(const floatx4 *)(p.next_w + S[rt].col0 + n0);
-        if (S[rt].bias) e.b[rt] = *(const floatx4 *)(S[rt].bias + n0);
+        if (p.mode == GM_RESID) {
+            e.a[rt] = *(const floatx4 *)(S[rt].out + (int64_t)ml * S[rt].ldo + S[rt].col0 + n0);
+            if (p.next_w) e.w[rt] = *(const floatx4 *)(p.next_w + S[rt].col0 + n0);
+        } else if (S[rt].bias) {
+            e.a[rt] = *(const floatx4 *)(S[rt].bias + n0);
+        }
     }
     if (p.rope.q16) e.pos = p.rope.pos[ml];
 }
@@ -303,7 +307,7 @@ __device__ __forceinline__ void rope_epilogue(const GemmParams &p, const GemmSeg
 #pragma unroll
         for (int rt = 0; rt < 2; rt++) {
             floatx4 r = v[rt];
-            if (S[rt].bias) r += e.b[rt];
+            if (S[rt].bias) r += e.a[rt];
 #pragma unroll
             for (int i = 0; i < 4; i++) x[rt][i] = r[i];
         }
@@ -375,9 +379,9 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)
         float *o = S[rt].out + (int64_t)m * S[rt].ldo + S[rt].col0 + n0;
         floatx4 r = v[rt];
         if (p.mode == GM_RESID) {
-            r += e.o[rt];
+            r += e.a[rt];
         } else if (S[rt].bias) {
-            r += e.b[rt];
+            r += e.a[rt];
         }
         *(floatx4 *)o = r;
         if (p.next_w) {
@@ -515,41 +519,34 @@ __device__ __forceinline__ void load_x(uintx4 (&b)[CT][8], rsrc_t xr, const uint
 constexpr int kDepth1 = 2;
 
 // ---- fused RMSNorm, input side ------------------------------------------------
-// The sums of squares of token m arrive as norm_parts partials (one per
-// 16-row tile of the residual matmul that produced h, or of the RMSNorm
-// kernel).  Lane (r16, g) adds the quarter g of token r16's partials, the four
-// quarters meet by xor-shuffles: the same fixed order in every workgroup.  The
-// loads are issued before the weight prologue and consumed after it, so
-// waiting for them does not wait for the weights (loads retire in order).
-constexpr int kNormMaxParts = 256;  // hidden <= 4096
-struct NormLoads {
-    floatx4 v[kNormMaxParts / 16];
+// The sums of squares of token m arrive as K/16 partials, one per 16-element
+// tile of h, i.e. 16 per superblock.  They travel with the superblocks: the
+// wave that multiplies superblock sb also loads its 16 partials (lane (r16, g)
+// the 4 of token r16 at 4g) and adds them to a running sum; the waves' sums
+// meet in the cross-wave reduction and the 4 lane groups' by xor-shuffles,
+// in a fixed order that depends on the matrix only.
+struct NormSrc {
+    rsrc_t r;
+    uint32_t vo;  // the lane's float4 inside a superblock's 16 partials
 };
-__device__ __forceinline__ void norm_issue(const GemmParams &p, NormLoads &nl) {
+__device__ __forceinline__ NormSrc norm_src(const GemmParams &p) {
     const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
-    const int np = p.norm_parts;
+    NormSrc n;
     // no norm: an empty resource, every load reads zero without a memory access
-    const rsrc_t r = make_rsrc(p.norm_ssq, p.norm_ssq ? (uint32_t)(p.M * np * 4) : 0u);
-    const int m = min(r16, p.M - 1);
-    const uint32_t vo = (uint32_t)(m * np + g * (np / 4)) * 4u;
-#pragma unroll
-    for (int j = 0; j < kNormMaxParts / 16; j++)
-        nl.v[j] = __builtin_bit_cast(floatx4, bld16(r, vo + 16u * j, uni(16 * j < np ? 0u : kNoLoad)));
+    n.r = make_rsrc(p.norm_ssq, p.norm_ssq ? (uint32_t)(p.M * p.norm_parts * 4) : 0u);
+    n.vo = (uint32_t)(min(r16, p.M - 1) * p.norm_parts + 4 * g) * 4u;
+    return n;
 }
-__device__ __forceinline__ float norm_finish(const GemmParams &p, const NormLoads &nl) {
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < kNormMaxParts / 16; j++) s += (nl.v[j].x + nl.v[j].y) + (nl.v[j].z + nl.v[j].w);
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
-    return p.norm_ssq ? 1.0f / sqrtf(s / (float)p.K + p.norm_eps) : 1.0f;
+__device__ __forceinline__ floatx4 norm_load(const NormSrc &n, int sb) {
+    return __builtin_bit_cast(floatx4, bld16(n.r, n.vo, uni(sb < 0 ? kNoLoad : (uint32_t)sb * 64u)));
 }
+__device__ __forceinline__ float norm_add(float s, const floatx4 &v) { return s + ((v.x + v.y) + (v.z + v.w)); }
 
 // Superblocks sb = ks, ks + KW, ... in increasing order;
 // `after_prologue` runs once the first superblock's loads are in flight.
 template <int FMT, int RT, int CT, int KW, typename Hook>
 __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT][CT],
-                                         Hook &&after_prologue) {
+                                         float &nsum, Hook &&after_prologue) {
     typedef QFmt<FMT> F;
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
@@ -567,20 +564,26 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
     if constexpr (CT == 1 && kDepth1 == 2) {
         // x and weights of the next superblock in flight during this one
         uintx4 b0[1][8], b1[1][8];
+        const NormSrc ns = norm_src(p);
         load_x<1>(b0, xr, xvo, sbi(0));
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+        floatx4 n0 = norm_load(ns, sbi(0)), n1;  // after the weights: waiting for them does not wait for it
         after_prologue();
         for (int i = 0;; i += 2) {
             load_x<1>(b1, xr, xvo, sbi(i + 1));
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
+            n1 = norm_load(ns, sbi(i + 1));
             qmm_step1<FMT, RT>(w0, b0[0], g, acc);
+            nsum = norm_add(nsum, n0);
             if (i + 1 >= nst) break;
             load_x<1>(b0, xr, xvo, sbi(i + 2));
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
+            n0 = norm_load(ns, sbi(i + 2));
             qmm_step1<FMT, RT>(w1, b1[0], g, acc);
+            nsum = norm_add(nsum, n1);
             if (i + 2 >= nst) break;
         }
     } else if constexpr (CT == 1) {
@@ -675,39 +678,34 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // Wave 0 runs the epilogue: it requests the epilogue's operands and the
-    // fused-norm sums first, and consumes the sums (and requests the RoPE
-    // table entries, which need the position) once its weights are in flight.
-    float inv = 1.0f;  // fused RMSNorm scale of this lane's token
+    // Wave 0 runs the epilogue: it requests the epilogue's operands first and
+    // the RoPE table entries (which need the position) once its weights are in
+    // flight.  Every wave sums the fused-norm partials of its superblocks.
     EpiPre<RT> e;
-    NormLoads nl;
-    if (wave == 0) {
-        epi_prefetch<RT>(p, S, rloc, r16, g, e);
-        norm_issue(p, nl);
-    }
+    if (wave == 0) epi_prefetch<RT>(p, S, rloc, r16, g, e);
     auto after_prologue = [&]() {
-        if (wave == 0) {
-            inv = norm_finish(p, nl);
-            epi_prefetch_rope<RT>(p, S, rloc, g, e);
-        }
+        if (wave == 0) epi_prefetch_rope<RT>(p, S, rloc, g, e);
     };
+    float nsum = 0.f;
     switch (S[0].fmt) {
-    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
-    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
-    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
-    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc, after_prologue); break;
+    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
+    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
+    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
+    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
     default: break;
     }
     // fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, one
-    // token tile at a time
+    // token tile at a time (CT == 1 here; the norm sums ride along)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
         floatx4 v[RT];
         if constexpr (KW > 1) {
             __shared__ floatx4 red[KW][RT][64];
+            __shared__ float nred[KW][64];
             __syncthreads();
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) red[wave][rt][lane] = acc[rt][ct];
+            nred[wave][lane] = nsum;
             __syncthreads();
             if (wave != 0) continue;
 #pragma unroll
@@ -717,12 +715,22 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
                 for (int w = 1; w < KW; w++) s += red[w][rt][lane];
                 v[rt] = s;
             }
+            float ns = nred[0][lane];
+#pragma unroll
+            for (int w = 1; w < KW; w++) ns += nred[w][lane];
+            nsum = ns;
         } else {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) v[rt] = acc[rt][ct];
         }
+        if (p.norm_ssq) {
+            // the token's four lane groups (g = 0..3) in a fixed order
+            float ns = nsum + __shfl_xor(nsum, 16);
+            ns += __shfl_xor(ns, 32);
+            const float inv = 1.0f / sqrtf(ns / (float)p.K + p.norm_eps);
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
+            for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
+        }
         epilogue<RT>(p, S, rloc, v, e, ct * 16 + r16, g, (int)blockIdx.x);
     }
 }
@@ -1035,8 +1043,7 @@ int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
                 throw BackendError("qgemm: segments must be consecutive");
     // the fused RMSNorm and RoPE epilogues exist in the M <= 16 kernel only
     if ((p.norm_ssq || p.next_w || p.rope.q16) && p.M > 16) throw BackendError("qgemm: fused epilogues need M <= 16");
-    if (p.norm_ssq && (p.norm_parts < 16 || p.norm_parts > 256 || p.norm_parts % 16))
-        throw BackendError("qgemm: norm partial count");
+    if (p.norm_ssq && p.norm_parts * 16 != p.K) throw BackendError("qgemm: norm partials must be one per 16 of K");
     if (p.next_w && (p.mode != GM_RESID || !p.next_u || !p.next_ssq)) throw BackendError("qgemm: next-norm outputs");
     if (p.rope.q16) {
         const RopeOut &R = p.rope;
