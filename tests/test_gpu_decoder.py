@@ -231,3 +231,33 @@ def test_variants_batched_and_tree(hip, over):
     lg, _ = hd.tree_logits_keep_kv(tree)
     for i in range(len(tree)):
         assert rel_err(lg[i], lo[i]) < TOL, (over, i)
+
+
+@pytest.mark.parametrize("over,prefix_len,shape", [
+    (dict(ctx_len=2048, n_layers=2), 1500, (4, 3, 2, 2)),
+    (dict(n_kv_heads=2, head_dim=128, hidden=1024, ctx_len=1024, n_layers=2), 900, (2, 2, 2, 2, 2)),
+])
+def test_long_context_verify(hip, over, prefix_len, shape):
+    """Long prefixes put the attention's key range over many splits (combine
+    kernel) and ragged last blocks, for both the M <= 16 kernel (linear
+    verify, 5 rows) and the query-parallel M > 16 kernel (89- and 63-node
+    trees, whose last query tile is partial)."""
+    od, hd, prefix = make_pair(hip, prefix_len=prefix_len, seed=4, **over)
+    assert rel_err(hd.next_logits(), od.next_logits()) < TOL
+    drafts = greedy_chain(od, 4)
+    b = od.batched_logits(drafts)
+    a = hd.batched_logits(drafts)
+    for i in range(5):
+        assert rel_err(a[i], b[i]) < TOL, (over, i)
+    hd.rollback_to(len(prefix))
+    od.rollback_to(len(prefix))
+    rng = np.random.default_rng(prefix_len)
+    cands = [[int(t) for t in rng.integers(0, 32000, w)] for w in shape]
+    tree = O.build_cartesian_tree(prefix[-1], cands)
+    assert len(tree) > 48
+    lo, ho = od.tree_logits_keep_kv(tree)
+    lg, hg = hd.tree_logits_keep_kv(tree)
+    for i in range(len(tree)):
+        assert rel_err(lg[i], lo[i]) < TOL, (over, i)
+        assert rel_err(hg[i], ho[i]) < TOL, (over, i)
+    assert hd.cache_len() == len(prefix) - 1 + len(tree)
