@@ -39,13 +39,16 @@ namespace sd {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-// two fp16 codes -> two fp16 results of round_f16(code * s + c) (f32 inside)
+// two fp16 codes -> two fp16 results of round_f16(code * s + c) (f32 inside).
+// Two v_fma_mix_f32 and one v_cvt_pk_f16_f32: on gfx950 v_fma_mixlo/hi_f16
+// (what the compiler makes of the plain expression) issue at half the rate of
+// v_fma_mix_f32, and the pair costs more than the three instructions here.
 __device__ __forceinline__ uint32_t fm2(uint32_t p, float s, float c) {
     const half2v h = __builtin_bit_cast(half2v, p);
-    half2v r;
-    r.x = (_Float16)__builtin_fmaf((float)h.x, s, c);
-    r.y = (_Float16)__builtin_fmaf((float)h.y, s, c);
-    return __builtin_bit_cast(uint32_t, r);
+    const float a = __builtin_fmaf((float)h.x, s, c), b = __builtin_fmaf((float)h.y, s, c);
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     const uintx4 u = {a, b, c, d};
