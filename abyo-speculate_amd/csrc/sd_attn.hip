@@ -40,8 +40,14 @@ __device__ __forceinline__ float qkv_at(const RopeKvParams &p, int m, int col) {
     const int64_t at = (int64_t)m * p.ld_qkv + col;
     if (p.nks <= 1) return p.qkv[at];
     const int64_t stride = (int64_t)p.M * p.ld_qkv;
-    float v = p.part[at];
-    for (int k = 1; k < p.nks; k++) v += p.part[at + k * stride];
+    // up to 8 slices, all loaded before the first add
+    float a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = k < p.nks ? p.part[at + k * stride] : 0.f;
+    float v = a[0];
+#pragma unroll
+    for (int k = 1; k < 8; k++)
+        if (k < p.nks) v += a[k];
     if (!p.bq) return v;
     const int qd = p.n_heads * p.hd, kvd = p.n_kv * p.hd;
     return v + (col < qd ? p.bq[col] : col < qd + kvd ? p.bk[col - qd] : p.bv[col - qd - kvd]);

@@ -17,7 +17,8 @@ namespace sd {
 // registers (vector loads, all issued before the first use), so the row is
 // read from memory once and there is one memory round trip, not K/256 of them.
 // With nks > 1 the residual matmul that produced x left K-slice partial sums
-// part[ks][M][K]: they are added to x in slice order first (and x is stored).
+// part[ks][M][K] (nks <= 8): they are added to x in slice order first (and x
+// is stored); every slice's loads are in flight before the first add.
 template <int NV>  // float4 vectors per thread: K = 1024 * NV
 __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K, float eps, uint16_t *out16,
                                                  int ld16, float *out32, const float *part, int nks,
@@ -31,16 +32,25 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K
 #pragma unroll
     for (int i = 0; i < NV; i++) wr[i] = wv[t + 256 * i];
     if (nks > 1) {
-        for (int k = 0; k < nks; k++) {
-            const float4 *pr = (const float4 *)(part + k * pstride + (int64_t)m * K);
+        constexpr int KS = NV <= 4 ? 8 : 4;  // slices per batch of loads (registers: KS * NV float4)
+        for (int k0 = 0; k0 < nks; k0 += KS) {
+            float4 a[KS][NV];
 #pragma unroll
-            for (int i = 0; i < NV; i++) {
-                const float4 a = pr[t + 256 * i];
-                v[i].x += a.x;
-                v[i].y += a.y;
-                v[i].z += a.z;
-                v[i].w += a.w;
+            for (int k = 0; k < KS; k++) {
+                const float4 *pr = (const float4 *)(part + (k0 + k) * pstride + (int64_t)m * K);
+#pragma unroll
+                for (int i = 0; i < NV; i++) a[k][i] = k0 + k < nks ? pr[t + 256 * i] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+#pragma unroll
+                for (int i = 0; i < NV; i++) {
+                    if (k0 + k >= nks) continue;
+                    v[i].x += a[k][i].x;
+                    v[i].y += a[k][i].y;
+                    v[i].z += a[k][i].z;
+                    v[i].w += a[k][i].w;
+                }
         }
 #pragma unroll
         for (int i = 0; i < NV; i++) row[t + 256 * i] = v[i];
@@ -65,8 +75,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K
         const float y[4] = {v[i].x / mrms * wr[i].x, v[i].y / mrms * wr[i].y, v[i].z / mrms * wr[i].z,
                             v[i].w / mrms * wr[i].w};
         if (out16) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) out16[(int64_t)m * ld16 + frag_index(k + j)] = f2h(y[j]);
+            // elements k .. k+3 sit in fragment slots f, f+2, f+1, f+3: one 8-byte store
+            const uint32_t lo = (uint32_t)f2h(y[0]) | ((uint32_t)f2h(y[2]) << 16);
+            const uint32_t hi = (uint32_t)f2h(y[1]) | ((uint32_t)f2h(y[3]) << 16);
+            *(uint2 *)(out16 + (int64_t)m * ld16 + frag_index(k)) = make_uint2(lo, hi);
         }
         if (out32) *(float4 *)(out32 + (int64_t)m * K + k) = make_float4(y[0], y[1], y[2], y[3]);
     }
