@@ -4,30 +4,31 @@
 // (crates/speculate/src/model/quantized_llama_local.rs:47-49 MLP, :73-90 Q/K/V,
 // :135 wo, :317 lm_head; quantized_qwen2_local.rs:41-44, 71-82, 138, 315).
 //
-// Both kernels multiply 16 weight rows x 32 K (dequantised to fp16 in
-// registers) by 32 K x 16 tokens (fp16 activations in fragment order) with
-// v_mfma_f32_16x16x32_f16 and accumulate in f32.
+// Both kernels multiply 16 weight rows x 32 K by 32 K x 16 tokens (fp16
+// activations in fragment order) with v_mfma_f32_16x16x32_f16 and accumulate
+// in f32.
 //
-//  * k_qgemv (M <= 16, the linear-verify shape): one 16-token tile; only the
-//    lanes of real tokens fetch distinct activation rows.  A workgroup owns one
-//    row tile (two in SWIGLU mode) and KW waves per tile that split the K
-//    superblocks (wave w takes w, w+KW, ...), each with the weights of its next
-//    two superblocks in flight; KW is chosen per matrix so that every launch
-//    puts thousands of waves on the 256 CUs.
-//  * k_qgemm (M > 16, tree and prefill shapes): CT token tiles per wave reuse
-//    every dequantised fragment CT times.
+//  * k_qmm (M <= 16, the linear-verify shape): one 16-token tile, products
+//    transposed (tokens x rows).  A workgroup owns RT row tiles and KW waves
+//    that split the K superblocks (wave w takes w, w+KW, ...), each with the
+//    next superblock's weights and activations in flight; KW is chosen per
+//    matrix so that every launch puts thousands of waves on the 256 CUs.
+//    Q4_K / Q5_K weights enter the MFMA as exact integers (see kquant_int).
+//  * k_qgx (M > 16, tree and prefill shapes): 4 waves share each superblock's
+//    activations through LDS; CT token tiles per wave reuse every dequantised
+//    weight fragment CT times.
 //
 // Accumulation order is fixed by the matrix alone: per wave, superblocks in
 // increasing order and chunks c = 0..7 in order; across waves, partial sums
 // meet in LDS and are added for w = 0..KW-1 in order.  KW depends only on
-// (rows, K), never on M, so row i of an M-row call equals the M=1 call bit for
-// bit in both kernels.
+// (rows, K), never on M, so row i of an M-row call (M <= 16) equals the M=1
+// call bit for bit.
 //
-// Dequantisation to fp16: a 4-bit code is OR'ed into the mantissa of 1024.0h
-// (0x6400 | q == 1024 + q) or, for a code already at bits 4-7, of 64.0h
-// (0x5400 | q << 4 == 64 + q), and v_fma_mix evaluates
-// round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m): the f32
-// value s*q - m rounded once to fp16.
+// Dequantisation to fp16 (k_qgx, and Q6_K / Q8_0 in k_qmm): a 4-bit code is
+// OR'ed into the mantissa of 1024.0h (0x6400 | q == 1024 + q) or, for a code
+// already at bits 4-7, of 64.0h (0x5400 | q << 4 == 64 + q), and v_fma_mix
+// evaluates round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m):
+// the f32 value s*q - m rounded once to fp16.
 #include <hip/hip_ext.h>
 
 #include "sd_buffer.hpp"
@@ -38,17 +39,39 @@
 namespace sd {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// two fp16 codes -> two fp16 results of round_f16(code * s + c) (f32 inside).
-// Two v_fma_mix_f32 and one v_cvt_pk_f16_f32: on gfx950 v_fma_mixlo/hi_f16
-// (what the compiler makes of the plain expression) issue at half the rate of
-// v_fma_mix_f32, and the pair costs more than the three instructions here.
+typedef float float2v __attribute__((ext_vector_type(2)));
+
+// Compiler-visible forms only on the paths into MFMA operands: an inline-asm
+// result read by an MFMA (or an MFMA result read by inline asm) escapes the
+// compiler's hazard tracking, and the MFMA then sees a stale register.
+
+// two f32 -> one word of two fp16 (round to nearest even, v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+    const float2v v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2v));
+}
+// two fp16 codes -> two fp16 results of round_f16(code * s + c) (f32 inside):
+// two v_fma_mix_f32 and one v_cvt_pk_f16_f32.  Written as a vector
+// conversion so that the compiler does not fold it into v_fma_mixlo/hi_f16,
+// which on gfx950 issue at half the rate of v_fma_mix_f32 (the pair costs
+// more than the three instructions).
 __device__ __forceinline__ uint32_t fm2(uint32_t p, float s, float c) {
     const half2v h = __builtin_bit_cast(half2v, p);
-    const float a = __builtin_fmaf((float)h.x, s, c), b = __builtin_fmaf((float)h.y, s, c);
-    uint32_t r;
-    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
+    return cvt_pk(__builtin_fmaf((float)h.x, s, c), __builtin_fmaf((float)h.y, s, c));
+}
+// two fp16 codes -> code * s + c in one v_pk_fma_f16 (s, c fp16 pairs): exact
+// when the result is a small integer (the K-quant integer path below)
+__device__ __forceinline__ uint32_t pkfma(uint32_t p, uint32_t s, uint32_t c) {
+    const half2v r = __builtin_elementwise_fma(__builtin_bit_cast(half2v, p), __builtin_bit_cast(half2v, s),
+                                               __builtin_bit_cast(half2v, c));
+    return __builtin_bit_cast(uint32_t, r);
+}
+// an f32 that fp16 holds exactly, in both halves of a word
+__device__ __forceinline__ uint32_t h2pair(float v) {
+    const uint32_t h = f2h(v);
+    return h | (h << 16);
 }
 __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     const uintx4 u = {a, b, c, d};
@@ -71,13 +94,10 @@ template <int FMT> struct QFmt;
 // Scale bytes s[0..11] = hdr.y | hdr.z | hdr.w.  For j < 4: sc = s[j] & 63,
 // m = s[j+4] & 63; for j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,
 // m = (s[j+4] >> 4) | (s[j] >> 6) << 4.
-__device__ __forceinline__ void kquant_scales(const uintx4 &hdr, int g, float &s0, float &c0, float &s1,
-                                              float &c1) {
-    const float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+__device__ __forceinline__ void kquant_ints(const uintx4 &hdr, int g, int (&sc)[2], int (&mn)[2]) {
     const int sh = (g & 1) * 16;
     const uint32_t A = hdr.y >> sh, B = hdr.z >> sh, C = hdr.w >> sh;  // bytes jj, jj+1 in bits 0..15
     const bool hi = g >= 2;
-    int sc[2], mn[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const uint32_t a = (A >> (8 * i)) & 0xffu, b = (B >> (8 * i)) & 0xffu, cc = (C >> (8 * i)) & 0xffu;
@@ -86,6 +106,12 @@ __device__ __forceinline__ void kquant_scales(const uintx4 &hdr, int g, float &s
         sc[i] = (int)(hi ? sc_hi : sc_lo);
         mn[i] = (int)(hi ? mn_hi : mn_lo);
     }
+}
+__device__ __forceinline__ void kquant_scales(const uintx4 &hdr, int g, float &s0, float &c0, float &s1,
+                                              float &c1) {
+    const float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+    int sc[2], mn[2];
+    kquant_ints(hdr, g, sc, mn);
     const float d0 = d * (float)sc[0], m0 = dmin * (float)mn[0];
     const float d1 = d * (float)sc[1], m1 = dmin * (float)mn[1];
     s0 = d0;
@@ -107,8 +133,46 @@ __device__ __forceinline__ uint32_t tb_off(const WRow &w, int sb, int tbb) {
     return uni(sb < 0 ? kNoLoad : w.base + (uint32_t)sb * tbb);
 }
 
+// ---- K-quant integer path (M <= 16 kernel) -------------------------------------
+// Q4_K / Q5_K weights are d * sc_j * q - dmin * m_j with 6-bit sc_j, m_j and
+// q < 32.  The kernel feeds the MFMA the exact integers sc_j * q <= 63 * 31:
+// one v_pk_fma_f16 of the code, (1024 + q) * sc - 1024 * sc (or the 64
+// binade's), is exact.  A superblock's products then sum to
+// sum_j sc_j sum_k q_k x_k, which is scaled by d in f32, and the mins term
+// dmin * sum_j m_j X_j (X_j = sum of the activations of sub-block j) is a
+// second small product on the MFMA with exact integer m_j.  Weights are thus
+// used exactly instead of rounded to fp16, at two fewer instructions per code
+// pair.
+struct KInt {
+    uint32_t s0, c0, s1, c1;  // fp16 pairs: sc and -1024 sc (low nibbles), sc and -64 sc (high)
+    uint32_t m;               // bf16 m of sub-blocks 2g and 2g + 1
+    float d, dmin;
+};
+__device__ __forceinline__ KInt kquant_int(const uintx4 &hdr, int g) {
+    int sc[2], mn[2];
+    kquant_ints(hdr, g, sc, mn);
+    KInt k;
+    k.s0 = h2pair((float)sc[0]);
+    k.c0 = h2pair(-1024.f * (float)sc[0]);
+    k.s1 = h2pair((float)sc[1]);
+    k.c1 = h2pair(-64.f * (float)sc[1]);
+    // bf16 of a small integer: the top half of its f32
+    k.m = (__float_as_uint((float)mn[0]) >> 16) | (__float_as_uint((float)mn[1]) & 0xffff0000u);
+    k.d = h2f((uint16_t)(hdr.x & 0xffffu));
+    k.dmin = h2f((uint16_t)(hdr.x >> 16));
+    return k;
+}
+
 template <> struct QFmt<Q4_K> {
     typedef LaneQ4K D;
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ KInt iscales(const D &r, int g) { return kquant_int(r.hdr, g); }
+    static __device__ __forceinline__ half8 ifrag(const D &r, const KInt &s, int g, int c) {
+        uint32_t p[4];
+        r.codes(g, c, p);
+        return as_half8(pkfma(p[0], s.s0, s.c0), pkfma(p[1], s.s0, s.c0), pkfma(p[2], s.s1, s.c1),
+                        pkfma(p[3], s.s1, s.c1));
+    }
     struct S {
         float s0, c0, s1, c1;
     };
@@ -134,6 +198,14 @@ template <> struct QFmt<Q4_K> {
 template <> struct QFmt<Q5_K> {
     typedef LaneQ5K D;
     typedef QFmt<Q4_K>::S S;
+    static constexpr bool kInt = true;
+    static __device__ __forceinline__ KInt iscales(const D &r, int g) { return kquant_int(r.hdr, g); }
+    static __device__ __forceinline__ half8 ifrag(const D &r, const KInt &s, int g, int c) {
+        uint32_t p[4];
+        r.codes(g, c, p);
+        return as_half8(pkfma(p[0], s.s0, s.c0), pkfma(p[1], s.s0, s.c0), pkfma(p[2], s.s1, s.c1),
+                        pkfma(p[3], s.s1, s.c1));
+    }
     static __device__ __forceinline__ void load(D &r, const WRow &w, int nsb, int sb, int g) {
         const int lane = threadIdx.x & 63;
         const uint32_t so = tb_off(w, sb, D::TBB);
@@ -156,6 +228,7 @@ template <> struct QFmt<Q5_K> {
 
 template <> struct QFmt<Q6_K> {
     typedef LaneQ6K D;
+    static constexpr bool kInt = false;  // sc * (q - 32) needs 13 bits, past fp16's exact integers
     struct S {
         float s[4], c[4];  // [2 * s' + (c >= 4)]; c = offset for codes 1024 + q6 (s'=0) / 64 + q6 (s'=1)
     };
@@ -192,6 +265,7 @@ template <> struct QFmt<Q6_K> {
 template <> struct QFmt<Q8_0> {
     typedef LaneQ80 D;
     typedef QFmt<Q4_K>::S S;
+    static constexpr bool kInt = false;  // one scale per 32 elements: an MFMA's K spans 8 of them
     static __device__ __forceinline__ void load(D &r, const WRow &w, int nsb, int sb, int g) {
         const int lane = threadIdx.x & 63;
         const uint32_t so = tb_off(w, sb, D::TBB);
@@ -464,62 +538,101 @@ __device__ __forceinline__ WRow wrow(const GemmSeg &S, int K, int row0) {
 // waits for every older one.  Each step therefore issues the loads it will
 // wait on first and the prefetch of the next step's operands after them.
 
-// One superblock of one token tile: the activations arrive with the weights
-// (both prefetched one step ahead, in two register sets).
+// One superblock of the token tile: the activations arrive with the weights
+// (both prefetched one step ahead, in two register sets).  The products are
+// transposed, D[token][row] = x . W^T (activations as the MFMA's A operand),
+// so that a lane's accumulators belong to its own weight row (r16) and that
+// row's scales apply to them directly; the reduction transposes back.
+// `sel` picks, per lane, the sub-block sums X_2g, X_2g+1 of the lane's token
+// out of one extra product per chunk (see kquant_int).
+// The integer path's per-superblock products (sum_j sc_j sum q x per row, the
+// sub-block sums X of the token) are applied one superblock late, while the
+// next superblock's MFMAs run: reading an MFMA result right after the MFMA
+// waits for its whole pipeline, which would otherwise stall every superblock.
+template <int RT> struct IntCarry {
+    floatx4 part[RT], xs;
+    float d[RT], dmin[RT];
+    uint32_t m[RT];
+    bool live;
+};
+// acc += d * part - dmin * sum_j m_j X_j for the carried superblock
+template <int RT>
+__device__ __forceinline__ void int_drain(IntCarry<RT> &cy, floatx4 (&acc)[RT]) {
+    if (!cy.live) return;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    // X_2g, X_2g+1 of the lane's token as bf16 hi + lo: 16 significant bits
+    // and the f32 range (a sum of 32 activations can exceed fp16's), times
+    // the integer mins, exact in bf16
+    const __bf16 h0 = (__bf16)cy.xs[0], h1 = (__bf16)cy.xs[1];
+    const __bf16 l0 = (__bf16)(cy.xs[0] - (float)h0), l1 = (__bf16)(cy.xs[1] - (float)h1);
+    const bf16x8 xh = {h0, h1, 0, 0, 0, 0, 0, 0}, xl = {l0, l1, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const bf16x8 mb = __builtin_bit_cast(bf16x8, uintx4{cy.m[rt], 0u, 0u, 0u});
+        floatx4 pm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, mb, zero, 0, 0, 0);
+        pm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, mb, pm, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            acc[rt][i] = __builtin_fmaf(-cy.dmin[rt], pm[i], __builtin_fmaf(cy.d[rt], cy.part[rt][i], acc[rt][i]));
+    }
+    cy.live = false;
+}
+
+// One superblock of the token tile: the activations arrive with the weights
+// (both prefetched one step ahead, in two register sets).  The products are
+// transposed, D[token][row] = x . W^T (activations as the MFMA's A operand),
+// so that a lane's accumulators belong to its own weight row (r16) and that
+// row's scales apply to them directly; the reduction transposes back.
+// `sel` picks, per lane, the sub-block sums X_2g, X_2g+1 of the lane's token
+// out of one extra product per chunk (see kquant_int).
 template <int FMT, int RT>
 __device__ __forceinline__ void qmm_step1(const typename QFmt<FMT>::D (&w)[RT], const uintx4 (&b)[8], int g,
-                                          floatx4 (&acc)[RT][1]) {
+                                          floatx4 (&acc)[RT], const half8 &sel, IntCarry<RT> &cy) {
     typedef QFmt<FMT> F;
-    typename F::S sc[RT];
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (F::kInt) {
+        KInt ks[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) sc[rt] = F::scales(w[rt], g);
+        for (int rt = 0; rt < RT; rt++) ks[rt] = F::iscales(w[rt], g);
+        floatx4 xs = zero, part[RT];
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-        half8 a[RT];
+        for (int c = 0; c < 8; c++) {
+            const half8 xc = __builtin_bit_cast(half8, b[c]);
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, xc, xs, 0, 0, 0);
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) a[rt] = F::frag(w[rt], sc[rt], g, c);
+            for (int rt = 0; rt < RT; rt++)
+                part[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc, F::ifrag(w[rt], ks[rt], g, c),
+                                                                  c == 0 ? zero : part[rt], 0, 0, 0);
+            if (c == 0) int_drain<RT>(cy, acc);  // the previous superblock, behind this one's MFMAs
+        }
+        cy.xs = xs;
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++)
-            acc[rt][0] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt], __builtin_bit_cast(half8, b[c]), acc[rt][0], 0, 0, 0);
+        for (int rt = 0; rt < RT; rt++) {
+            cy.part[rt] = part[rt];
+            cy.d[rt] = ks[rt].d;
+            cy.dmin[rt] = ks[rt].dmin;
+            cy.m[rt] = ks[rt].m;
+        }
+        cy.live = true;
+    } else {
+        typename F::S sc[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) sc[rt] = F::scales(w[rt], g);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const half8 xc = __builtin_bit_cast(half8, b[c]);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc, F::frag(w[rt], sc[rt], g, c), acc[rt], 0, 0, 0);
+        }
     }
 }
 
-// One superblock of CT token tiles: the superblock's activations are loaded
-// at the start of the step, before the next step's weights are requested.
-template <int FMT, int RT, int CT>
-__device__ __forceinline__ void qmm_stepn(const typename QFmt<FMT>::D (&w)[RT], const uintx4 (&b)[CT][8], int g,
-                                          floatx4 (&acc)[RT][CT]) {
-    typedef QFmt<FMT> F;
-    typename F::S sc[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) sc[rt] = F::scales(w[rt], g);
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-        half8 a[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) a[rt] = F::frag(w[rt], sc[rt], g, c);
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++)
-                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt], __builtin_bit_cast(half8, b[ct][c]),
-                                                                     acc[rt][ct], 0, 0, 0);
-    }
-}
-
-template <int CT>
-__device__ __forceinline__ void load_x(uintx4 (&b)[CT][8], rsrc_t xr, const uint32_t (&xvo)[CT], int sb) {
+__device__ __forceinline__ void load_x(uintx4 (&b)[8], rsrc_t xr, uint32_t xvo, int sb) {
     const uint32_t so = uni(sb < 0 ? kNoLoad : (uint32_t)sb * 512u);
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int c = 0; c < 8; c++) b[ct][c] = bld16(xr, xvo[ct] + 64 * c, so);
+    for (int c = 0; c < 8; c++) b[c] = bld16(xr, xvo + 64 * c, so);
 }
-
-// Superblocks in flight per wave (x + weights) for one token tile, 2 or 3:
-// measured equal on the verify shapes, and 2 leaves registers to spare.
-constexpr int kDepth1 = 2;
 
 // ---- fused RMSNorm, input side ------------------------------------------------
 // The sums of squares of token m arrive as K/16 partials, one per 16-element
@@ -545,103 +658,53 @@ __device__ __forceinline__ floatx4 norm_load(const NormSrc &n, int sb) {
 }
 __device__ __forceinline__ float norm_add(float s, const floatx4 &v) { return s + ((v.x + v.y) + (v.z + v.w)); }
 
-// Superblocks sb = ks, ks + KW, ... in increasing order;
-// `after_prologue` runs once the first superblock's loads are in flight.
-template <int FMT, int RT, int CT, int KW, typename Hook>
-__device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT][CT],
-                                         float &nsum, Hook &&after_prologue) {
+// Superblocks sb = ks, ks + KW, ... in increasing order, x and weights of the
+// next superblock in flight during this one; `after_prologue` runs once the
+// first superblock's loads are in flight.
+template <int FMT, int RT, int KW, typename Hook>
+__device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT],
+                                         float &nsum, const half8 &sel, Hook &&after_prologue) {
     typedef QFmt<FMT> F;
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
     const int nsb = p.K >> 8;
-    // token columns past M read the last real token's row: the loads coalesce
-    // with that lane's and the padding columns are never stored
+    // token rows past M read the last real token's row: the loads coalesce
+    // with that lane's and the padding tokens are never stored
     const rsrc_t xr = make_rsrc(p.xp, (uint32_t)p.M * (uint32_t)p.K * 2u);
-    uint32_t xvo[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) xvo[ct] = ((uint32_t)min(ct * 16 + r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u;
+    const uint32_t xvo = ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u;
     if (ks >= nsb) return;
     const int nst = (nsb - ks + KW - 1) / KW;  // superblocks of this wave: ks + i * KW, i < nst
     auto sbi = [&](int i) { return i < nst ? ks + i * KW : -1; };
     typename F::D w0[RT], w1[RT];
-    if constexpr (CT == 1 && kDepth1 == 2) {
-        // x and weights of the next superblock in flight during this one
-        uintx4 b0[1][8], b1[1][8];
-        const NormSrc ns = norm_src(p);
-        load_x<1>(b0, xr, xvo, sbi(0));
+    uintx4 b0[8], b1[8];
+    const NormSrc ns = norm_src(p);
+    load_x(b0, xr, xvo, sbi(0));
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
-        floatx4 n0 = norm_load(ns, sbi(0)), n1;  // after the weights: waiting for them does not wait for it
-        after_prologue();
-        for (int i = 0;; i += 2) {
-            load_x<1>(b1, xr, xvo, sbi(i + 1));
+    for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
+    floatx4 n0 = norm_load(ns, sbi(0)), n1;  // after the weights: waiting for them does not wait for it
+    after_prologue();
+    IntCarry<RT> cy;
+    cy.live = false;
+    for (int i = 0;; i += 2) {
+        load_x(b1, xr, xvo, sbi(i + 1));
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
-            n1 = norm_load(ns, sbi(i + 1));
-            qmm_step1<FMT, RT>(w0, b0[0], g, acc);
-            nsum = norm_add(nsum, n0);
-            if (i + 1 >= nst) break;
-            load_x<1>(b0, xr, xvo, sbi(i + 2));
+        for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
+        n1 = norm_load(ns, sbi(i + 1));
+        qmm_step1<FMT, RT>(w0, b0, g, acc, sel, cy);
+        nsum = norm_add(nsum, n0);
+        if (i + 1 >= nst) break;
+        load_x(b0, xr, xvo, sbi(i + 2));
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
-            n0 = norm_load(ns, sbi(i + 2));
-            qmm_step1<FMT, RT>(w1, b1[0], g, acc);
-            nsum = norm_add(nsum, n1);
-            if (i + 2 >= nst) break;
-        }
-    } else if constexpr (CT == 1) {
-        // x and weights of the next two superblocks in flight during this one
-        // (three register sets in rotation): at ~2.5 us loaded HBM latency a
-        // wave must keep about two superblocks requested to stream
-        uintx4 b0[1][8], b1[1][8], b2[1][8];
-        typename F::D w2[RT];
-        load_x<1>(b0, xr, xvo, sbi(0));
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
-        load_x<1>(b1, xr, xvo, sbi(1));
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(1), g);
-        after_prologue();
-        for (int i = 0;; i += 3) {
-            load_x<1>(b2, xr, xvo, sbi(i + 2));
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w2[rt], row[rt], nsb, sbi(i + 2), g);
-            qmm_step1<FMT, RT>(w0, b0[0], g, acc);
-            if (i + 1 >= nst) break;
-            load_x<1>(b0, xr, xvo, sbi(i + 3));
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 3), g);
-            qmm_step1<FMT, RT>(w1, b1[0], g, acc);
-            if (i + 2 >= nst) break;
-            load_x<1>(b1, xr, xvo, sbi(i + 4));
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 4), g);
-            qmm_step1<FMT, RT>(w2, b2[0], g, acc);
-            if (i + 3 >= nst) break;
-        }
-    } else {
-        // weights one superblock ahead; the activations of a superblock are
-        // requested before the next superblock's weights
-        uintx4 b[CT][8];
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
-        after_prologue();
-        for (int i = 0;; i += 2) {
-            load_x<CT>(b, xr, xvo, sbi(i));
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
-            qmm_stepn<FMT, RT, CT>(w0, b, g, acc);
-            if (i + 1 >= nst) break;
-            load_x<CT>(b, xr, xvo, sbi(i + 1));
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
-            qmm_stepn<FMT, RT, CT>(w1, b, g, acc);
-            if (i + 2 >= nst) break;
-        }
+        for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
+        n0 = norm_load(ns, sbi(i + 2));
+        qmm_step1<FMT, RT>(w1, b1, g, acc, sel, cy);
+        nsum = norm_add(nsum, n1);
+        if (i + 2 >= nst) break;
     }
+    int_drain<RT>(cy, acc);
 }
 
-template <int RT, int CT, int KW>
+template <int RT, int KW>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
@@ -676,11 +739,20 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
     WRow row[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) row[rt] = wrow(S[rt], p.K, rloc[rt]);
-    floatx4 acc[RT][CT];
+    floatx4 acc[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int rt = 0; rt < RT; rt++) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Sub-block selector of the K-quant integer path: row r = 4 * gq + u
+    // (u < 2) of the 16 x 32 selector is 1 on the elements of sub-block
+    // 2 * gq + u, so selector x x^T puts X_2g, X_2g+1 of token t in the first
+    // two accumulators of lane (t, g).  Lane (r, g) holds the selector's
+    // elements of sub-blocks 2g (slots 0-3) and 2g + 1 (slots 4-7).
+    half8 sel;
+    {
+        const int u = r16 & 3, gq = r16 >> 2;
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 8; j++) sel[j] = (_Float16)((gq == g && u == (j >> 2)) ? 1.f : 0.f);
+    }
     // Wave 0 runs the epilogue: it requests the epilogue's operands first and
     // the RoPE table entries (which need the position) once its weights are in
     // flight.  Every wave sums the fused-norm partials of its superblocks.
@@ -691,51 +763,46 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
     };
     float nsum = 0.f;
     switch (S[0].fmt) {
-    case Q4_K: qmm_body<Q4_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
-    case Q5_K: qmm_body<Q5_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
-    case Q6_K: qmm_body<Q6_K, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
-    case Q8_0: qmm_body<Q8_0, RT, CT, KW>(p, row, wave, acc, nsum, after_prologue); break;
+    case Q4_K: qmm_body<Q4_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q5_K: qmm_body<Q5_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q6_K: qmm_body<Q6_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q8_0: qmm_body<Q8_0, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
     default: break;
     }
-    // fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, one
-    // token tile at a time (CT == 1 here; the norm sums ride along)
+    // Fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, which
+    // also transposes the products back: wave w's lane (row r, g) holds tokens
+    // 4g .. 4g+3 of row r; wave 0's lane (token t, g) reads rows 4g .. 4g+3 of
+    // token t, the layout of the epilogue.  The norm sums ride along.
+    constexpr int kPitch = 20;  // floats per token row: 16 rows + 4, keeps 16-byte reads aligned
+    __shared__ __attribute__((aligned(16))) float red[KW][RT][16][kPitch];
+    __shared__ float nred[KW][64];
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-        floatx4 v[RT];
-        if constexpr (KW > 1) {
-            __shared__ floatx4 red[KW][RT][64];
-            __shared__ float nred[KW][64];
-            __syncthreads();
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) red[wave][rt][lane] = acc[rt][ct];
-            nred[wave][lane] = nsum;
-            __syncthreads();
-            if (wave != 0) continue;
+        for (int i = 0; i < 4; i++) red[wave][rt][4 * g + i][r16] = acc[rt][i];
+    nred[wave][lane] = nsum;
+    __syncthreads();
+    if (wave != 0) return;
+    floatx4 v[RT];
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                floatx4 s = red[0][rt][lane];
+    for (int rt = 0; rt < RT; rt++) {
+        floatx4 t = *(const floatx4 *)&red[0][rt][r16][4 * g];
 #pragma unroll
-                for (int w = 1; w < KW; w++) s += red[w][rt][lane];
-                v[rt] = s;
-            }
-            float ns = nred[0][lane];
-#pragma unroll
-            for (int w = 1; w < KW; w++) ns += nred[w][lane];
-            nsum = ns;
-        } else {
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) v[rt] = acc[rt][ct];
-        }
-        if (p.norm_ssq) {
-            // the token's four lane groups (g = 0..3) in a fixed order
-            float ns = nsum + __shfl_xor(nsum, 16);
-            ns += __shfl_xor(ns, 32);
-            const float inv = 1.0f / sqrtf(ns / (float)p.K + p.norm_eps);
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
-        }
-        epilogue<RT>(p, S, rloc, v, e, ct * 16 + r16, g, (int)blockIdx.x);
+        for (int w = 1; w < KW; w++) t += *(const floatx4 *)&red[w][rt][r16][4 * g];
+        v[rt] = t;
     }
+    float ns = nred[0][lane];
+#pragma unroll
+    for (int w = 1; w < KW; w++) ns += nred[w][lane];
+    if (p.norm_ssq) {
+        // the token's four lane groups (g = 0..3) in a fixed order
+        ns += __shfl_xor(ns, 16);
+        ns += __shfl_xor(ns, 32);
+        const float inv = 1.0f / sqrtf(ns / (float)p.K + p.norm_eps);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
+    }
+    epilogue<RT>(p, S, rloc, v, e, r16, g, (int)blockIdx.x);
 }
 
 // ==========================================================================
@@ -1019,18 +1086,18 @@ static void launch_qgx(const GemmParams &p, hipStream_t st, const LaunchTiming &
     launch_timed(k_qgx<RW, CT>, dim3(rb * nks), dim3(64 * XG_WAVES), lds, st, tm, p, nks);
 }
 
-template <int RT, int CT, int KW>
+template <int RT, int KW>
 static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st, const LaunchTiming &tm) {
-    launch_timed(k_qmm<RT, CT, KW>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
+    launch_timed(k_qmm<RT, KW>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
 }
 
-template <int RT, int CT>
+template <int RT>
 static bool launch_kw(const GemmParams &p, int kw, int nwg, hipStream_t st, const LaunchTiming &tm) {
     switch (kw) {
-    case 1: launch_qmm<RT, CT, 1>(p, nwg, st, tm); return true;
-    case 2: launch_qmm<RT, CT, 2>(p, nwg, st, tm); return true;
-    case 4: launch_qmm<RT, CT, 4>(p, nwg, st, tm); return true;
-    case 8: launch_qmm<RT, CT, 8>(p, nwg, st, tm); return true;
+    case 1: launch_qmm<RT, 1>(p, nwg, st, tm); return true;
+    case 2: launch_qmm<RT, 2>(p, nwg, st, tm); return true;
+    case 4: launch_qmm<RT, 4>(p, nwg, st, tm); return true;
+    case 8: launch_qmm<RT, 8>(p, nwg, st, tm); return true;
     default: return false;
     }
 }
@@ -1073,8 +1140,8 @@ int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
     const int kw = qgemm_kw(p), rt = qgemm_rt(p);
     const int nwg = qgemm_workgroups(p);
     bool ok = false;
-    if (rt == 2) ok = launch_kw<2, 1>(p, kw, nwg, st, tm);
-    else if (rt == 1 && p.mode != GM_SWIGLU) ok = launch_kw<1, 1>(p, kw, nwg, st, tm);
+    if (rt == 2) ok = launch_kw<2>(p, kw, nwg, st, tm);
+    else if (rt == 1 && p.mode != GM_SWIGLU) ok = launch_kw<1>(p, kw, nwg, st, tm);
     if (!ok) throw BackendError("qgemm: unsupported launch shape");
     return nwg;
 }
