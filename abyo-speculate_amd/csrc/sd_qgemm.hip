@@ -264,7 +264,12 @@ template <> struct QFmt<Q6_K> {
 
 template <> struct QFmt<Q8_0> {
     typedef LaneQ80 D;
-    typedef QFmt<Q4_K>::S S;
+    // d of blocks 2g and 2g+1 in both halves of a word: fp16 (d * q) with d
+    // itself fp16 is one v_pk_mul_f16 of the exact integer q, the same single
+    // rounding as the f32 route at a third of its cost
+    struct S {
+        uint32_t d0, d1;
+    };
     static constexpr bool kInt = false;  // one scale per 32 elements: an MFMA's K spans 8 of them
     static __device__ __forceinline__ void load(D &r, const WRow &w, int nsb, int sb, int g) {
         const int lane = threadIdx.x & 63;
@@ -276,18 +281,20 @@ template <> struct QFmt<Q8_0> {
         r.d = bld4(w.rs, D::off_d(lane), so);
     }
     static __device__ __forceinline__ S scales(const D &r, int g) {
-        const float da = h2f((uint16_t)(r.d & 0xffffu)), db = h2f((uint16_t)(r.d >> 16));
         S s;
-        s.s0 = da;
-        s.c0 = -1152.f * da;  // codes 1024 + (q + 128)
-        s.s1 = db;
-        s.c1 = -1152.f * db;
+        s.d0 = (r.d & 0xffffu) * 0x10001u;
+        s.d1 = (r.d >> 16) * 0x10001u;
         return s;
+    }
+    // codes 1024 + (q + 128) -> q (exact) -> round_f16(q * d)
+    static __device__ __forceinline__ uint32_t qd2(uint32_t p, uint32_t d) {
+        const half2v q = __builtin_bit_cast(half2v, p) + (half2v){(_Float16)-1152.f, (_Float16)-1152.f};
+        return __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(half2v, d));
     }
     static __device__ __forceinline__ half8 frag(const D &r, const S &s, int g, int c) {
         uint32_t p[4];
         r.codes(g, c, p);
-        return as_half8(fm2(p[0], s.s0, s.c0), fm2(p[1], s.s0, s.c0), fm2(p[2], s.s1, s.c1), fm2(p[3], s.s1, s.c1));
+        return as_half8(qd2(p[0], s.d0), qd2(p[1], s.d0), qd2(p[2], s.d1), qd2(p[3], s.d1));
     }
 };
 
