@@ -6,12 +6,17 @@
 #include "speculate_hip.h"
 #include "sd_model.hpp"
 #include "sd_common.hpp"
+#include "sd_gguf.hpp"
 #include "sd_qcodes.hpp"
 #include "sd_tiles.hpp"
 
 struct sd_model {
     std::unique_ptr<sd::Model> model;
     std::unique_ptr<sd::Decoder> dec;
+};
+
+struct sd_gguf {
+    std::unique_ptr<sd::GgufFile> file;
 };
 
 static thread_local std::string g_err;
@@ -119,6 +124,79 @@ sd_status sd_model_synthesize(sd_model *m, int32_t mix, uint64_t seed, float std
     return guard([&] {
         need(m);
         m->model->synthesize(mix, seed, stdv);
+        m->dec->last_valid = false;
+    });
+}
+
+sd_status sd_gguf_open(const char *path, sd_gguf **out) {
+    return guard([&] {
+        if (!path || !out) throw sd::ArgError("null argument");
+        *out = nullptr;
+        auto g = std::make_unique<sd_gguf>();
+        g->file = std::make_unique<sd::GgufFile>(path);
+        *out = g.release();
+    });
+}
+
+void sd_gguf_close(sd_gguf *g) { delete g; }
+
+static const sd::GgufFile &gfile(const sd_gguf *g) {
+    if (!g || !g->file) throw sd::ArgError("null gguf handle");
+    return *g->file;
+}
+
+sd_status sd_gguf_config(const sd_gguf *g, int32_t arch, sd_config *cfg) {
+    return guard([&] {
+        if (!cfg) throw sd::ArgError("null argument");
+        const sd::ModelCfg c = gfile(g).config(arch);
+        sd_config o;
+        o.arch = c.arch;
+        o.n_layers = c.n_layers;
+        o.hidden = c.hidden;
+        o.n_heads = c.n_heads;
+        o.n_kv_heads = c.n_kv_heads;
+        o.head_dim = c.head_dim;
+        o.ffn = c.ffn;
+        o.vocab = c.vocab;
+        o.rope_theta = c.rope_theta;
+        o.rms_eps = c.rms_eps;
+        o.ctx_len = c.ctx_len;
+        o.max_batch = c.max_batch;
+        o.tied_output = c.tied_output;
+        o.device = c.device;
+        *cfg = o;
+    });
+}
+
+sd_status sd_gguf_layout(const sd_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset) {
+    return guard([&] {
+        const sd::GgufFile &f = gfile(g);
+        if (version) *version = f.version;
+        if (alignment) *alignment = f.alignment;
+        if (data_offset) *data_offset = f.data_start;
+    });
+}
+
+size_t sd_gguf_tensor_count(const sd_gguf *g) { return g && g->file ? g->file->tensors.size() : 0; }
+
+sd_status sd_gguf_tensor_info(const sd_gguf *g, const char *name, int32_t *type, int32_t *n_dims, uint64_t *ne,
+                              uint64_t *offset) {
+    return guard([&] {
+        if (!name) throw sd::ArgError("null name");
+        const sd::GgufTensor &t = gfile(g).tensor(name);
+        if (type) *type = (int32_t)t.type;
+        if (n_dims) *n_dims = (int32_t)t.n_dims;
+        if (ne)
+            for (int d = 0; d < 4; d++) ne[d] = t.ne[d];
+        if (offset) *offset = t.offset;
+    });
+}
+
+sd_status sd_model_load_gguf(sd_model *m, const sd_gguf *g) {
+    return guard([&] {
+        need(m);
+        const sd::GgufFile &f = gfile(g);
+        f.load(*m->model);
         m->dec->last_valid = false;
     });
 }

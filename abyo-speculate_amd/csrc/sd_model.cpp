@@ -12,7 +12,9 @@ namespace sd {
 static const bool kIsF32Kind[K_NUM] = {false, false, true, false, false, false, false,
                                        false, false, false, true, true, true, true, true};
 
-static void shape_of(const ModelCfg &c, int kind, int &rows, int &K) {
+bool kind_is_f32(int kind) { return kind >= 0 && kind < K_NUM && kIsF32Kind[kind]; }
+
+void tensor_shape(const ModelCfg &c, int kind, int &rows, int &K) {
     const int H = c.hidden, F = c.ffn;
     switch (kind) {
     case K_TOK_EMBD: case K_OUTPUT: rows = c.vocab; K = H; break;
@@ -181,7 +183,7 @@ static DevTensor &slot(Model &m, int layer, int kind) {
 void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t bytes) {
     DevTensor &t = slot(*this, layer, kind);
     int rows, K;
-    shape_of(cfg, kind, rows, K);
+    tensor_shape(cfg, kind, rows, K);
     check_fmt(kind, fmt, K);
     const size_t want = (size_t)rows * gguf_row_bytes(fmt, K);
     if (bytes != want) throw ArgError("tensor byte size does not match its shape and format");
@@ -282,7 +284,7 @@ void Model::synthesize(int mix, uint64_t seed, float stdv) {
     auto make = [&](int layer, int kind) {
         DevTensor &t = slot(*this, layer, kind);
         int rows, K;
-        shape_of(cfg, kind, rows, K);
+        tensor_shape(cfg, kind, rows, K);
         const int fmt = mix_fmt(mix, cfg.n_layers, layer, kind);
         if ((size_t)dev_tensor_bytes(fmt, rows, K) >= ((size_t)1 << 31))
             throw UnsupportedError("a matrix must be smaller than 2 GiB (32-bit buffer offsets)");

@@ -51,6 +51,11 @@ struct ModelCfg {
     int kv_dim() const { return n_kv_heads * head_dim; }
 };
 
+// [rows][K] of a tensor kind under a config (norms and biases: rows = 1), and
+// whether the kind is an F32 vector (norm or bias) rather than a matrix
+void tensor_shape(const ModelCfg &c, int kind, int &rows, int &K);
+bool kind_is_f32(int kind);
+
 struct DevTensor {
     int fmt = -1;
     int rows = 0, K = 0;

@@ -155,6 +155,13 @@ def load_library(path: str = LIB_PATH):
         "sd_unpack_tiles": ([I32, P, SZ, SZ, P], I32),
         "sd_lane_codes": ([I32, P, I32, I32, P], I32),
         "sd_tree_prune": ([P, P, SZ, P, P, SZ, SZ, P, P, pSZ], I32),
+        "sd_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(P)], I32),
+        "sd_gguf_close": ([P], None),
+        "sd_gguf_config": ([P, I32, ctypes.POINTER(SdConfig)], I32),
+        "sd_gguf_layout": ([P, P, P, P], I32),
+        "sd_gguf_tensor_count": ([P], SZ),
+        "sd_gguf_tensor_info": ([P, ctypes.c_char_p, P, P, P, P], I32),
+        "sd_model_load_gguf": ([P, P], I32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -190,8 +197,88 @@ def tree_arrays(tree) -> Tuple[np.ndarray, np.ndarray]:
     return _u32(toks), _u32(pars)
 
 
+class GgufFile:
+    """An opened .gguf file (gguf_file::Content::read, candle-core 0.8.4): the
+    header, metadata and tensor directory.  Parsing is host code; no GPU needed."""
+
+    def __init__(self, path: str):
+        L = load_library()
+        h = ctypes.c_void_p()
+        _check(L.sd_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+        self.path = path
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.sd_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def config(self, arch: int = -1, ctx_len: Optional[int] = None, max_batch: int = 128,
+               device: int = 0) -> Config:
+        """ModelWeights::from_gguf's hyper-parameters (quantized_llama_local.rs:222-240,
+        quantized_qwen2_local.rs:215-230); arch -1 reads general.architecture.
+        ctx_len defaults to the file's context_length."""
+        c = SdConfig()
+        _check(_lib.sd_gguf_config(self._h, arch, ctypes.byref(c)))
+        cfg = Config(**{k: getattr(c, k) for k, _ in SdConfig._fields_})
+        if ctx_len is not None:
+            cfg.ctx_len = ctx_len
+        cfg.max_batch = max_batch
+        cfg.device = device
+        return cfg
+
+    def layout(self) -> Tuple[int, int, int]:
+        """(GGUF version, alignment, absolute offset of the data section)."""
+        v, a, d = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(_lib.sd_gguf_layout(self._h, ctypes.byref(v), ctypes.byref(a), ctypes.byref(d)))
+        return v.value, a.value, d.value
+
+    def tensor_count(self) -> int:
+        return int(_lib.sd_gguf_tensor_count(self._h))
+
+    def tensor_info(self, name: str) -> Tuple[int, Tuple[int, ...], int]:
+        """(GGML type, dims with ne[0] first, offset from the data section)."""
+        t, nd = ctypes.c_int32(), ctypes.c_int32()
+        ne = np.zeros(4, np.uint64)
+        off = ctypes.c_uint64()
+        _check(_lib.sd_gguf_tensor_info(self._h, name.encode(), ctypes.byref(t), ctypes.byref(nd), _ptr(ne),
+                                        ctypes.byref(off)))
+        return t.value, tuple(int(v) for v in ne[:nd.value]), off.value
+
+
 class HipQuantDecoder:
     """One quantised target decoder resident on one GPU (LlamaQuantDecoder contract)."""
+
+    @classmethod
+    def from_gguf(cls, gguf_path: str, arch: int = -1, ctx_len: Optional[int] = None, max_batch: int = 128,
+                  device: int = 0, eos_token_ids: Sequence[int] = ()) -> "HipQuantDecoder":
+        """LlamaQuantDecoder::from_gguf / Qwen2QuantDecoder::from_gguf
+        (quantized_llama.rs:57-98, quantized_qwen2.rs:55-100) without the
+        tokenizer: the config from the file's metadata, then every tensor.
+        arch picks the decoder type (ARCH_LLAMA reads llama.* keys); -1 follows
+        general.architecture."""
+        with GgufFile(gguf_path) as g:
+            dec = cls(g.config(arch, ctx_len=ctx_len, max_batch=max_batch, device=device))
+            try:
+                _check(_lib.sd_model_load_gguf(dec._h, g._h))
+            except Exception:
+                dec.close()
+                raise
+        if eos_token_ids:
+            dec.set_eos_token_ids(eos_token_ids)
+        return dec
 
     def __init__(self, cfg: Config):
         L = load_library()

@@ -241,6 +241,27 @@ def main():
                      "bytes_per_launch": int(per_launch_bytes), "avg_launch_us": round(avg_launch_s * 1e6, 2)},
     }
 
+    # ---------------- M=1 decode step (what autoregressive decoding runs per token) ----------------
+    dec.rollback_to(n0)
+
+    def step_ar():
+        dec.observe(drafts[:1])
+        dec.rollback_to(n0)
+
+    for _ in range(args.warmup):
+        step_ar()
+    dec.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step_ar()
+    dec.synchronize()
+    t_ar = (time.perf_counter() - t0) / args.steps
+    log(f"M=1 decode step: {t_ar * 1e6:.1f} us")
+    result["ar_m1"] = {"us": round(t_ar * 1e6, 1), "tokens_per_s": round(1.0 / t_ar, 1),
+                       "kv_positions": args.prefix,
+                       "what": "observe of one token: M=1 forward with the lm_head row (the step an autoregressive "
+                               "decoder runs per token, logits left on the device)"}
+
     # ---------------- 60-node tree verify ----------------
     if not args.no_tree:
         hist = [int(v) for v in rng.integers(0, cfg.vocab, args.tree_prefix + 1)]

@@ -278,6 +278,44 @@ sd_status sd_unpack_tiles(int32_t fmt, const void *tiles, size_t rows, size_t K,
  * 64 + q for slots 4-7 (1024 + q + 128 throughout for Q8_0). */
 sd_status sd_lane_codes(int32_t fmt, const void *tile_block, int32_t lane, int32_t chunk, uint32_t *out);
 
+/* ---- GGUF files (parsing is host only; sd_model_load_gguf uploads) -------------- */
+/* An opened .gguf file: header, metadata and tensor directory, read as
+ * gguf_file::Content::read (candle-core 0.8.4) does at quantized_llama.rs:63-65
+ * / quantized_qwen2.rs:61-63 (GGUF v1-v3; general.alignment, default 32).  The
+ * file stays memory-mapped until sd_gguf_close.  A malformed file is
+ * SD_ERR_BACKEND (Error::Candle), never an out-of-range read. */
+typedef struct sd_gguf sd_gguf;
+sd_status sd_gguf_open(const char *path, sd_gguf **out);
+void sd_gguf_close(sd_gguf *g);
+/* The hyper-parameters ModelWeights::from_gguf reads
+ * (quantized_llama_local.rs:222-240, quantized_qwen2_local.rs:215-230): arch
+ * SD_ARCH_LLAMA / SD_ARCH_QWEN2 picks the key prefix ("llama." / "qwen2.", the
+ * decoder type the caller builds), -1 takes it from general.architecture.
+ * Missing keys fail in the reference's order ("cannot find <key> in GGUF
+ * metadata"); rope.freq_base defaults to 10000; head_dim = embedding_length /
+ * head_count; ffn and vocab are the rows of blk.0.ffn_gate.weight and
+ * token_embd.weight; tied_output = 1 when output.weight is absent (the
+ * fallback at quantized_llama_local.rs:248-252).  ctx_len is set to
+ * context_length, max_batch to 128, device to 0: the caller may change these
+ * three before sd_model_create. */
+sd_status sd_gguf_config(const sd_gguf *g, int32_t arch, sd_config *cfg);
+/* File layout: GGUF version, alignment and the absolute offset of the data section. */
+sd_status sd_gguf_layout(const sd_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset);
+size_t sd_gguf_tensor_count(const sd_gguf *g);
+/* One tensor-directory entry: GGML type, dims (ne[0] the contiguous one; the
+ * unused ones are 1), offset from the data section.  SD_ERR_BACKEND "cannot
+ * find tensor info for <name>" if absent (Content::tensor). */
+sd_status sd_gguf_tensor_info(const sd_gguf *g, const char *name, int32_t *type, int32_t *n_dims, uint64_t *ne,
+                              uint64_t *offset);
+/* Uploads every tensor ModelWeights::from_gguf loads
+ * (quantized_llama_local.rs:242-281, quantized_qwen2_local.rs:232-283), in
+ * its order; F16/BF16 norms and biases are widened to F32 as
+ * RmsNorm::from_qtensor / dequantize do.  All tensors are checked (present,
+ * shape, Q4_K/Q5_K/Q6_K/Q8_0 matrices, data inside the file) before the first
+ * upload; the model must have been created from this file's config (ctx_len,
+ * max_batch and device aside), else SD_ERR_ARG. */
+sd_status sd_model_load_gguf(sd_model *m, const sd_gguf *g);
+
 /* ---- draft-tree builders (host only; no GPU needed) ---------------------------- */
 /* build_cartesian_tree (methods/medusa.rs:172-193): step d has branching[d]
  * candidate tokens, stored back to back in cand[]; layer d+1 hangs every
