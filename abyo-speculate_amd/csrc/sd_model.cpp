@@ -74,8 +74,8 @@ Model::~Model() {
     }
     for (void *p : {(void *)kv, (void *)cos_t, (void *)sin_t, (void *)h, (void *)qkv, (void *)logits,
                     (void *)hidden_out, (void *)last_row, (void *)part_o, (void *)part_ml, (void *)amax_v,
-                    (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids, (void *)d_pos,
-                    (void *)d_src, (void *)d_mask, (void *)xp, (void *)ap, (void *)act, (void *)q16,
+                    (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids,
+                    (void *)d_src, (void *)xp, (void *)ap, (void *)act, (void *)q16,
                     (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part})
         F(p);
@@ -127,10 +127,12 @@ void Model::alloc_buffers() {
     amax_i = dalloc<int>((size_t)Mx * amax_ld);
     argmax = dalloc<int>(Mx);
     collect_buf = dalloc<float>((size_t)c.n_layers * c.hidden);
-    d_ids = dalloc<int>(Mx);
-    d_pos = dalloc<int>(Mx);
+    // ids | pos | (unused) | mask in one block laid out as the pinned staging
+    // buffer, so that one copy uploads a forward's inputs
+    d_ids = dalloc<int>((size_t)3 * Mx + (Mx & 1) + (size_t)4 * Mx);
+    d_pos = d_ids + Mx;
+    d_mask = (uint64_t *)(d_ids + 3 * Mx + (Mx & 1));
     d_src = dalloc<int>(Mx);
-    d_mask = dalloc<uint64_t>((size_t)Mx * 2);
     qg_part_cap = std::max<int64_t>((int64_t)8 * Mx * std::max(qkvd, c.hidden), (int64_t)2 * Mx * 2 * c.ffn);
     qg_part = dalloc<float>((size_t)qg_part_cap);
     ssq = dalloc<float>((size_t)16 * (c.hidden / 16));
@@ -517,15 +519,15 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     if (P + M > c.ctx_len) throw ArgError("forward: KV capacity exceeded");
     if (mask_words < 1 || mask_words > 2) throw ArgError("forward: mask words");
     SD_HIP_CHECK(hipSetDevice(c.device));
-    // stage ids | pos | mask in pinned memory, one H2D copy each
+    // stage ids | pos | mask in pinned memory with the device block's layout,
+    // then one H2D copy
     stage_wait();
     std::memcpy(h_stage, ids, M * sizeof(int));
     std::memcpy(h_stage + c.max_batch, pos, M * sizeof(int));
-    uint64_t *hm = (uint64_t *)(h_stage + 3 * c.max_batch + (c.max_batch & 1));
-    std::memcpy(hm, mask, (size_t)M * mask_words * sizeof(uint64_t));
-    SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, M * sizeof(int), hipMemcpyHostToDevice, st));
-    SD_HIP_CHECK(hipMemcpyAsync(d_pos, h_stage + c.max_batch, M * sizeof(int), hipMemcpyHostToDevice, st));
-    SD_HIP_CHECK(hipMemcpyAsync(d_mask, hm, (size_t)M * mask_words * sizeof(uint64_t), hipMemcpyHostToDevice, st));
+    const size_t mask_at = (size_t)3 * c.max_batch + (c.max_batch & 1);
+    std::memcpy(h_stage + mask_at, mask, (size_t)M * mask_words * sizeof(uint64_t));
+    SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, mask_at * sizeof(int) + (size_t)M * mask_words * sizeof(uint64_t),
+                                hipMemcpyHostToDevice, st));
     stage_done();
 
     const int H = c.hidden, QD = c.q_dim(), KVD = c.kv_dim(), QKVD = QD + 2 * KVD;
