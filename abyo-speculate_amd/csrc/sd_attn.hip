@@ -628,6 +628,38 @@ __global__ __launch_bounds__(128) void k_attn_combine(AttnParams p) {
     const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
     const int64_t pi0 = (int64_t)head * p.M + m;
     const uint16_t *po = (const uint16_t *)p.part_o;
+    constexpr int kFew = 12;
+    if (ns <= kFew) {
+        // every split's (m, l) and output element requested at once: one
+        // memory round trip instead of two; same arithmetic and order as below
+        float ms[kFew], ls[kFew];
+        uint16_t os[kFew];
+#pragma unroll
+        for (int s = 0; s < kFew; s++) {
+            if (s < ns) {
+                const int64_t pi = pi0 + s * stride;
+                ms[s] = p.part_ml[2 * pi];
+                ls[s] = p.part_ml[2 * pi + 1];
+                os[s] = po[pi * HD + d];
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kFew; s++)
+            if (s < ns) mx = fmaxf(mx, ms[s]);
+        float W = 0.f, acc = 0.f;
+#pragma unroll
+        for (int s = 0; s < kFew; s++) {
+            if (s < ns) {
+                const float w = ms[s] == -INFINITY ? 0.f : ls[s] * exp2f(ms[s] - mx);
+                W += w;
+                acc += h2f(os[s]) * w;
+            }
+        }
+        const int64_t k = (int64_t)head * HD + d;
+        p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / W);
+        return;
+    }
     float mx = -INFINITY;
     for (int s = 0; s < ns; s++) mx = fmaxf(mx, p.part_ml[2 * (pi0 + s * stride)]);
     float W = 0.f, acc = 0.f;
