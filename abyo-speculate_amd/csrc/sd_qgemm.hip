@@ -24,11 +24,14 @@
 // (rows, K), never on M, so row i of an M-row call (M <= 16) equals the M=1
 // call bit for bit.
 //
-// Dequantisation to fp16 (k_qgx, and Q6_K / Q8_0 in k_qmm): a 4-bit code is
-// OR'ed into the mantissa of 1024.0h (0x6400 | q == 1024 + q) or, for a code
-// already at bits 4-7, of 64.0h (0x5400 | q << 4 == 64 + q), and v_fma_mix
-// evaluates round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m):
-// the f32 value s*q - m rounded once to fp16.
+// Dequantisation to fp16 (k_qgx, and Q6_K / Q8_0 in k_qmm): a code is OR'ed
+// into the mantissa of 1024.0h (0x6400 | q == 1024 + q) or, for a code already
+// at bits 4-7, of 64.0h (0x5400 | q << 4 == 64 + q).  Q6_K: v_fma_mix
+// evaluates round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m),
+// the f32 value s*q - m rounded once.  Q8_0: q exactly, times the fp16 block
+// scale in one v_pk_mul_f16.  Q4_K / Q5_K (k_qgx): q exactly, then one
+// v_pk_fma_f16 with the sub-block's fp16 scale and min, round_f16(q * s16 -
+// m16) where s16 = fp16(d * sc) and m16 = fp16(dmin * m).
 #include <hip/hip_ext.h>
 
 #include "sd_buffer.hpp"
@@ -107,18 +110,6 @@ __device__ __forceinline__ void kquant_ints(const uintx4 &hdr, int g, int (&sc)[
         mn[i] = (int)(hi ? mn_hi : mn_lo);
     }
 }
-__device__ __forceinline__ void kquant_scales(const uintx4 &hdr, int g, float &s0, float &c0, float &s1,
-                                              float &c1) {
-    const float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
-    int sc[2], mn[2];
-    kquant_ints(hdr, g, sc, mn);
-    const float d0 = d * (float)sc[0], m0 = dmin * (float)mn[0];
-    const float d1 = d * (float)sc[1], m1 = dmin * (float)mn[1];
-    s0 = d0;
-    c0 = -(1024.f * d0 + m0);  // low nibbles, codes 1024 + q
-    s1 = d1;
-    c1 = -(64.f * d1 + m1);    // high nibbles, codes 64 + q
-}
 
 // Loads address one tile block: the wave-uniform part (tile, superblock) goes
 // in the scalar offset, the lane's fixed position inside the block in the
@@ -163,6 +154,29 @@ __device__ __forceinline__ KInt kquant_int(const uintx4 &hdr, int g) {
     return k;
 }
 
+// fp16 pairs of one lane's two sub-blocks (see QFmt<Q4_K>::S)
+struct KS16 {
+    uint32_t s0, m0, s1, m1;
+};
+__device__ __forceinline__ KS16 kquant_s16(const uintx4 &hdr, int g) {
+    const float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+    int sc[2], mn[2];
+    kquant_ints(hdr, g, sc, mn);
+    KS16 k;
+    k.s0 = h2pair(d * (float)sc[0]);  // exact f32 products, one rounding each
+    k.m0 = h2pair(-(dmin * (float)mn[0]));
+    k.s1 = h2pair(d * (float)sc[1]);
+    k.m1 = h2pair(-(dmin * (float)mn[1]));
+    return k;
+}
+constexpr uint32_t kOff1024 = 0xE400E400u;  // (-1024, -1024) in fp16
+constexpr uint32_t kOff64 = 0xD400D400u;    // (-64, -64)
+// codes (off + q) -> round_f16(q * s + nm), q exact
+__device__ __forceinline__ uint32_t qsm(uint32_t p, uint32_t off, uint32_t s, uint32_t nm) {
+    const half2v q = __builtin_bit_cast(half2v, p) + __builtin_bit_cast(half2v, off);
+    return pkfma(__builtin_bit_cast(uint32_t, q), s, nm);
+}
+
 template <> struct QFmt<Q4_K> {
     typedef LaneQ4K D;
     static constexpr bool kInt = true;
@@ -173,9 +187,12 @@ template <> struct QFmt<Q4_K> {
         return as_half8(pkfma(p[0], s.s0, s.c0), pkfma(p[1], s.s0, s.c0), pkfma(p[2], s.s1, s.c1),
                         pkfma(p[3], s.s1, s.c1));
     }
-    struct S {
-        float s0, c0, s1, c1;
-    };
+    // Above 16 rows (weights as the MFMA's fp16 operand): the sub-block
+    // scales as fp16 pairs, s = fp16(d * sc) and -m = -fp16(dmin * mn); a code
+    // (1024 + q or 64 + q) minus its offset is q exactly, and one
+    // v_pk_fma_f16 gives round_f16(q * s - m) (a single rounding of the exact
+    // q * s - m).  Two packed instructions per pair of weights.
+    typedef KS16 S;
     static __device__ __forceinline__ void load(D &r, const WRow &w, int nsb, int sb, int g) {
         const int lane = threadIdx.x & 63;
         const uint32_t so = tb_off(w, sb, D::TBB);
@@ -183,15 +200,12 @@ template <> struct QFmt<Q4_K> {
         r.q0 = bld16(w.rs, D::off_q0(lane), so);
         r.q1 = bld16(w.rs, D::off_q1(lane), so);
     }
-    static __device__ __forceinline__ S scales(const D &r, int g) {
-        S s;
-        kquant_scales(r.hdr, g, s.s0, s.c0, s.s1, s.c1);
-        return s;
-    }
+    static __device__ __forceinline__ S scales(const D &r, int g) { return kquant_s16(r.hdr, g); }
     static __device__ __forceinline__ half8 frag(const D &r, const S &s, int g, int c) {
         uint32_t p[4];
         r.codes(g, c, p);
-        return as_half8(fm2(p[0], s.s0, s.c0), fm2(p[1], s.s0, s.c0), fm2(p[2], s.s1, s.c1), fm2(p[3], s.s1, s.c1));
+        return as_half8(qsm(p[0], kOff1024, s.s0, s.m0), qsm(p[1], kOff1024, s.s0, s.m0),
+                        qsm(p[2], kOff64, s.s1, s.m1), qsm(p[3], kOff64, s.s1, s.m1));
     }
 };
 
@@ -214,15 +228,12 @@ template <> struct QFmt<Q5_K> {
         r.q0 = bld16(w.rs, D::off_q0(lane), so);
         r.q1 = bld16(w.rs, D::off_q1(lane), so);
     }
-    static __device__ __forceinline__ S scales(const D &r, int g) {
-        S s;
-        kquant_scales(r.hdr, g, s.s0, s.c0, s.s1, s.c1);
-        return s;
-    }
+    static __device__ __forceinline__ S scales(const D &r, int g) { return kquant_s16(r.hdr, g); }
     static __device__ __forceinline__ half8 frag(const D &r, const S &s, int g, int c) {
         uint32_t p[4];
         r.codes(g, c, p);
-        return as_half8(fm2(p[0], s.s0, s.c0), fm2(p[1], s.s0, s.c0), fm2(p[2], s.s1, s.c1), fm2(p[3], s.s1, s.c1));
+        return as_half8(qsm(p[0], kOff1024, s.s0, s.m0), qsm(p[1], kOff1024, s.s0, s.m0),
+                        qsm(p[2], kOff64, s.s1, s.m1), qsm(p[3], kOff64, s.s1, s.m1));
     }
 };
 

@@ -62,8 +62,72 @@ def test_set_tensor_roundtrip(hip, mix):
 def int_path(fmt, M):
     """Up to 16 rows, Q4_K and Q5_K weights enter the MFMA as the exact
     integers sc * q, with d, dmin and the mins applied in f32; the other
-    formats and larger M use weights rounded to fp16."""
+    formats and larger M use fp16 weights."""
     return M <= 16 and fmt in (O.Q4_K, O.Q5_K)
+
+
+def kquant_fields(fmt, raw, rows, K):
+    """Per weight (q, sc, m, d, dmin) of a Q4_K / Q5_K matrix, decoded from the
+    GGUF blocks (ggml's dequantize_row_q4_K / _q5_K element order), each
+    [rows, K] float64; checked against the oracle's dequantisation below."""
+    bb = O.BLOCK_BYTES[fmt]
+    blk = raw.reshape(-1, bb)
+    nb = blk.shape[0]
+    d = blk[:, 0:2].copy().view(np.float16)[:, 0].astype(np.float64)
+    dmin = blk[:, 2:4].copy().view(np.float16)[:, 0].astype(np.float64)
+    sc = np.zeros((nb, 8))
+    mn = np.zeros((nb, 8))
+    for b in range(nb):
+        sb = bytes(blk[b, 4:16])
+        for j in range(8):
+            sc[b, j], mn[b, j] = O.get_scale_min_k4(j, sb)
+    q = np.zeros((nb, 256))
+    qs = blk[:, 16:144] if fmt == O.Q4_K else blk[:, 48:176]
+    for c in range(4):
+        lo = (qs[:, 32 * c:32 * c + 32] & 15).astype(np.float64)
+        hi = (qs[:, 32 * c:32 * c + 32] >> 4).astype(np.float64)
+        if fmt == O.Q5_K:
+            qh = blk[:, 16:48]
+            lo += 16 * ((qh >> (2 * c)) & 1)
+            hi += 16 * ((qh >> (2 * c + 1)) & 1)
+        q[:, 64 * c:64 * c + 32] = lo
+        q[:, 64 * c + 32:64 * c + 64] = hi
+    sub = np.arange(256) // 32
+    f = lambda a: a.reshape(rows, K)  # noqa: E731
+    return (f(q), f(sc[:, sub]), f(mn[:, sub]), f(np.repeat(d, 256)), f(np.repeat(dmin, 256)))
+
+
+def wide_kquant_weights(fmt, raw, rows, K):
+    """The fp16 weights the M > 16 kernel multiplies with for Q4_K / Q5_K:
+    round_f16(q * s16 - m16), s16 = fp16(d * sc), m16 = fp16(dmin * m)
+    (exact products and difference in f64, one rounding each)."""
+    q, sc, mn, d, dmin = kquant_fields(fmt, raw, rows, K)
+    s16 = (d * sc).astype(np.float16).astype(np.float64)
+    m16 = (dmin * mn).astype(np.float16).astype(np.float64)
+    return (q * s16 - m16).astype(np.float16).astype(np.float32)
+
+
+def operand_weights(fmt, raw, rows, K, M):
+    """The weights K1 multiplies an M-row input with."""
+    W = O.dequant_matrix(fmt, raw, rows, K)
+    if int_path(fmt, M):
+        return W
+    if fmt in (O.Q4_K, O.Q5_K):
+        return wide_kquant_weights(fmt, raw, rows, K)
+    return O.round_f16(W)
+
+
+@pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q5_k", O.K_ATTN_O)])
+def test_kquant_field_decoder_matches_oracle(mix, kind):
+    """The test's block decoder reproduces the oracle's dequantisation
+    (d * sc in f32 times q, minus dmin * m in f32, as ggml), bit for bit."""
+    ocfg = oracle_cfg(mix=mix, n_layers=1, vocab=2048)
+    fmt, raw = O.synth_tensor(ocfg, 0, kind)
+    rows, K = ocfg.shape(kind)
+    q, sc, mn, d, dmin = kquant_fields(fmt, raw, rows, K)
+    f32 = np.float32
+    W = (d.astype(f32) * sc.astype(f32)) * q.astype(f32) - dmin.astype(f32) * mn.astype(f32)
+    assert np.array_equal(W.view(np.uint32), O.dequant_matrix(fmt, raw, rows, K).view(np.uint32))
 
 
 CASES = [("q4_k", 0, O.K_ATTN_Q), ("q4_k", 0, O.K_FFN_DOWN), ("q6_k", 0, O.K_FFN_GATE),
@@ -82,7 +146,7 @@ def test_qmatmul_vs_oracle(hip, mix, layer, kind, M):
     W = O.dequant_matrix(fmt, raw, rows, K)
     x = np.random.default_rng(M * 7 + kind).standard_normal((M, K)).astype(np.float32)
     y = dec.qmatmul(layer, kind, x)
-    Wk = W if int_path(fmt, M) else O.round_f16(W)
+    Wk = operand_weights(fmt, raw, rows, K, M)
     ref16 = O.round_f16(x).astype(np.float64) @ Wk.astype(np.float64).T
     ref32 = x.astype(np.float64) @ W.astype(np.float64).T
     assert rel_err(y, ref16) < 1e-4, rel_err(y, ref16)
@@ -107,13 +171,34 @@ def test_qmatmul_int_path_one_hot(hip, mix, kind):
         np.testing.assert_allclose(y[i], W[:, k], rtol=2e-7, atol=1e-9, err_msg=f"k={k}")
 
 
+@pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q5_k", O.K_ATTN_O), ("q6_k", O.K_FFN_DOWN),
+                                      ("q8_0", O.K_FFN_UP)])
+def test_qmatmul_wide_one_hot(hip, mix, kind):
+    """Above 16 rows, one-hot activations read the kernel's fp16 weights back
+    out bit for bit: the emulated round_f16(q * s16 - m16) for Q4_K / Q5_K,
+    round_f16(W) for Q6_K / Q8_0."""
+    ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
+    fmt, raw = O.synth_tensor(ocfg, 0, kind)
+    rows, K = ocfg.shape(kind)
+    Wk = operand_weights(fmt, raw, rows, K, 64)
+    ks = [0, 1, 2, 3, 5, 15, 16, 31, 32, 33, 63, 64, 100, 127, 128, 160, 200, 224, 255, 256, 300, K - 2, K - 1]
+    ks += [K // 4 + 3 * i for i in range(41)]  # 64 rows: the kernel with 4 token tiles
+    x = np.zeros((len(ks), K), np.float32)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    assert len(ks) > 16
+    y = dec.qmatmul(0, kind, x)
+    for i, k in enumerate(ks):
+        assert np.array_equal(y[i].view(np.uint32), Wk[:, k].view(np.uint32)), f"k={k}"
+
+
 @pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q6_k", O.K_FFN_DOWN), ("q8_0", O.K_FFN_UP),
                                       ("q5_k", O.K_ATTN_V)])
 def test_qmatmul_m_invariant(hip, mix, kind):
     """Up to 16 rows (the linear-verify shapes) row i of an M-row product equals
     the single-row product bit for bit: the K split is a function of the
     matrix only.  Past 16 rows the activation-staged kernel sums K in other
-    slices (and rounds Q4_K / Q5_K weights to fp16), so rows agree to
+    slices (and uses Q4_K / Q5_K weights rounded to fp16), so rows agree to
     rounding (the reference's own GEMV and GEMM paths differ the same way,
     which is why its strict root mode exists)."""
     ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
