@@ -67,6 +67,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-tree", action="store_true", help="skip the 60-node tree leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-ar", action="store_true", help="skip the M=1 decode-step leg")
     ap.add_argument("--prefix", type=int, default=512, help="KV positions before the M=5 verify")
     ap.add_argument("--tree-prefix", type=int, default=4096, help="KV positions before the tree verify")
     return ap.parse_args()
@@ -242,25 +243,26 @@ def main():
     }
 
     # ---------------- M=1 decode step (what autoregressive decoding runs per token) ----------------
-    dec.rollback_to(n0)
-
-    def step_ar():
-        dec.observe(drafts[:1])
+    if not args.no_ar:
         dec.rollback_to(n0)
 
-    for _ in range(args.warmup):
-        step_ar()
-    dec.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step_ar()
-    dec.synchronize()
-    t_ar = (time.perf_counter() - t0) / args.steps
-    log(f"M=1 decode step: {t_ar * 1e6:.1f} us")
-    result["ar_m1"] = {"us": round(t_ar * 1e6, 1), "tokens_per_s": round(1.0 / t_ar, 1),
-                       "kv_positions": args.prefix,
-                       "what": "observe of one token: M=1 forward with the lm_head row (the step an autoregressive "
-                               "decoder runs per token, logits left on the device)"}
+        def step_ar():
+            dec.observe(drafts[:1])
+            dec.rollback_to(n0)
+
+        for _ in range(args.warmup):
+            step_ar()
+        dec.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step_ar()
+        dec.synchronize()
+        t_ar = (time.perf_counter() - t0) / args.steps
+        log(f"M=1 decode step: {t_ar * 1e6:.1f} us")
+        result["ar_m1"] = {"us": round(t_ar * 1e6, 1), "tokens_per_s": round(1.0 / t_ar, 1),
+                           "kv_positions": args.prefix,
+                           "what": "observe of one token: M=1 forward with the lm_head row (the step an "
+                                   "autoregressive decoder runs per token, logits left on the device)"}
 
     # ---------------- 60-node tree verify ----------------
     if not args.no_tree:
