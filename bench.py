@@ -14,7 +14,12 @@ on the GPU, 512 fp16 KV positions filled with N(0, 1)-like values.
 The same run also times the 60-node tree verify of the same weights: a
 (4,3,2,2,1,1) Cartesian draft tree pruned to 60 nodes (depth 6) over 4096 KV
 positions, greedy longest-path acceptance and compaction of the accepted
-path's KV rows (sd_verify_greedy_tree + sd_commit_tree_path), then rollback.
+path's KV rows (sd_verify_greedy_tree + sd_commit_tree_path), then rollback;
+the M=1 decode step (observe of one token); an EAGLE-3-style verify (64-node
+depth-7 tree over 8192 positions, draft rows in a 32000-token vocabulary
+mapped through a seeded injective d2t, rejection sampling at T=1, compaction);
+and a Qwen2.5-7B-shaped Q5_K / Q8_0 target with QKV bias verifying k=8 drafts
+(M=9) over 2048 positions with rejection sampling at T=1.
 
 Timing: W untimed warmup steps, then K steps bracketed by device
 synchronisation.  A second pass of K steps with HIP-event timing on the
@@ -54,6 +59,10 @@ KV_SEED = 0x4B560002
 
 LLAMA8B = dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
                rope_theta=500000.0, rms_eps=1e-5)
+QWEN7B = dict(n_layers=28, hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, ffn=18944, vocab=152064,
+              rope_theta=1000000.0, rms_eps=1e-6)
+EAGLE3_PREFIX, EAGLE3_DRAFT_VOCAB = 8192, 32000
+QWEN_PREFIX, QWEN_K = 2048, 8
 
 
 def log(msg: str):
@@ -68,6 +77,8 @@ def parse():
     ap.add_argument("--no-tree", action="store_true", help="skip the 60-node tree leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ar", action="store_true", help="skip the M=1 decode-step leg")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the rejection-sampling legs (EAGLE-3 64-node tree at 8192, Qwen2.5-7B M=9 at 2048)")
     ap.add_argument("--prefix", type=int, default=512, help="KV positions before the M=5 verify")
     ap.add_argument("--tree-prefix", type=int, default=4096, help="KV positions before the tree verify")
     return ap.parse_args()
@@ -83,6 +94,44 @@ def make_tree(S, root: int, rng: np.random.Generator):
 
 def gemm_rows(prof, classes):
     return [e for e in prof if e[0] in classes]
+
+
+def draft_rows(rng, n, V, scale=2.0):
+    """Draft distributions: softmax of N(0, scale^2) logits (seeded)."""
+    z = rng.standard_normal((n, V)) * scale
+    z = np.exp(z - z.max(axis=1, keepdims=True))
+    return (z / z.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def timed_leg(dec, step, args):
+    """(seconds per step, per-launch profile of a second pass, mean of step()'s return)."""
+    for _ in range(args.warmup):
+        step()
+    dec.synchronize()
+    t0 = time.perf_counter()
+    acc = 0.0
+    for _ in range(args.steps):
+        acc += step()
+    dec.synchronize()
+    t = (time.perf_counter() - t0) / args.steps
+    dec.profile_enable(True)
+    for _ in range(args.steps):
+        step()
+    dec.synchronize()
+    prof = dec.profile_read()
+    dec.profile_enable(False)
+    return t, prof, acc / args.steps
+
+
+def leg_summary(t, prof, tokens_per_step, extra):
+    g = gemm_rows(prof, ("qkv", "wo", "gate_up", "down", "lm_head"))
+    b = sum(e[1] for e in g)
+    tt = sum(e[2] for e in g) * 1e-3
+    out = {"us": round(t * 1e6, 1), "tokens_per_s": round(tokens_per_step / t, 1),
+           "k1_gbps": round(b / tt / 1e9, 1), "k1_frac": round(b / tt / 1e9 / PEAK_HBM_GBPS, 4),
+           "k1_avg_launch_us": round(tt / len(g) * 1e6, 2), "kernels": summarize(prof)}
+    out.update(extra)
+    return out
 
 
 def summarize(prof):
@@ -173,7 +222,7 @@ def main():
         __graft_entry__.build()
     S.load_library()
 
-    ctx = max(args.prefix + 8, args.tree_prefix + 64) + 64
+    ctx = max(args.prefix + 8, args.tree_prefix + 64, 0 if args.no_extra else EAGLE3_PREFIX + 72) + 64
     cfg = S.Config(arch=S.ARCH_LLAMA, ctx_len=ctx, max_batch=64, **LLAMA8B)
     log(f"creating decoder (ctx {ctx}) and synthesising Q4_K_M weights")
     dec = S.HipQuantDecoder(cfg)
@@ -307,7 +356,67 @@ def main():
                             "k1_avg_launch_us": round(tt / len(tg) * 1e6, 2),
                             "k1_traffic": measured_traffic("tree60")[0],
                             "kernels": summarize(tprof)}
+
+    if not args.no_extra:
+        # ---------------- EAGLE-3 verify: 64-node tree at 8192, d2t, rejection ----------------
+        erng = np.random.default_rng(SEED + 5)
+        Vd = EAGLE3_DRAFT_VOCAB
+        d2t = erng.choice(cfg.vocab, size=Vd, replace=False).astype(np.int64)
+        dec.set_d2t(d2t)
+        hist = [int(v) for v in erng.integers(0, cfg.vocab, EAGLE3_PREFIX + 1)]
+        dec.prime_synthetic(hist, KV_SEED + 2)
+        n1 = len(hist)
+        cand_d = [[int(v) for v in erng.choice(Vd, b, replace=False)] for b in (4, 3, 2, 2, 1, 1, 1)]
+        lps = [list(np.sort(np.log(erng.dirichlet(np.ones(len(c)))))[::-1].astype(np.float32)) for c in cand_d]
+        etree = S.tree_prune(S.tree_cartesian(hist[-1], [[int(d2t[v]) for v in c] for c in cand_d]), lps, 64)
+        ne = len(etree[0])
+        q_d = draft_rows(erng, ne, Vd)
+        u = [float(x) for x in erng.random(ne, dtype=np.float32)]
+
+        def step_e3():
+            path, tok, used = dec.verify_rejection_tree(etree, q_d, list(range(ne)), u, 1.0)
+            dec.commit_tree_path(etree, path)
+            dec.rollback_to(n1)
+            return len(path)
+
+        log(f"EAGLE-3 verify: {ne}-node tree at KV {EAGLE3_PREFIX}, d2t {Vd} -> {cfg.vocab}, rejection at T=1")
+        t_e3, eprof, plen = timed_leg(dec, step_e3, args)
+        log(f"EAGLE-3 verify: {t_e3 * 1e6:.1f} us/step")
+        result["eagle3_tree64"] = leg_summary(
+            t_e3, eprof, plen,
+            {"nodes": ne, "kv_positions": EAGLE3_PREFIX, "draft_vocab": Vd,
+             "what": "tree forward (K1 M=64, tree attention over 8192 positions), rejection walk over the d2t-mapped "
+                     "draft rows (64 x 32000 f32 uploaded per step), compaction of the accepted path"})
     dec.close()
+
+    if not args.no_extra:
+        # ---------------- Qwen2.5-7B-shaped Q5_K/Q8_0, M=9 at 2048, rejection ----------------
+        qcfg = S.Config(arch=S.ARCH_QWEN2, ctx_len=QWEN_PREFIX + 128, max_batch=64, **QWEN7B)
+        log("creating the Qwen2.5-7B-shaped decoder (Q5_K attention, Q8_0 FFN, QKV bias)")
+        qd = S.HipQuantDecoder(qcfg)
+        qd.synthesize(S.MIX_Q5K_Q80, SEED, 0.02)
+        qrng = np.random.default_rng(SEED + 3)
+        hist = [int(v) for v in qrng.integers(0, qcfg.vocab, QWEN_PREFIX + 1)]
+        qd.prime_synthetic(hist, KV_SEED + 3)
+        n0q = len(hist)
+        q = draft_rows(qrng, QWEN_K, qcfg.vocab)
+        qdrafts = [int(qrng.choice(qcfg.vocab, p=r.astype(np.float64) / r.astype(np.float64).sum())) for r in q]
+        uq = [float(x) for x in qrng.random(QWEN_K + 1, dtype=np.float32)]
+
+        def step_q():
+            commits, n_acc, used = qd.verify_rejection_linear(qdrafts, q, uq, 1.0)
+            qd.rollback_to(n0q)
+            return len(commits)
+
+        log(f"Qwen2.5-7B verify: M={QWEN_K + 1} at KV {QWEN_PREFIX}, rejection at T=1")
+        t_q, qprof, ncom = timed_leg(qd, step_q, args)
+        log(f"Qwen2.5-7B verify: {t_q * 1e6:.1f} us/step")
+        result["qwen7b_m9"] = leg_summary(
+            t_q, qprof, ncom,
+            {"M": QWEN_K + 1, "kv_positions": QWEN_PREFIX,
+             "what": "linear verify of 8 drafts (K1 M=9 on Q5_K / Q8_0 with QKV bias), rejection walk over "
+                     "8 x 152064 f32 draft rows uploaded per step"})
+        qd.close()
 
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
