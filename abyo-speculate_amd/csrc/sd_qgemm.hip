@@ -26,10 +26,9 @@
 //
 // Dequantisation to fp16 (k_qgx, and Q6_K / Q8_0 in k_qmm): a code is OR'ed
 // into the mantissa of 1024.0h (0x6400 | q == 1024 + q) or, for a code already
-// at bits 4-7, of 64.0h (0x5400 | q << 4 == 64 + q).  Q6_K: v_fma_mix
-// evaluates round_f16((64|1024 + q) * s + c) in f32, c = -((64|1024) * s + m),
-// the f32 value s*q - m rounded once.  Q8_0: q exactly, times the fp16 block
-// scale in one v_pk_mul_f16.  Q4_K / Q5_K (k_qgx): q exactly, then one
+// at bits 4-7, of 64.0h (0x5400 | q << 4 == 64 + q).  Q6_K: q - 32 exactly,
+// times the fp16 sub-block scale fp16(d * sc) in one v_pk_mul_f16.  Q8_0: q
+// exactly, times the fp16 block scale in one v_pk_mul_f16.  Q4_K / Q5_K (k_qgx): q exactly, then one
 // v_pk_fma_f16 with the sub-block's fp16 scale and min, round_f16(q * s16 -
 // m16) where s16 = fp16(d * sc) and m16 = fp16(dmin * m).
 #include <hip/hip_ext.h>
@@ -44,26 +43,10 @@ namespace sd {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-typedef float float2v __attribute__((ext_vector_type(2)));
-
 // Compiler-visible forms only on the paths into MFMA operands: an inline-asm
 // result read by an MFMA (or an MFMA result read by inline asm) escapes the
 // compiler's hazard tracking, and the MFMA then sees a stale register.
 
-// two f32 -> one word of two fp16 (round to nearest even, v_cvt_pk_f16_f32)
-__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
-    const float2v v = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2v));
-}
-// two fp16 codes -> two fp16 results of round_f16(code * s + c) (f32 inside):
-// two v_fma_mix_f32 and one v_cvt_pk_f16_f32.  Written as a vector
-// conversion so that the compiler does not fold it into v_fma_mixlo/hi_f16,
-// which on gfx950 issue at half the rate of v_fma_mix_f32 (the pair costs
-// more than the three instructions).
-__device__ __forceinline__ uint32_t fm2(uint32_t p, float s, float c) {
-    const half2v h = __builtin_bit_cast(half2v, p);
-    return cvt_pk(__builtin_fmaf((float)h.x, s, c), __builtin_fmaf((float)h.y, s, c));
-}
 // two fp16 codes -> code * s + c in one v_pk_fma_f16 (s, c fp16 pairs): exact
 // when the result is a small integer (the K-quant integer path below)
 __device__ __forceinline__ uint32_t pkfma(uint32_t p, uint32_t s, uint32_t c) {
@@ -240,8 +223,11 @@ template <> struct QFmt<Q5_K> {
 template <> struct QFmt<Q6_K> {
     typedef LaneQ6K D;
     static constexpr bool kInt = false;  // sc * (q - 32) needs 13 bits, past fp16's exact integers
+    // fp16 pairs of d * sc, [2 * s' + (c >= 4)]: a code (1024 + q6 or 64 + q6)
+    // minus 1056 (or 96) is q6 - 32 exactly, and one v_pk_mul_f16 gives
+    // round_f16((q6 - 32) * fp16(d * sc))
     struct S {
-        float s[4], c[4];  // [2 * s' + (c >= 4)]; c = offset for codes 1024 + q6 (s'=0) / 64 + q6 (s'=1)
+        uint32_t s[4];
     };
     static __device__ __forceinline__ void load(D &r, const WRow &w, int nsb, int sb, int g) {
         const int lane = threadIdx.x & 63;
@@ -257,19 +243,21 @@ template <> struct QFmt<Q6_K> {
         S s;
         // sc bytes of the lane: [s'=0, l<16], [s'=0, l>=16], [s'=1, l<16], [s'=1, l>=16]
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float v = d * (float)(int8_t)((r.sc >> (8 * i)) & 0xffu);
-            s.s[i] = v;
-            s.c[i] = (i < 2 ? -1056.f : -96.f) * v;  // value (q6 - 32) * v
-        }
+        for (int i = 0; i < 4; i++) s.s[i] = h2pair(d * (float)(int8_t)((r.sc >> (8 * i)) & 0xffu));  // exact, one rounding
         return s;
+    }
+    static __device__ __forceinline__ uint32_t qmul(uint32_t p, uint32_t off, uint32_t sc) {
+        const half2v q = __builtin_bit_cast(half2v, p) + __builtin_bit_cast(half2v, off);
+        return __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(half2v, sc));
     }
     static __device__ __forceinline__ half8 frag(const D &r, const S &s, int g, int c) {
         uint32_t p[4];
         r.codes(g, c, p);
         const int hl = c >= 4 ? 1 : 0;
-        const float sa = s.s[hl], ca = s.c[hl], sb = s.s[2 + hl], cb = s.c[2 + hl];
-        return as_half8(fm2(p[0], sa, ca), fm2(p[1], sa, ca), fm2(p[2], sb, cb), fm2(p[3], sb, cb));
+        const uint32_t sa = s.s[hl], sb = s.s[2 + hl];
+        constexpr uint32_t off1056 = 0xE420E420u, off96 = 0xD600D600u;  // (-1056, -1056), (-96, -96) in fp16
+        return as_half8(qmul(p[0], off1056, sa), qmul(p[1], off1056, sa), qmul(p[2], off96, sb),
+                        qmul(p[3], off96, sb));
     }
 };
 

@@ -107,14 +107,56 @@ def wide_kquant_weights(fmt, raw, rows, K):
     return (q * s16 - m16).astype(np.float16).astype(np.float32)
 
 
+def q6k_fields(raw, rows, K):
+    """Per weight (q6 - 32, sc, d) of a Q6_K matrix from its GGUF blocks (ggml's
+    dequantize_row_q6_K element order), each [rows, K] float64."""
+    blk = raw.reshape(-1, 210)
+    nb = blk.shape[0]
+    ql, qh = blk[:, 0:128].astype(np.int64), blk[:, 128:192].astype(np.int64)
+    scs = blk[:, 192:208].copy().view(np.int8).astype(np.float64)
+    d = blk[:, 208:210].copy().view(np.float16)[:, 0].astype(np.float64)
+    q = np.zeros((nb, 256))
+    sc = np.zeros((nb, 256))
+    for h in range(2):
+        L, H, S = ql[:, 64 * h:64 * h + 64], qh[:, 32 * h:32 * h + 32], scs[:, 8 * h:8 * h + 8]
+        for l in range(32):
+            base = 128 * h + l
+            vals = [(L[:, l] & 15) | (((H[:, l] >> 0) & 3) << 4), (L[:, l + 32] & 15) | (((H[:, l] >> 2) & 3) << 4),
+                    (L[:, l] >> 4) | (((H[:, l] >> 4) & 3) << 4), (L[:, l + 32] >> 4) | (((H[:, l] >> 6) & 3) << 4)]
+            for j, v in enumerate(vals):
+                q[:, base + 32 * j] = v - 32
+                sc[:, base + 32 * j] = S[:, l // 16 + 2 * j]
+    f = lambda a: a.reshape(rows, K)  # noqa: E731
+    return f(q), f(sc), f(np.repeat(d, 256))
+
+
 def operand_weights(fmt, raw, rows, K, M):
-    """The weights K1 multiplies an M-row input with."""
+    """The weights K1 multiplies an M-row input with: exact on the integer
+    path; round_f16(q * s16 - m16) for Q4_K / Q5_K and round_f16((q6 - 32) *
+    fp16(d * sc)) for Q6_K otherwise (exact products, one rounding each);
+    round_f16(W) for Q8_0 (one rounding of d * q)."""
     W = O.dequant_matrix(fmt, raw, rows, K)
     if int_path(fmt, M):
         return W
     if fmt in (O.Q4_K, O.Q5_K):
         return wide_kquant_weights(fmt, raw, rows, K)
+    if fmt == O.Q6_K:
+        q, sc, d = q6k_fields(raw, rows, K)
+        s16 = (d * sc).astype(np.float16).astype(np.float64)
+        return (q * s16).astype(np.float16).astype(np.float32)
     return O.round_f16(W)
+
+
+def test_q6k_field_decoder_matches_oracle():
+    """The test's Q6_K decoder reproduces the oracle's dequantisation (d * sc
+    times q - 32 in f32, as ggml), bit for bit."""
+    ocfg = oracle_cfg(mix="q6_k", n_layers=1, vocab=2048)
+    fmt, raw = O.synth_tensor(ocfg, 0, O.K_FFN_DOWN)
+    rows, K = ocfg.shape(O.K_FFN_DOWN)
+    q, sc, d = q6k_fields(raw, rows, K)
+    f32 = np.float32
+    W = (d.astype(f32) * sc.astype(f32)) * q.astype(f32)
+    assert np.array_equal(W.view(np.uint32), O.dequant_matrix(fmt, raw, rows, K).view(np.uint32))
 
 
 @pytest.mark.parametrize("mix,kind", [("q4_k", O.K_ATTN_Q), ("q5_k", O.K_ATTN_O)])
@@ -138,8 +180,9 @@ CASES = [("q4_k", 0, O.K_ATTN_Q), ("q4_k", 0, O.K_FFN_DOWN), ("q6_k", 0, O.K_FFN
 @pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 60, 64, 100, 128])
 def test_qmatmul_vs_oracle(hip, mix, layer, kind, M):
     """K1 against (a) its operands in f64 (tight): fp16 activations times the
-    exact weights on the integer path, times fp16-rounded weights otherwise,
-    and (b) the f32 oracle QMatMul (the 1e-2 relative contract)."""
+    weights it uses (operand_weights: exact on the integer path, the emulated
+    fp16 roundings otherwise), and (b) the f32 oracle QMatMul (the 1e-2
+    relative contract)."""
     ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
     fmt, raw = O.synth_tensor(ocfg, layer, kind)
     rows, K = ocfg.shape(kind)
@@ -175,8 +218,7 @@ def test_qmatmul_int_path_one_hot(hip, mix, kind):
                                       ("q8_0", O.K_FFN_UP)])
 def test_qmatmul_wide_one_hot(hip, mix, kind):
     """Above 16 rows, one-hot activations read the kernel's fp16 weights back
-    out bit for bit: the emulated round_f16(q * s16 - m16) for Q4_K / Q5_K,
-    round_f16(W) for Q6_K / Q8_0."""
+    out bit for bit (operand_weights: the emulated roundings)."""
     ocfg, dec = _model(hip, mix, n_layers=1, vocab=2048)
     fmt, raw = O.synth_tensor(ocfg, 0, kind)
     rows, K = ocfg.shape(kind)
