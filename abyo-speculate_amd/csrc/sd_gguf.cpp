@@ -385,7 +385,7 @@ void GgufFile::load(Model &m) const {
         if (!vec && t.type != GT_Q4_K && t.type != GT_Q5_K && t.type != GT_Q6_K && t.type != GT_Q8_0)
             throw UnsupportedError(it.name + ": GGML type " + std::to_string(t.type) +
                                    " (matrices load from Q4_K, Q5_K, Q6_K, Q8_0)");
-        if (t.offset > size_ - data_start || t.bytes > size_ - data_start - t.offset)
+        if (data_start > size_ || t.offset > size_ - data_start || t.bytes > size_ - data_start - t.offset)
             throw BackendError(it.name + ": tensor data past the end of the file");
     }
     std::vector<float> conv;

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from _gguf import gguf_bytes, model_metadata, model_tensors
+from _gguf import U32, gguf_bytes, model_metadata, model_tensors
 from _models import all_tensor_keys, hip_cfg, oracle_cfg, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -146,4 +146,6 @@ def test_gguf_load_errors_leave_the_decoder_unchanged(hip, tmp_path):
     # a file cut short inside the last tensor's data
     full = gguf_bytes(md, ents)
     load(full[:-100], hip.BackendError, "past the end of the file")
+    # an alignment that puts the data section past the end of the file
+    load(gguf_bytes(md + [("general.alignment", U32, 1 << 24)], ents), hip.BackendError, "past the end of the file")
     dec.close()
