@@ -1,6 +1,6 @@
 """GGUF reader and the from_gguf hyper-parameter reads -- TEST INFRASTRUCTURE ONLY.
 
-Only ``tests/`` may import this module, as the checker of the library's GGUF
+Only ``tests/`` may import this module, to check the library's GGUF
 loader; the product never imports it.
 
 * ``read_gguf`` restates ``gguf_file::Content::read`` of candle-core 0.8.4

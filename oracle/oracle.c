@@ -2,7 +2,7 @@
  * CPU oracle for the target-verify path: TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker (or as the timed CPU baseline).
+ * load this library, and only to check results against (or as the timed CPU baseline).
  * The product library (abyo-speculate_amd/) never links, loads or calls it.
  *
  * What is restated here, and from where (paths relative to the reference
@@ -23,7 +23,7 @@
  *     first-max argmax fold (crates/speculate/src/methods/eagle.rs:626-637):
  *     sequential f32 folds with libm expf, in the reference's order.
  *   - Synthetic weights: a seeded counter hash -> Irwin-Hall normal ->
- *     this build's own deterministic block quantiser.  The reference has no
+ *     the library's own deterministic block quantiser.  The reference has no
  *     quantiser of its own (candle's QTensor::quantize is external); parity
  *     is defined on the blocks, and this generator must equal the product's
  *     GPU generator bit for bit.

@@ -1,7 +1,7 @@
 """CPU oracle for the target-verify path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-may import this module, and only as the checker (or as the timed CPU
+may import this module, and only to check results against (or as the timed CPU
 baseline).  The product (``abyo-speculate_amd/``) never imports it.
 
 It restates, op by op, the reference's quantized target forward and the

@@ -205,7 +205,7 @@ def test_reference_error_cases(hip, tmp_path):
     data = gguf_bytes(bad, tens)
     with hip.GgufFile(_write(tmp_path, data)) as g, pytest.raises(hip.BackendError, match="not a u32"):
         g.config(0)
-    # partial rotary embedding is not a shape this build runs
+    # partial rotary embedding is not a shape the library runs
     bad = [(k, t, 32) if k == "llama.rope.dimension_count" else (k, t, v) for k, t, v in md]
     data = gguf_bytes(bad, tens)
     assert _lib_view(hip, _write(tmp_path, data))[3][0] == "unsupported" == _oracle_view(data)[3][0]

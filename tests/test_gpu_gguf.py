@@ -131,7 +131,7 @@ def test_gguf_load_errors_leave_the_decoder_unchanged(hip, tmp_path):
     # a file of another shape
     other = _cfg(mix="q4_k", n_layers=1)
     load(gguf_bytes(model_metadata(other), model_tensors(other, _tensors(other))), hip.ArgError, "config")
-    # a matrix in a format this build does not run (Q4_0: 18-byte blocks of 32)
+    # a matrix in a format the library does not run (Q4_0: 18-byte blocks of 32)
     rows, K = cfg.shape(O.K_ATTN_K)
     q40 = rng.integers(0, 256, rows * K // 32 * 18, dtype=np.uint8).tobytes()
     bad = [(n, 2, d, q40) if n == "blk.1.attn_k.weight" else (n, t, d, r) for n, t, d, r in ents]
