@@ -13,24 +13,24 @@ namespace sd {
 
 #pragma clang fp contract(off)
 
-// One workgroup (256 threads) per row.  Each thread keeps its K/256 values in
+// One workgroup (NT threads) per row.  Each thread keeps its K/NT values in
 // registers (vector loads, all issued before the first use), so the row is
-// read from memory once and there is one memory round trip, not K/256 of them.
+// read from memory once and there is one memory round trip, not K/NT of them.
 // With nks > 1 the residual matmul that produced x left K-slice partial sums
 // part[ks][M][K] (nks <= 8): they are added to x in slice order first (and x
 // is stored); every slice's loads are in flight before the first add.
-template <int NV>  // float4 vectors per thread: K = 1024 * NV
-__global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K, float eps, uint16_t *out16,
-                                                 int ld16, float *out32, const float *part, int nks,
-                                                 int64_t pstride) {
+template <int NV, int NT>  // NT threads, NV float4 vectors per thread: K = 4 * NT * NV
+__global__ __launch_bounds__(NT) void k_rmsnorm(float *x, const float *w, int K, float eps, uint16_t *out16,
+                                                int ld16, float *out32, const float *part, int nks,
+                                                int64_t pstride) {
     const int m = blockIdx.x, t = threadIdx.x;
     float4 *row = (float4 *)(x + (int64_t)m * K);
     const float4 *wv = (const float4 *)w;
     float4 v[NV], wr[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++) v[i] = row[t + 256 * i];
+    for (int i = 0; i < NV; i++) v[i] = row[t + NT * i];
 #pragma unroll
-    for (int i = 0; i < NV; i++) wr[i] = wv[t + 256 * i];
+    for (int i = 0; i < NV; i++) wr[i] = wv[t + NT * i];
     if (nks > 1) {
         constexpr int KS = NV <= 4 ? 8 : 4;  // slices per batch of loads (registers: KS * NV float4)
         for (int k0 = 0; k0 < nks; k0 += KS) {
@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K
             for (int k = 0; k < KS; k++) {
                 const float4 *pr = (const float4 *)(part + (k0 + k) * pstride + (int64_t)m * K);
 #pragma unroll
-                for (int i = 0; i < NV; i++) a[k][i] = k0 + k < nks ? pr[t + 256 * i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int i = 0; i < NV; i++) a[k][i] = k0 + k < nks ? pr[t + NT * i] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int k = 0; k < KS; k++)
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K
                 }
         }
 #pragma unroll
-        for (int i = 0; i < NV; i++) row[t + 256 * i] = v[i];
+        for (int i = 0; i < NV; i++) row[t + NT * i] = v[i];
     }
     float ss = 0.f;
 #pragma unroll
@@ -64,14 +64,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *x, const float *w, int K
     ss += __shfl_xor(ss, 8);
     ss += __shfl_xor(ss, 16);
     ss += __shfl_xor(ss, 32);
-    __shared__ float red[4];
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW];
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) tot += red[i];  // fixed order
     const float mrms = sqrtf(tot / (float)K + eps);
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int k = 4 * (t + 256 * i);
+        const int k = 4 * (t + NT * i);
         const float y[4] = {v[i].x / mrms * wr[i].x, v[i].y / mrms * wr[i].y, v[i].z / mrms * wr[i].z,
                             v[i].w / mrms * wr[i].w};
         if (out16) {
@@ -251,15 +254,17 @@ __global__ __launch_bounds__(256) void k_keep_kv_tail(uint16_t *kv, int64_t stre
 void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
                     hipStream_t st, const float *part, int nks) {
     const int64_t ps = (int64_t)M * K;
-#define SD_RMS(KERN) hipLaunchKernelGGL(KERN, dim3(M), dim3(256), 0, st, x, w, K, eps, out16, ld16, out32, part, nks, ps)
+#define SD_RMS(KERN, NT) hipLaunchKernelGGL(KERN, dim3(M), dim3(NT), 0, st, x, w, K, eps, out16, ld16, out32, part, nks, ps)
+    // one float4 per thread (and slice) where K allows: the row's loads spread
+    // over 16 waves
     switch (K) {
-    case 1024: SD_RMS(k_rmsnorm<1>); break;
-    case 2048: SD_RMS(k_rmsnorm<2>); break;
-    case 3072: SD_RMS(k_rmsnorm<3>); break;
-    case 4096: SD_RMS(k_rmsnorm<4>); break;
-    case 5120: SD_RMS(k_rmsnorm<5>); break;
-    case 8192: SD_RMS(k_rmsnorm<8>); break;
-    default: SD_RMS(k_rmsnorm_any); break;
+    case 1024: SD_RMS((k_rmsnorm<1, 256>), 256); break;
+    case 2048: SD_RMS((k_rmsnorm<2, 256>), 256); break;
+    case 3072: SD_RMS((k_rmsnorm<3, 256>), 256); break;
+    case 4096: SD_RMS((k_rmsnorm<1, 1024>), 1024); break;
+    case 5120: SD_RMS((k_rmsnorm<5, 256>), 256); break;
+    case 8192: SD_RMS((k_rmsnorm<2, 1024>), 1024); break;
+    default: SD_RMS(k_rmsnorm_any, 256); break;
     }
 #undef SD_RMS
 }
