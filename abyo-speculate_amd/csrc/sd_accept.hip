@@ -21,7 +21,14 @@
 // by its adjusted distribution against the node's draft row before the next
 // sibling is tested (multi-candidate speculative sampling); if no child is
 // accepted the final token is drawn from the last adjusted distribution, and
-// after a leaf from the leaf's own distribution.
+// after a leaf from the leaf's own distribution.  Two sibling rules: with
+// i.i.d. siblings (each drawn from q with replacement) the draft row q stays
+// fixed; with siblings drawn without replacement from q (distinct tokens), q
+// is zeroed at every rejected token and renormalised before the next sibling
+// is tested (q_r(y) = q(y) / R_r off the rejected set, R_{r+1} = R_r - q(x_r)).
+// Either rule leaves the committed token distributed as the target's when
+// its precondition on the siblings holds; deterministic top-k siblings meet
+// neither.
 //
 // Sums here are parallel (per-thread sequential chunks, then a fixed-order
 // tree), so they can differ from the reference's sequential f32 sums in the
@@ -105,9 +112,21 @@ struct WalkShared {
     float scan[WT];
     int first[WT];
     float Z[MAX_REJ];  // normalisers of the successive adjusted distributions at the current node
+    float R[MAX_REJ];  // without replacement: the mass of q left before rejection r (R[0] = 1)
+    int rej[MAX_REJ];  // without replacement: the rejected tokens at the current node
     int node, krej, used, plen, fin, status, go;
     float u;
 };
+
+// the draft probability of x (q0 = q(x)) that rejection r at the current
+// node tests against: q itself for i.i.d. siblings; without replacement, 0 on
+// the tokens rejected before r and q(x) / R_r elsewhere (0 once no mass is left)
+__device__ __forceinline__ float walk_q(const AcceptParams &a, const WalkShared &W, float q0, int r, int x) {
+    if (!a.wor) return q0;
+    for (int i = 0; i < r; i++)
+        if (W.rej[i] == x) return 0.f;
+    return W.R[r] > 0.f ? q0 / W.R[r] : 0.f;
+}
 
 // probability of x at `node` after `krej` rejections there
 __device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared &W, int node, int krej, int x) {
@@ -122,10 +141,8 @@ __device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared 
     }
     if (krej > 0) {
         const int qr = a.q_row_of[node];
-        for (int r = 0; r < krej; r++) {
-            const float q = accept_q(a, qr, x);
-            p = fmaxf(p - q, 0.f) / W.Z[r];
-        }
+        const float q0 = accept_q(a, qr, x);
+        for (int r = 0; r < krej; r++) p = fmaxf(p - walk_q(a, W, q0, r, x), 0.f) / W.Z[r];
     }
     return p;
 }
@@ -180,6 +197,9 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     }
     __syncthreads();
     while (true) {
+        // every thread has read the previous turn's W.go / W.node / W.krej
+        // before thread 0 rewrites them
+        __syncthreads();
         // ---- thread 0: test the children of the current node in BFS order ----
         if (t == 0) {
             W.go = 0;  // 0: descend done / 1: sample at node / 2: normaliser pass needed / 3: stop
@@ -200,7 +220,8 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                     const float u = a.uniforms[W.used++];
                     const int tok = a.tokens[c];
                     const float p = walk_p(a, W, node, W.krej, tok);
-                    const float q = accept_q(a, a.q_row_of[node], tok);
+                    if (W.krej == 0) W.R[0] = 1.f;
+                    const float q = walk_q(a, W, accept_q(a, a.q_row_of[node], tok), W.krej, tok);
                     // modified_rejection_step (vanilla.rs:59-73)
                     const bool acc = q <= 0.f || u <= fminf(p / q, 1.f);
                     if (acc) {
@@ -208,6 +229,10 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                         break;
                     }
                     W.go = 2;  // rejected: the adjusted distribution's normaliser is needed
+                    if (W.krej < MAX_REJ) {
+                        W.rej[W.krej] = tok;
+                        if (W.krej + 1 < MAX_REJ) W.R[W.krej + 1] = W.R[W.krej] - accept_q(a, a.q_row_of[node], tok);
+                    }
                     break;
                 }
                 if (accepted >= 0) {
@@ -234,7 +259,7 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
             }
             const int qr = a.q_row_of[node];
             const float Z = block_sum(W, a.V, false, [&](int x) {
-                return fmaxf(walk_p(a, W, node, krej, x) - accept_q(a, qr, x), 0.f);
+                return fmaxf(walk_p(a, W, node, krej, x) - walk_q(a, W, accept_q(a, qr, x), krej, x), 0.f);
             });
             if (t == 0) {
                 if (!(Z > 0.f) || !isfinite(Z)) {

@@ -25,6 +25,9 @@
 // kernel (skipped when one split covers all keys).  Up to 16 tokens,
 // keys_per_wave and the split boundaries depend on P only, so a query's
 // result does not depend on how many other queries share the call.
+#include <mutex>
+#include <vector>
+
 #include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels_attn.hpp"
@@ -716,6 +719,24 @@ int attn_max_splits(int n_kv) {
     return (t > kTMaxSplits ? t : kTMaxSplits) + 3;
 }
 
+// LDS beyond the 64 KiB default for the M > 16 kernel: a function attribute
+// set once per device (the caller's current device), under a lock, since
+// handles on different devices may launch from different threads.
+static void allow_attn_t_lds() {
+    static std::mutex mu;
+    static std::vector<bool> done;
+    int dev = 0;
+    SD_ATTN_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev < done.size() && done[dev]) return;
+    SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)attn_t_lds<128>()));
+    SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)attn_t_lds<64>()));
+    if ((size_t)dev >= done.size()) done.resize(dev + 1, false);
+    done[dev] = true;
+}
+
 void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.keys_per_wave < 32 || p.keys_per_wave % 32) throw BackendError("attention: keys_per_wave");
     if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
@@ -728,14 +749,7 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
         // query blocks of 4 waves x kTQW tiles sharing each key block through LDS
         const dim3 grid(p.n_kv, p.nsplit, (nqt + 4 * kTQW - 1) / (4 * kTQW));
         if (p.keys_per_wave * 4 % (32 * kTKS)) throw BackendError("attention: split size");
-        static bool lds_set = false;  // LDS beyond the 64 KiB default, once per process
-        if (!lds_set) {
-            SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              (int)attn_t_lds<128>()));
-            SD_ATTN_CHECK(hipFuncSetAttribute((const void *)k_attn_t<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              (int)attn_t_lds<64>()));
-            lds_set = true;
-        }
+        allow_attn_t_lds();
         if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(256 * kTKS), attn_t_lds<128>(), st, p);
         else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(256 * kTKS), attn_t_lds<64>(), st, p);
     } else {

@@ -377,12 +377,15 @@ sd_status sd_verify_greedy_linear(sd_model *m, const uint32_t *drafts, size_t k,
 
 sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                 int32_t strict, uint32_t *path, size_t *path_len, uint32_t *bonus,
-                                int32_t *bonus_node) {
+                                int32_t *bonus_node, uint32_t *committed, size_t *n_committed, size_t *keep_len,
+                                int32_t *stop) {
     return guard([&] {
         need_weights(m);
-        if (!tokens || !parents || !path || !path_len || !bonus || !bonus_node) throw sd::ArgError("null argument");
+        if (!tokens || !parents || !path || !path_len || !bonus || !bonus_node || !n_committed || !keep_len || !stop)
+            throw sd::ArgError("null argument");
         setdev(m);
-        m->dec->verify_greedy_tree(tokens, parents, n, strict, path, path_len, bonus, bonus_node);
+        m->dec->verify_greedy_tree(tokens, parents, n, strict, path, path_len, bonus, bonus_node, committed,
+                                   n_committed, keep_len, stop);
     });
 }
 
@@ -402,8 +405,8 @@ sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t
 sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                    const float *q_rows, size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
                                    const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
-                                   size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
-                                   size_t *n_used) {
+                                   int32_t siblings, size_t max_commit, uint32_t *path, size_t *path_len,
+                                   int32_t *token, size_t *n_used) {
     return guard([&] {
         need_weights(m);
         if (!tokens || !parents || !q_row_of || !uniforms || !path || !path_len || !token || !n_used ||
@@ -411,7 +414,7 @@ sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const ui
             throw sd::ArgError("null argument");
         setdev(m);
         m->dec->verify_rejection_tree(tokens, parents, n, q_rows, q_rows_n, q_vocab, q_row_of, uniforms, n_uniforms,
-                                      temperature, use_t2d, max_commit, path, path_len, token, n_used);
+                                      temperature, use_t2d, siblings, max_commit, path, path_len, token, n_used);
     });
 }
 

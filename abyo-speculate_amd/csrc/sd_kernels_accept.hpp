@@ -25,6 +25,8 @@ struct AcceptParams {
     const int *q_row_of;   // [n] q row of each node's children (-1 for leaves)
     const float *uniforms; // >= n values
     int max_commit;        // 0: no limit; else stop after this many committed drafts
+    int wor;               // 1: siblings were drawn without replacement from q, so each rejected
+                           // token's q is zeroed and q renormalised before the next sibling
     int *out_path;         // [n] accepted node indices, root first
     int *out_info;         // [4]: path length, final token (-1 none), uniforms used, status
 };

@@ -77,7 +77,8 @@ Model::~Model() {
                     (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids,
                     (void *)d_src, (void *)xp, (void *)ap, (void *)act, (void *)q16,
                     (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
-                    (void *)acc_out, (void *)t2d_inv, (void *)qg_part})
+                    (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
+                    (void *)aux_ids, (void *)ssq})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -142,6 +143,10 @@ void Model::alloc_buffers() {
     acc_u = dalloc<float>(Mx);
     acc_tree = dalloc<int>((size_t)3 * Mx);
     acc_out = dalloc<int>((size_t)Mx + 4);
+    aux_h = dalloc<float>((size_t)kAuxRows * c.hidden);
+    aux_x = dalloc<uint16_t>((size_t)(kAuxRows + 16) * c.hidden);
+    aux_y = dalloc<float>((size_t)kAuxRows * c.vocab);
+    aux_ids = dalloc<int>(kAuxRows);
     h_stage_bytes = (size_t)Mx * (3 * sizeof(int) + 2 * sizeof(uint64_t)) + 256;
     SD_HIP_CHECK(hipHostMalloc((void **)&h_stage, h_stage_bytes, hipHostMallocDefault));
     SD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev, hipEventDisableTiming));
@@ -751,27 +756,30 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     }
 }
 
+// apply_lm_head and embed_tokens take &self in the reference
+// (model/mod.rs:148, 182): they run on buffers of their own (aux_*), in
+// chunks of kAuxRows rows, and leave the verify pass's logits, argmax rows,
+// hidden states and inputs as they were.  Chunks of <= 16 rows run the M <= 16
+// matmul, whose rows do not depend on the chunking.
 void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
     const ModelCfg &c = cfg;
     SD_HIP_CHECK(hipSetDevice(c.device));
-    logits_rows_last = 0;
     const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
-    for (int r0 = 0; r0 < rows; r0 += c.max_batch) {
-        const int n = std::min(c.max_batch, rows - r0);
-        SD_HIP_CHECK(hipMemcpyAsync(hidden_out, hidden_host + (size_t)r0 * c.hidden, (size_t)n * c.hidden * 4,
+    for (int r0 = 0; r0 < rows; r0 += kAuxRows) {
+        const int n = std::min(kAuxRows, rows - r0);
+        SD_HIP_CHECK(hipMemcpyAsync(aux_h, hidden_host + (size_t)r0 * c.hidden, (size_t)n * c.hidden * 4,
                                     hipMemcpyHostToDevice, st));
-        launch_to_frag16(hidden_out, n, c.hidden, xp, xp_ld, st);
+        launch_to_frag16(aux_h, n, c.hidden, aux_x, c.hidden, st);
         GemmParams p{};
-        gemm_workspace(p);
-        p.seg[0] = seg_of(W, 0, logits, c.vocab, 0, nullptr);
+        p.seg[0] = seg_of(W, 0, aux_y, c.vocab, 0, nullptr);
         p.nseg = 1;
         p.ntiles = W.rows / 16;
-        p.xp = xp;
+        p.xp = aux_x;
         p.K = c.hidden;
         p.M = n;
         p.mode = GM_STORE;
         launch_qgemm(p, st);
-        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.vocab, logits, (size_t)n * c.vocab * 4,
+        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.vocab, aux_y, (size_t)n * c.vocab * 4,
                                     hipMemcpyDeviceToHost, st));
         SD_HIP_CHECK(hipStreamSynchronize(st));
     }
@@ -780,16 +788,13 @@ void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
 void Model::embed_rows(const int *ids, int n, float *out_host) {
     const ModelCfg &c = cfg;
     SD_HIP_CHECK(hipSetDevice(c.device));
-    for (int r0 = 0; r0 < n; r0 += c.max_batch) {
-        const int k = std::min(c.max_batch, n - r0);
-        for (int i = 0; i < k; i++)
-            if (ids[r0 + i] < 0 || ids[r0 + i] >= c.vocab) throw ArgError("token id out of range");
-        stage_wait();
-        std::memcpy(h_stage, ids + r0, k * sizeof(int));
-        SD_HIP_CHECK(hipMemcpyAsync(d_ids, h_stage, k * sizeof(int), hipMemcpyHostToDevice, st));
-        stage_done();
-        launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), c.hidden, d_ids, k, hidden_out, st);
-        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.hidden, hidden_out, (size_t)k * c.hidden * 4,
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= c.vocab) throw ArgError("token id out of range");
+    for (int r0 = 0; r0 < n; r0 += kAuxRows) {
+        const int k = std::min(kAuxRows, n - r0);
+        SD_HIP_CHECK(hipMemcpyAsync(aux_ids, ids + r0, k * sizeof(int), hipMemcpyHostToDevice, st));
+        launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), c.hidden, aux_ids, k, aux_h, st);
+        SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.hidden, aux_h, (size_t)k * c.hidden * 4,
                                     hipMemcpyDeviceToHost, st));
         SD_HIP_CHECK(hipStreamSynchronize(st));
     }
@@ -959,6 +964,9 @@ void Decoder::batched_logits(const uint32_t *drafts, size_t k, float *out) {
     if (k + 1 > (size_t)m.cfg.max_batch) throw ArgError("too many draft tokens for one verify pass");
     for (size_t i = 0; i < k; i++)
         if (drafts[i] >= (uint32_t)m.cfg.vocab) throw ArgError("token id out of range");
+    // every check forward_advance makes, before the cache is touched: a
+    // failed call leaves the decoder as it was
+    if (history.size() - 1 + k + 1 > (size_t)m.cfg.ctx_len) throw ArgError("KV capacity exceeded");
     const uint32_t last = history.back();
     truncate(history.size() - 1);
     std::vector<uint32_t> comb;
@@ -1158,7 +1166,8 @@ void Decoder::verify_greedy_linear(const uint32_t *drafts, size_t k, uint32_t *c
 // bonus_node = first child of that node carrying the bonus token (eagle.rs:700-709),
 // -1 if none or in strict mode.
 void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, int strict,
-                                 uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node) {
+                                 uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node,
+                                 uint32_t *committed, size_t *n_committed, size_t *keep_len, int32_t *stop) {
     if (history.empty()) throw SamplingError("tree_logits with empty history");
     Model &m = *model;
     int32_t root_am = -1;
@@ -1186,13 +1195,43 @@ void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents
     *path_len = best.size();
     const size_t deepest = best.back();
     *bonus = (uint32_t)am[deepest];
+    // Commit composition (eagle.rs:664-732, eagle3.rs:758-782): committed =
+    // the path's tokens and the bonus, cut after the first EOS (stop); an EOS
+    // among the path's tokens keeps the path up to that node and takes no
+    // bonus forward, otherwise the whole path is kept and the bonus joins it
+    // when a child of the deepest node carries it (not in strict mode).
+    auto is_eos = [&](uint32_t x) { return std::find(eos.begin(), eos.end(), x) != eos.end(); };
+    std::vector<uint32_t> com;
+    for (size_t i = 1; i < best.size(); i++) com.push_back(t.tokens[best[i]]);
+    size_t eos_in_path = com.size();
+    for (size_t i = 0; i < com.size(); i++)
+        if (is_eos(com[i])) {
+            eos_in_path = i;
+            break;
+        }
+    com.push_back(*bonus);
+    size_t cut = com.size();
+    for (size_t i = 0; i < com.size(); i++)
+        if (is_eos(com[i])) {
+            cut = i + 1;
+            break;
+        }
+    *stop = cut < com.size() || is_eos(com.back()) ? 1 : 0;
+    com.resize(cut);
+    if (committed) std::copy(com.begin(), com.end(), committed);
+    *n_committed = com.size();
     *bonus_node = -1;
-    if (!strict)
-        for (size_t c = 1; c < n; c++)
-            if (t.parents[c] == deepest && t.tokens[c] == *bonus) {
-                *bonus_node = (int32_t)c;
-                break;
-            }
+    if (eos_in_path < best.size() - 1) {
+        *keep_len = eos_in_path + 2;  // root + the path through the EOS node
+    } else {
+        *keep_len = best.size();
+        if (!strict)
+            for (size_t c = 1; c < n; c++)
+                if (t.parents[c] == deepest && t.tokens[c] == *bonus) {
+                    *bonus_node = (int32_t)c;
+                    break;
+                }
+    }
 }
 
 // ---- rejection sampling ------------------------------------------------------
@@ -1215,7 +1254,7 @@ void Decoder::set_d2t(const int64_t *d2t, size_t n) {
 
 void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
                           size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature,
-                          int use_t2d, size_t max_commit, std::vector<int> &path, int &fin, size_t &used) {
+                          int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used) {
     Model &m = *model;
     const ModelCfg &c = m.cfg;
     if (m.logits_rows_last < n) throw BackendError("acceptance: fewer logits rows than tree nodes");
@@ -1258,6 +1297,7 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     a.q_map = q_vocab == (size_t)c.vocab ? nullptr : m.t2d_inv;
     a.uniforms = m.acc_u;
     a.max_commit = (int)max_commit;
+    a.wor = wor;
     a.out_path = m.acc_out + 4;
     a.out_info = m.acc_out;
     launch_accept_walk(a, m.st);
@@ -1306,7 +1346,7 @@ void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const fl
     std::vector<int> path;
     int fin;
     size_t used;
-    accept_walk(parents.data(), tokens.data(), n, q_rows, k, m.cfg.vocab, qrow.data(), uniforms, temperature, 0,
+    accept_walk(parents.data(), tokens.data(), n, q_rows, k, m.cfg.vocab, qrow.data(), uniforms, temperature, 0, 0,
                 max_commit, path, fin, used);
     size_t nc = 0;
     for (size_t i = 1; i < path.size(); i++) commits[nc++] = (uint32_t)tokens[path[i]];
@@ -1319,10 +1359,11 @@ void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const fl
 void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *q_rows,
                                     size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
                                     const float *uniforms, size_t n_uniforms, float temperature, int use_t2d,
-                                    size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
-                                    size_t *n_used) {
+                                    int siblings, size_t max_commit, uint32_t *path, size_t *path_len,
+                                    int32_t *token, size_t *n_used) {
     Model &m = *model;
     check_temperature(temperature);
+    if (siblings != 0 && siblings != 1) throw ArgError("sibling rule must be 0 (i.i.d.) or 1 (without replacement)");
     if (history.empty()) throw SamplingError("tree_logits with empty history");
     const DraftTreeC t = DraftTreeC::from_arrays(tokens, parents, n);
     if (n_uniforms < n) throw ArgError("rejection verify needs one uniform per tree node");
@@ -1350,7 +1391,7 @@ void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *pare
     int fin;
     size_t used;
     accept_walk(par.data(), tok.data(), (int)n, q_rows, q_rows_n, q_vocab, qr.data(), uniforms, temperature, use_t2d,
-                max_commit, p, fin, used);
+                siblings, max_commit, p, fin, used);
     for (size_t i = 0; i < p.size(); i++) path[i] = (uint32_t)p[i];
     *path_len = p.size();
     *token = fin;

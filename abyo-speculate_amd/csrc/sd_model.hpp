@@ -156,6 +156,12 @@ class Model {
     int amax_ld = 0;
     int nsplit_max = 0;
     int logits_rows_last = 0;  // rows of `logits` / `argmax` produced by the last forward
+    // apply_lm_head / embed_tokens work buffers (kAuxRows rows per chunk),
+    // apart from the verify pass's
+    static constexpr int kAuxRows = 16;
+    float *aux_h = nullptr, *aux_y = nullptr;
+    uint16_t *aux_x = nullptr;
+    int *aux_ids = nullptr;
     // pinned staging for small H2D transfers
     int *h_stage = nullptr;
     size_t h_stage_bytes = 0;
@@ -200,7 +206,8 @@ class Decoder {
     void verify_greedy_linear(const uint32_t *drafts, size_t k, uint32_t *commits, size_t *n_commit,
                               size_t *n_accepted);
     void verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, int strict,
-                            uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node);
+                            uint32_t *path, size_t *path_len, uint32_t *bonus, int32_t *bonus_node,
+                            uint32_t *committed, size_t *n_committed, size_t *keep_len, int32_t *stop);
     void argmax_rows(int32_t *out, size_t n);
     // batched_logits + the rejection walk of vanilla.rs:178-210 on the device
     void verify_rejection_linear(const uint32_t *drafts, size_t k, const float *q_rows, const float *uniforms,
@@ -209,8 +216,8 @@ class Decoder {
     // tree_logits_keep_kv + the tree rejection walk (sd_accept.hip)
     void verify_rejection_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *q_rows,
                                size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of, const float *uniforms,
-                               size_t n_uniforms, float temperature, int use_t2d, size_t max_commit, uint32_t *path,
-                               size_t *path_len, int32_t *token, size_t *n_used);
+                               size_t n_uniforms, float temperature, int use_t2d, int siblings, size_t max_commit,
+                               uint32_t *path, size_t *path_len, int32_t *token, size_t *n_used);
     // EAGLE-3 vocabulary map (eagle3.rs:377-397, 476-513)
     void set_d2t(const int64_t *d2t, size_t n);
     std::vector<int64_t> d2t_host;
@@ -224,7 +231,7 @@ class Decoder {
     // the acceptance walk over logits rows [0, n) of the last pass
     void accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
                      size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature, int use_t2d,
-                     size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
+                     int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
     void truncate(size_t len);
     void tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden, int &prefix);
 };

@@ -11,7 +11,8 @@
 //   p2: slots 4,5   p3: slots 6,7   (half s' = 1)
 // A code is an fp16 number 1024 + q (p0, p1: 0x6400 | q) or 64 + q (p2, p3:
 // 0x5400 | q << 4) holding the element's unsigned quant value q exactly, so
-// the kernel's v_fma_mix can turn it into (q - offset) * scale - min in f32.
+// one packed fp16 FMA or multiply per pair of codes removes the offset and
+// applies the scale (the matmul kernels' QFmt::frag / ifrag).
 #pragma once
 #include <stdint.h>
 

@@ -135,11 +135,11 @@ def load_library(path: str = LIB_PATH):
         "sd_num_hidden_layers": ([P], SZ),
         "sd_hidden_size": ([P], SZ),
         "sd_verify_greedy_linear": ([P, P, SZ, P, pSZ, pSZ], I32),
-        "sd_verify_greedy_tree": ([P, P, P, SZ, I32, P, pSZ, P, P], I32),
+        "sd_verify_greedy_tree": ([P, P, P, SZ, I32, P, pSZ, P, P, P, pSZ, pSZ, P], I32),
         "sd_last_argmax": ([P, P, SZ], I32),
         "sd_verify_rejection_linear": ([P, P, SZ, P, P, SZ, ctypes.c_float, SZ, P, pSZ, pSZ, pSZ], I32),
-        "sd_verify_rejection_tree": ([P, P, P, SZ, P, SZ, SZ, P, P, SZ, ctypes.c_float, I32, SZ, P, pSZ, P, pSZ],
-                                     I32),
+        "sd_verify_rejection_tree": ([P, P, P, SZ, P, SZ, SZ, P, P, SZ, ctypes.c_float, I32, I32, SZ, P, pSZ, P,
+                                      pSZ], I32),
         "sd_set_d2t": ([P, P, SZ], I32),
         "sd_draft_to_target": ([P, P, SZ, P], I32),
         "sd_t2d_mask": ([P, P, SZ], SZ),
@@ -256,6 +256,22 @@ class GgufFile:
         _check(_lib.sd_gguf_tensor_info(self._h, name.encode(), ctypes.byref(t), ctypes.byref(nd), _ptr(ne),
                                         ctypes.byref(off)))
         return t.value, tuple(int(v) for v in ne[:nd.value]), off.value
+
+
+@dataclass
+class TreeCommit:
+    """Greedy tree verify + commit composition (eagle.rs:605-732): commit
+    path[:keep_len] (+ bonus_node when >= 0) with commit_tree_path; committed
+    tokens are EOS-truncated and stop is set when an EOS was committed."""
+    path: List[int]
+    bonus: int
+    bonus_node: int
+    committed: List[int]
+    keep_len: int
+    stop: bool
+
+    def keep(self) -> List[int]:
+        return self.path[:self.keep_len] + ([self.bonus_node] if self.bonus_node >= 0 else [])
 
 
 class HipQuantDecoder:
@@ -443,15 +459,25 @@ class HipQuantDecoder:
                                             ctypes.byref(na)))
         return [int(v) for v in commits[:nc.value]], int(na.value)
 
-    def verify_greedy_tree(self, tree, strict: bool = False):
+    def verify_greedy_tree(self, tree, strict: bool = False, compose: bool = False):
+        """-> (path, bonus, bonus_node); with compose=True a TreeCommit that
+        also holds the EOS-aware commit composition (eagle.rs:664-732)."""
         t, p = tree_arrays(tree)
         path = np.empty(t.size, np.uint32)
-        plen = ctypes.c_size_t()
+        committed = np.empty(t.size, np.uint32)
+        plen, ncom, keep = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
         bonus = ctypes.c_uint32()
-        bnode = ctypes.c_int32()
+        bnode, stop = ctypes.c_int32(), ctypes.c_int32()
         _check(_lib.sd_verify_greedy_tree(self._h, _ptr(t), _ptr(p), t.size, 1 if strict else 0, _ptr(path),
-                                          ctypes.byref(plen), ctypes.byref(bonus), ctypes.byref(bnode)))
-        return [int(v) for v in path[:plen.value]], int(bonus.value), int(bnode.value)
+                                          ctypes.byref(plen), ctypes.byref(bonus), ctypes.byref(bnode),
+                                          _ptr(committed), ctypes.byref(ncom), ctypes.byref(keep),
+                                          ctypes.byref(stop)))
+        pth = [int(v) for v in path[:plen.value]]
+        if not compose:
+            return pth, int(bonus.value), int(bnode.value)
+        return TreeCommit(path=pth, bonus=int(bonus.value), bonus_node=int(bnode.value),
+                          committed=[int(v) for v in committed[:ncom.value]], keep_len=int(keep.value),
+                          stop=bool(stop.value))
 
     def verify_rejection_linear(self, drafts: Sequence[int], q_rows: np.ndarray, uniforms: Sequence[float],
                                 temperature: float, max_commit: int = 0):
@@ -469,8 +495,11 @@ class HipQuantDecoder:
         return [int(v) for v in commits[:nc.value]], int(na.value), int(nu.value)
 
     def verify_rejection_tree(self, tree, q_rows: np.ndarray, q_row_of: Sequence[int], uniforms: Sequence[float],
-                              temperature: float, use_t2d: bool = False, max_commit: int = 0):
-        """-> (path node indices, final token or -1, uniforms_used)."""
+                              temperature: float, use_t2d: bool = False, max_commit: int = 0,
+                              without_replacement: bool = False):
+        """-> (path node indices, final token or -1, uniforms_used).  The
+        sibling rule: i.i.d. siblings (q fixed) or, with without_replacement,
+        siblings drawn without replacement (rejected tokens zeroed in q)."""
         t, p = tree_arrays(tree)
         q = np.ascontiguousarray(q_rows, np.float32)
         if q.ndim != 2:
@@ -484,7 +513,8 @@ class HipQuantDecoder:
         tok = ctypes.c_int32()
         _check(_lib.sd_verify_rejection_tree(self._h, _ptr(t), _ptr(p), t.size, _ptr(q), q.shape[0], q.shape[1],
                                              _ptr(qr), _ptr(u), u.size, float(temperature), 1 if use_t2d else 0,
-                                             max_commit, _ptr(path), ctypes.byref(plen), ctypes.byref(tok),
+                                             1 if without_replacement else 0, max_commit, _ptr(path),
+                                             ctypes.byref(plen), ctypes.byref(tok),
                                              ctypes.byref(nu)))
         return [int(v) for v in path[:plen.value]], int(tok.value), int(nu.value)
 

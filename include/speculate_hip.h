@@ -160,7 +160,10 @@ sd_status sd_observe_returning_last_hidden(sd_model *m, const uint32_t *ids, siz
  * out_final [hidden], out_layers [n_layers_requested][hidden]. */
 sd_status sd_last_hidden_states_multi(sd_model *m, const uint32_t *layers, size_t n_layers, float *out_final,
                                       float *out_layers);
-/* TreeDecoder::apply_lm_head (quantized_llama.rs:112-122): hidden [rows][hidden] -> out [rows][vocab]. */
+/* TreeDecoder::apply_lm_head (quantized_llama.rs:112-122): hidden [rows][hidden] -> out [rows][vocab].
+ * A &self method in the reference (model/mod.rs:148): it runs on buffers of its
+ * own and leaves the last verify pass (its logits rows, sd_last_argmax, device
+ * acceptance) and the decoder state as they were.  embed_tokens likewise. */
 sd_status sd_apply_lm_head(sd_model *m, const float *hidden, size_t rows, float *out);
 /* TreeDecoder::embed_tokens (quantized_llama.rs:258-260 via ModelWeights::embed_tokens): out [n][hidden]. */
 sd_status sd_embed_tokens(sd_model *m, const uint32_t *ids, size_t n, float *out);
@@ -175,13 +178,25 @@ size_t sd_hidden_size(const sd_model *m);                     /* LlamaQuantDecod
 sd_status sd_verify_greedy_linear(sd_model *m, const uint32_t *drafts, size_t k, uint32_t *commits,
                                   size_t *n_commit, size_t *n_accepted);
 /* tree_logits_keep_kv + the greedy longest-path walk of eagle.rs:605-661
- * (eagle3.rs:714-756): path = accepted node indices from the root (room for n),
- * bonus = argmax of the deepest accepted row, bonus_node = the first child of
- * that node carrying the bonus token or -1 (eagle.rs:700-709; -1 when strict).
+ * (eagle3.rs:714-756) + the commit composition of eagle.rs:664-732
+ * (eagle3.rs:758-782):
+ *  - path = accepted node indices from the root (room for n), bonus = argmax
+ *    of the deepest accepted row;
+ *  - committed (room for n; NULL to skip) = the path's tokens (root excluded)
+ *    followed by the bonus, cut after the first token of the decoder's EOS set
+ *    (sd_set_eos_token_ids); stop = 1 when that set was hit (the caller's
+ *    loop ends after this round);
+ *  - keep_len: commit path[0 .. keep_len) (plus bonus_node when >= 0) with
+ *    sd_commit_tree_path.  An EOS among the path's tokens keeps the root and
+ *    the path up to the EOS node, bonus_node = -1 and no bonus forward
+ *    follows; otherwise keep_len = path_len and bonus_node = the first child
+ *    of the deepest node carrying the bonus token or -1 (eagle.rs:700-709;
+ *    always -1 when strict), and the caller observes the bonus when it is -1.
  * strict != 0 takes row 0 from next_logits (EagleRunConfig::strict_root_gemv). */
 sd_status sd_verify_greedy_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                 int32_t strict, uint32_t *path, size_t *path_len, uint32_t *bonus,
-                                int32_t *bonus_node);
+                                int32_t *bonus_node, uint32_t *committed, size_t *n_committed, size_t *keep_len,
+                                int32_t *stop);
 /* First-max argmax of each row of the last verify pass (eagle.rs:626-637 fold). */
 sd_status sd_last_argmax(sd_model *m, int32_t *out, size_t n);
 
@@ -207,10 +222,18 @@ sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t
  * eagle.rs:739-740, eagle3.rs:789); this one reduces to the linear walk above
  * on a chain: the children of a node are tested in BFS order with the rule of
  * vanilla.rs:59-73 against the node's current distribution p (softmax of its
- * row) and its draft row q = q_rows[q_row_of[node]]; a rejection replaces p by
+ * row) and its current draft distribution q; a rejection replaces p by
  * max(0, p - q) renormalised before the next sibling is tested; if no child is
  * accepted the final token is drawn from the current p, after a leaf from the
- * leaf's row.  q_rows has q_rows_n rows of q_vocab entries: q_vocab = vocab
+ * leaf's row.  The committed token follows the target distribution only when
+ * the siblings were drawn as `siblings` states:
+ *  - siblings = 0: i.i.d. draws from q_rows[q_row_of[node]] (with
+ *    replacement); q stays that row for every sibling;
+ *  - siblings = 1: draws without replacement from that row (distinct
+ *    tokens); after each rejected token x, q(x) is set to 0 and q
+ *    renormalised over the remaining mass before the next sibling.
+ * Deterministic top-k siblings meet neither precondition.  At most 16
+ * children per node (SD_ERR_UNSUPPORTED beyond).  q_rows has q_rows_n rows of q_vocab entries: q_vocab = vocab
  * (target ids) or the draft vocabulary of sd_set_d2t (target id x reads entry
  * t2d(x), 0 where unreachable).  use_t2d masks target entries unreachable
  * through d2t to -inf first (mask_target_logits, eagle3.rs:498-513).
@@ -219,8 +242,8 @@ sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t
 sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                    const float *q_rows, size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
                                    const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
-                                   size_t max_commit, uint32_t *path, size_t *path_len, int32_t *token,
-                                   size_t *n_used);
+                                   int32_t siblings, size_t max_commit, uint32_t *path, size_t *path_len,
+                                   int32_t *token, size_t *n_used);
 /* EAGLE-3 vocabulary map (Eagle3DraftCandle's d2t, eagle3.rs:377-397): d2t[draft id]
  * = absolute target id; entries outside [0, vocab) are skipped; the inverse
  * keeps the last draft id of a target id (HashMap::insert). */

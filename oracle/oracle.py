@@ -329,8 +329,38 @@ def silu(x: np.ndarray) -> np.ndarray:
 
 
 def matmul_t(x: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """x [M,K] . w[N,K]^T with f64 accumulation."""
-    return (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    """x [M,K] . w[N,K]^T with f64 accumulation (row chunks bound the f64 copy)."""
+    x64 = x.astype(np.float64)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    step = max(1, (1 << 24) // max(1, w.shape[1]))
+    for r0 in range(0, w.shape[0], step):
+        out[:, r0:r0 + step] = (x64 @ w[r0:r0 + step].astype(np.float64).T).astype(np.float32)
+    return out
+
+
+def attend(q: np.ndarray, k_all: np.ndarray, v_all: np.ndarray, mask: np.ndarray, scale: float) -> np.ndarray:
+    """LayerWeights::run_attn's core (quantized_llama_local.rs:116-129):
+    softmax(q k^T * scale + bias) v with GQA through repeat_kv (query head h
+    reads KV head h // n_rep: repeat_kv concatenates n_rep copies along the
+    sequence axis and reshapes, candle-transformers utils, restated at
+    llama_local.rs:171-177).  q [n_heads, M, hd], k_all/v_all [n_kv, T, hd],
+    mask [M, T] bool (True = visible; the additive bias is 0 / -inf).
+    f64 throughout; returns [M, n_heads, hd] f32."""
+    n_heads, M, hd = q.shape
+    n_kv = k_all.shape[0]
+    n_rep = n_heads // n_kv
+    y = np.empty((M, n_heads, hd), np.float32)
+    K = k_all.astype(np.float64)
+    V = v_all.astype(np.float64)
+    for h in range(n_heads):
+        kv = h // n_rep
+        s = (q[h].astype(np.float64) @ K[kv].T) * float(scale)
+        s = np.where(mask, s, -np.inf)
+        s = s - s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        p = p / p.sum(axis=1, keepdims=True)
+        y[:, h, :] = (p @ V[kv]).astype(np.float32)
+    return y
 
 
 class OracleModel:
@@ -409,7 +439,6 @@ class OracleModel:
         rope = rope_interleaved if cfg.arch == "llama" else rope_half
         x = self.embed(ids)
         collected: Dict[int, np.ndarray] = {}
-        nrep = cfg.n_heads // cfg.n_kv_heads
         scale = np.float32(1.0 / math.sqrt(cfg.head_dim))
         for li in range(cfg.n_layers):
             W = lambda k: self.w[(li, k)]
@@ -432,19 +461,9 @@ class OracleModel:
             else:
                 self.k_cache[li] = np.concatenate([self.k_cache[li], k16], axis=1)
                 self.v_cache[li] = np.concatenate([self.v_cache[li], v16], axis=1)
-            K_all = self.k_cache[li].astype(np.float64)  # [nkv, T, hd]
-            V_all = self.v_cache[li].astype(np.float64)
-            T = K_all.shape[1]
+            T = self.k_cache[li].shape[1]
             assert mask.shape == (M, T), (mask.shape, M, T)
-            y = np.empty((M, cfg.n_heads, cfg.head_dim), np.float32)
-            for h in range(cfg.n_heads):
-                kv = h // nrep
-                s = (q[h].astype(np.float64) @ K_all[kv].T) * float(scale)
-                s = np.where(mask, s, -np.inf)
-                s = s - s.max(axis=1, keepdims=True)
-                p = np.exp(s)
-                p = p / p.sum(axis=1, keepdims=True)
-                y[:, h, :] = (p @ V_all[kv]).astype(np.float32)
+            y = attend(q, self.k_cache[li], self.v_cache[li], mask, scale)
             attn = matmul_t(y.reshape(M, cfg.q_dim), W(K_ATTN_O))
             x = (attn + x).astype(np.float32)
             xn = rms_norm(x, W(K_FFN_NORM)[0], cfg.rms_eps)
@@ -706,6 +725,31 @@ def bonus_in_tree(tree: DraftTree, deepest: int, bonus: int) -> Optional[int]:
     return None
 
 
+def greedy_tree_commit(tree: DraftTree, best: Sequence[int], bonus: int, eos: Sequence[int], strict: bool = False):
+    """Commit composition of run_eagle (eagle.rs:664-732; eagle3.rs:758-782
+    is the same without the bonus-in-tree shortcut, i.e. strict here).
+
+    -> (committed tokens, stop, kept node indices for commit_tree_path,
+    bonus node or None).  committed = path tokens (root excluded) + bonus,
+    cut after the first EOS; an EOS among the path tokens keeps the root and
+    the path through that node (no bonus forward follows); otherwise the
+    whole path is kept, plus the first child of the deepest node carrying the
+    bonus token when not strict.
+    """
+    eos_set = set(int(e) for e in eos)
+    path_tokens = [tree.token_at(i) for i in best[1:]]
+    committed = path_tokens + [bonus]
+    eos_pos = next((i for i, t in enumerate(committed) if t in eos_set), None)
+    stop = eos_pos is not None
+    if eos_pos is not None:
+        committed = committed[:eos_pos + 1]
+    path_eos = next((i for i, t in enumerate(path_tokens) if t in eos_set), None)
+    if path_eos is not None:
+        return committed, stop, list(best[:path_eos + 2]), None
+    bn = None if strict else bonus_in_tree(tree, best[-1], bonus)
+    return committed, stop, list(best) + ([bn] if bn is not None else []), bn
+
+
 def greedy_linear_accept(drafts: Sequence[int], argmaxes: Sequence[int]) -> Tuple[int, int]:
     """Greedy verify of a k-token chain: (#accepted, bonus = argmax of row #accepted)."""
     a = 0
@@ -751,7 +795,8 @@ def rejection_linear_accept(target_rows: Sequence[np.ndarray], q_rows: Sequence[
 
 def rejection_tree_accept(tree: "DraftTree", target_rows: Sequence[np.ndarray], q_rows: Sequence[np.ndarray],
                           q_row_of: Sequence[int], uniforms: Sequence[float], temperature: float,
-                          t2d_mask: Optional[np.ndarray] = None, max_commit: Optional[int] = None):
+                          t2d_mask: Optional[np.ndarray] = None, max_commit: Optional[int] = None,
+                          without_replacement: bool = False):
     """Tree rejection walk (a build extension: the reference has no tree rule,
     eagle.rs:739-740 and eagle3.rs:789 ignore the temperature), made of the
     reference's own steps: at the current node, children are tested in BFS
@@ -763,6 +808,12 @@ def rejection_tree_accept(tree: "DraftTree", target_rows: Sequence[np.ndarray], 
     sample_from_distribution(p) (tokens.rs:99-120).  On a chain this is exactly
     rejection_linear_accept.  t2d_mask (eagle3.rs:498-513) sets unreachable
     target logits to -inf first.
+
+    Sibling rule: with i.i.d. siblings q stays the node's draft row; with
+    ``without_replacement`` (siblings drawn without replacement from q) the
+    sibling tested after rejections x_0..x_{r-1} sees q_r(y) = q(y) / R_r off
+    the rejected tokens and 0 on them, R_0 = 1, R_{r+1} = R_r - q(x_r) in f32
+    (0 everywhere once R_r <= 0), and each rejection adjusts p against that q_r.
 
     Returns (path node indices, final token or None, uniforms used).
     """
@@ -781,8 +832,14 @@ def rejection_tree_accept(tree: "DraftTree", target_rows: Sequence[np.ndarray], 
             row[~t2d_mask] = -np.inf
         p = softmax_t(row, temperature)
         accepted = None
+        R = np.float32(1.0)
+        rejected: List[int] = []
         for c in children[node]:
-            q = np.asarray(q_rows[q_row_of[node]], np.float32)
+            q0 = np.asarray(q_rows[q_row_of[node]], np.float32)
+            q = q0
+            if without_replacement:
+                q = (q0 / R).astype(np.float32) if R > 0 else np.zeros_like(q0)
+                q[rejected] = 0.0
             tok = tree.token_at(c)
             u = uniforms[used]
             used += 1
@@ -790,6 +847,8 @@ def rejection_tree_accept(tree: "DraftTree", target_rows: Sequence[np.ndarray], 
                 accepted = c
                 break
             p = adjusted_distribution(p, q)
+            rejected.append(tok)
+            R = np.float32(R - q0[tok])
         if accepted is not None:
             path.append(accepted)
             node = accepted

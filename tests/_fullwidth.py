@@ -1,0 +1,100 @@
+"""Production-width parity helpers: a 2-layer decoder at the full Llama-3-8B
+or Qwen2.5-7B widths on the device, and the oracle model built from the same
+GGUF bytes, with the oracle's KV prefix read back from the device cache (the
+seeded synthetic prefix of prime_synthetic), so that one oracle forward at
+the verify shape checks the device pass at the benchmark's widths: every
+8B-shaped matrix kernel (K1 with KW=8 / KW=1, RT 1 and 2, the 8-slice split-K
+of the M > 16 kernel and its finalisers), RMSNorm at hidden 4096 / ffn
+14336, the 128256-row lm_head and its argmax partials, and attention over
+thousands of cached positions."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+LLAMA8B = dict(arch="llama", hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+               rope_theta=500000.0, rms_eps=1e-5)
+QWEN7B = dict(arch="qwen2", hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, ffn=18944, vocab=152064,
+              rope_theta=1e6, rms_eps=1e-6)
+TOL = 1e-2
+
+
+def build_pair(hip, shape, mix, n_layers, ctx):
+    """(device decoder, oracle model) of one seeded 2-layer model."""
+    ocfg = O.ModelConfig(n_layers=n_layers, ctx_len=ctx, mix=mix, seed=0x5EED0003, **shape)
+    mix_id = {"q4_k_m": hip.MIX_Q4_K_M, "q5k_q80": hip.MIX_Q5K_Q80}[mix]
+    dec = hip.HipQuantDecoder(hip.Config(arch=0 if shape["arch"] == "llama" else 1, n_layers=n_layers,
+                                         hidden=shape["hidden"], n_heads=shape["n_heads"],
+                                         n_kv_heads=shape["n_kv_heads"], head_dim=shape["head_dim"],
+                                         ffn=shape["ffn"], vocab=shape["vocab"], rope_theta=shape["rope_theta"],
+                                         rms_eps=shape["rms_eps"], ctx_len=ctx, max_batch=64))
+    dec.synthesize(mix_id, ocfg.seed, ocfg.weight_std)
+    keys = [(-1, O.K_TOK_EMBD), (-1, O.K_OUTPUT_NORM), (-1, O.K_OUTPUT)]
+    for li in range(n_layers):
+        keys += [(li, k) for k in ocfg.layer_kinds()]
+    tensors = {}
+    for (li, k) in keys:
+        fmt, rows, K, _ = dec.tensor_info(li, k)
+        assert fmt == ocfg.fmt(li, k), (li, k, fmt)
+        tensors[(li, k)] = (fmt, dec.get_tensor(li, k))
+    # the device generator is the oracle's, at the full width too (one
+    # matrix of each format family checked here; the rest at small widths)
+    for (li, k) in ((0, O.K_ATTN_K), (n_layers - 1, O.K_ATTN_V)):
+        assert np.array_equal(tensors[(li, k)][1], O.synth_tensor(ocfg, li, k)[1]), (li, k)
+    return dec, O.OracleModel(ocfg, tensors)
+
+
+def load_prefix(dec, om, P):
+    """Oracle KV cache := the device's rows [0, P) (fp16 values)."""
+    c = om.cfg
+    om.clear_kv_cache()
+    for li in range(c.n_layers):
+        k = np.empty((c.n_kv_heads, P, c.head_dim), np.float32)
+        v = np.empty_like(k)
+        for h in range(c.n_kv_heads):
+            k[h] = dec.read_kv_rows(li, 0, h, 0, P).view(np.float16).astype(np.float32)
+            v[h] = dec.read_kv_rows(li, 1, h, 0, P).view(np.float16).astype(np.float32)
+        om.k_cache[li], om.v_cache[li] = k, v
+
+
+def oracle_pass(om, ids, positions, mask):
+    """(logits, final-norm hidden) of one oracle forward; the oracle cache
+    grows by len(ids) rows as the device's does."""
+    hidden, _ = om.forward(ids, positions, mask)
+    return om.lm_head(hidden), hidden
+
+
+def tree_mask(tree: O.DraftTree, P: int) -> np.ndarray:
+    n = len(tree)
+    m = np.ones((n, P + n), bool)
+    m[:, P:] = np.asarray(tree.attention_mask_bool(), bool)
+    return m
+
+
+def rel_rows(a, b):
+    """Per-row max |a - b| / max |b|."""
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    return np.max(np.abs(a64 - b64), axis=-1) / np.maximum(np.max(np.abs(b64), axis=-1), 1e-30)
+
+
+def argmax_agreement(dev, ora):
+    """Rows whose oracle top-2 margin exceeds twice the row's largest
+    device/oracle difference must have the same first-max argmax.  Returns
+    the indices of the rows that are nearer a tie than that."""
+    near = []
+    for i in range(dev.shape[0]):
+        s = np.sort(ora[i].astype(np.float64))[::-1]
+        d = float(np.max(np.abs(dev[i].astype(np.float64) - ora[i])))
+        if s[0] - s[1] > 2 * d:
+            assert O.argmax_fold(dev[i]) == O.argmax_fold(ora[i]), i
+        else:
+            near.append(i)
+    return near
+
+
+def random_tree(hip, rng, root, vocab, branching, n):
+    cands = [[int(v) for v in rng.integers(0, vocab, b)] for b in branching]
+    lps = [list(np.sort(np.log(rng.dirichlet(np.ones(b))))[::-1].astype(np.float32)) for b in branching]
+    toks, pars = hip.tree_prune(hip.tree_cartesian(root, cands), lps, n)
+    return O.DraftTree(list(toks), list(pars))

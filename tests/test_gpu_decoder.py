@@ -1,14 +1,18 @@
 """Decoder-level GPU parity (through the C ABI) against the oracle decoder.
 
 Contract (per the path's spec): logits and hidden states within 1e-2
-relative (max |a-b| / max |b| per row block); greedy acceptance results
-identical except where the oracle row has a near tie (top-2 margin below the
-logits tolerance); KV compaction bit-exact (a pure row copy).
+relative (max |a-b| / max |b| per row block); first-max argmaxes and greedy
+acceptance identical to the oracle's wherever the oracle's top-2 margin
+exceeds twice the row's actual device/oracle difference -- such near ties are
+counted and bounded, not skipped -- and the device walk always equal to the
+walk over the device's own argmaxes; KV compaction bit-exact (a pure row
+copy).
 """
 import numpy as np
 import pytest
 
 import oracle as O
+from _fullwidth import argmax_agreement
 from _models import MIX_IDS, hip_cfg, oracle_cfg, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -32,11 +36,6 @@ def make_pair(hip, prefix_len=128, seed=1, **over):
     return od, hd, prefix
 
 
-def safe(row: np.ndarray) -> bool:
-    s = np.sort(row.astype(np.float64))[::-1]
-    return (s[0] - s[1]) > 4 * TOL * np.max(np.abs(row))
-
-
 def greedy_chain(od, n):
     """The oracle's own greedy continuation (then restored)."""
     L = len(od.history)
@@ -53,8 +52,7 @@ def test_observe_and_next_logits(hip):
     od, hd, _ = make_pair(hip)
     a, b = hd.next_logits(), od.next_logits()
     assert rel_err(a, b) < TOL
-    if safe(b):
-        assert int(np.argmax(a)) == O.argmax_fold(b)
+    assert argmax_agreement(a[None], b[None]) == []
     assert hd.history() == od.history and hd.cache_len() == len(od.history)
 
 
@@ -69,14 +67,17 @@ def test_batched_logits_and_greedy_linear(hip):
     for i in range(5):
         assert rel_err(a[i], b[i]) < TOL, i
     assert hd.history() == od.history
-    # device greedy acceptance == oracle walk on oracle logits
+    # device greedy acceptance == oracle walk on oracle logits; every row's
+    # argmax must agree unless the oracle's top-2 margin is within twice the
+    # row's device/oracle difference (counted, not skipped)
+    near = argmax_agreement(a, b)
+    assert near == [], near
     hd.rollback_to(L)
     commits, n_acc = hd.verify_greedy_linear(drafts)
     am = [O.argmax_fold(r) for r in b]
     exp_acc, exp_bonus = O.greedy_linear_accept(drafts, am)
-    if all(safe(b[i]) for i in range(exp_acc + 1)):
-        assert n_acc == exp_acc == 2
-        assert commits == drafts[:exp_acc] + [exp_bonus]
+    assert n_acc == exp_acc == 2
+    assert commits == drafts[:exp_acc] + [exp_bonus]
     # device argmax == host first-max fold of the device logits (bit-exact logic)
     got_am = hd.last_argmax(5)
     assert [int(v) for v in got_am] == [O.argmax_fold(r) for r in a]
@@ -106,7 +107,13 @@ def test_tree_keep_kv_verify_and_commit(hip):
     path, bonus, bnode = hd.verify_greedy_tree(tree)
     am_o = [O.argmax_fold(r) for r in lo]
     best, exp_bonus = O.greedy_tree_accept(tree, lo, am_o)
-    if all(safe(lo[i]) for i in range(n)):
+    near = argmax_agreement(lg, lo)
+    assert len(near) <= 1, near
+    # the device walk is the walk over its own argmaxes ...
+    dbest, dbonus = O.greedy_tree_accept(tree, None, [int(v) for v in hd.last_argmax(n)])
+    assert path == dbest and bonus == dbonus
+    # ... and the oracle's, unless a row on it sits on a near tie
+    if not set(near) & set(best):
         assert path == best and bonus == exp_bonus
         assert bnode == (O.bonus_in_tree(tree, best[-1], exp_bonus) or -1)
         assert len(best) == 4  # root + the embedded 3-token greedy chain
@@ -146,13 +153,18 @@ def test_strict_root_row(hip):
         # different row counts take different K splits; fp16 activations carry
         # the rounding differences through the layers
         assert rel_err(row, nl.astype(np.float64)) < 2e-3
-        if safe(nl):
-            assert int(np.argmax(row)) == int(np.argmax(nl))  # tree_logits_consistency.rs:74-122
+        assert argmax_agreement(row[None], nl[None]) == []  # tree_logits_consistency.rs:74-122
     assert np.array_equal(strict[1:].view(np.uint32), fast[1:].view(np.uint32))
     # the strict row is exactly the single-token (M = 1) pass of the root
     hd.rollback_to(len(prefix) - 1)
     hd.observe([prefix[-1]])
     assert np.array_equal(strict[0].view(np.uint32), hd.next_logits().view(np.uint32))
+    # and the strict tree_logits of the oracle (quantized_llama.rs:262-325)
+    ostrict = od.tree_logits(tree)
+    assert od.cache_len == len(prefix)
+    for i in range(len(tree)):
+        assert rel_err(strict[i], ostrict[i]) < TOL, i
+    assert len(argmax_agreement(strict, ostrict)) <= 1
 
 
 def test_error_semantics_keep_state(hip):
@@ -185,6 +197,80 @@ def test_error_semantics_keep_state(hip):
     assert rel_err(hd.next_logits(), od.next_logits()) < TOL
     with pytest.raises(hip.ArgError):
         hd.observe([40000])
+
+
+def test_capacity_error_keeps_state(hip):
+    """A verify that does not fit the cache fails before anything moves; the
+    decoder then continues exactly where it was (model/mod.rs:35-38)."""
+    od, hd, prefix = make_pair(hip, prefix_len=126, ctx_len=128)
+    with pytest.raises(hip.ArgError):
+        hd.batched_logits([1, 2, 3])  # 125 + 4 rows > 128
+    assert hd.history() == prefix and hd.cache_len() == len(prefix)
+    with pytest.raises(hip.ArgError):
+        hd.verify_greedy_linear([1, 2, 3])
+    assert hd.history() == prefix and hd.cache_len() == len(prefix)
+    assert rel_err(hd.next_logits(), od.next_logits()) < TOL
+    hd.observe([9])
+    od.observe([9])
+    assert rel_err(hd.next_logits(), od.next_logits()) < TOL
+    a = hd.batched_logits([4])  # 127 + 1 rows fit
+    b = od.batched_logits([4])
+    assert rel_err(a, b) < TOL and hd.cache_len() == 128
+
+
+def test_apply_lm_head_leaves_verify_state(hip):
+    """apply_lm_head / embed_tokens take &self (model/mod.rs:148, 182): a
+    pending argmax and device acceptance of the last verify survive them."""
+    od, hd, prefix = make_pair(hip, prefix_len=40)
+    drafts = greedy_chain(od, 3)
+    rows = hd.batched_logits(drafts)
+    am = [int(v) for v in hd.last_argmax(4)]
+    h = np.random.default_rng(3).standard_normal((37, 512)).astype(np.float32)
+    out = hd.apply_lm_head(h)
+    assert rel_err(out, od.m.lm_head(h)) < TOL
+    hd.embed_tokens([1, 2, 3])
+    assert [int(v) for v in hd.last_argmax(4)] == am == [O.argmax_fold(r) for r in rows]
+    # the 37 rows ran in chunks of 16: each row equals its own 1-row product
+    for i in (0, 16, 36):
+        assert np.array_equal(hd.apply_lm_head(h[i:i + 1])[0].view(np.uint32), out[i].view(np.uint32))
+    assert hd.history() == prefix + drafts
+
+
+def test_greedy_tree_commit_with_eos(hip):
+    """EOS-aware commit composition (eagle.rs:664-732) on the device against
+    the oracle's, for an EOS inside the accepted path, an EOS bonus and none."""
+    od, hd, prefix = make_pair(hip, prefix_len=64)
+    chain = greedy_chain(od, 3)
+    tree = O.build_cartesian_tree(prefix[-1], _tree_with_chain(chain, 32000))
+    n = len(tree)
+    lo, _ = od.tree_logits_keep_kv(tree)
+    od.rollback_to(len(prefix))
+    lg, _ = hd.tree_logits_keep_kv(tree)
+    assert argmax_agreement(lg, lo) == []
+    best, bonus = O.greedy_tree_accept(tree, lo)
+    assert len(best) == 4
+    for eos in ([], [chain[1]], [bonus], [chain[0], bonus]):
+        for strict in (False, True):
+            hd.rollback_to(len(prefix))
+            hd.set_eos_token_ids(eos)
+            res = hd.verify_greedy_tree((tree.tokens(), tree.parents()), strict=strict, compose=True)
+            com, stop, keep, bn = O.greedy_tree_commit(tree, best, bonus, eos, strict=strict)
+            assert res.path == best and res.bonus == bonus
+            assert res.committed == com and res.stop == stop, (eos, strict)
+            assert res.keep() == keep and res.bonus_node == (bn if bn is not None else -1), (eos, strict)
+    # committing the composed path leaves the cache as the oracle's
+    hd.rollback_to(len(prefix))
+    hd.set_eos_token_ids([chain[1]])
+    res = hd.verify_greedy_tree((tree.tokens(), tree.parents()), compose=True)
+    hd.commit_tree_path((tree.tokens(), tree.parents()), res.keep())
+    od.tree_logits_keep_kv(tree)
+    od.commit_tree_path(tree, res.keep())
+    assert hd.history() == od.history == prefix + chain[:2]
+    assert hd.cache_len() == od.cache_len == len(prefix) + 2
+    hd.observe([11])
+    od.observe([11])
+    assert rel_err(hd.next_logits(), od.next_logits()) < TOL
+    assert n > 4
 
 
 def test_hidden_state_apis(hip):

@@ -33,31 +33,42 @@ def _p64(row, T, mask=None):
     return e / e.sum()
 
 
-def _walk64(tree, rows, q_rows, q_row_of, u, T, mask=None, max_commit=None):
-    """f64 restatement of the walk; returns (path, token, min decision margin,
-    draw target, f64 CDF of the drawn distribution)."""
+def _walk64(tree, rows, q_rows, q_row_of, u, T, mask=None, max_commit=None, flip=frozenset(), wor=False):
+    """f64 restatement of the walk; returns (path, token, {uniform index:
+    decision margin}, draw target, f64 CDF of the drawn distribution).  The
+    accept decisions of the uniforms in `flip` are inverted (the other side
+    of a near tie)."""
     n = len(tree)
     children = [[] for _ in range(n)]
     for c in range(1, n):
         children[tree.parent_of(c)].append(c)
-    used, node, path, margin = 0, 0, [0], np.inf
+    used, node, path, margins = 0, 0, [0], {}
     while True:
         if max_commit and len(path) - 1 >= max_commit:
-            return path, None, margin, None, None
+            return path, None, margins, None, None
         p = _p64(rows[node], T, mask)
         acc = None
+        q0 = np.asarray(q_rows[q_row_of[node]], np.float64) if children[node] else None
+        R, rejected = 1.0, []
         for c in children[node]:
-            q = np.asarray(q_rows[q_row_of[node]], np.float64)
+            q = q0
+            if wor:
+                q = q0 / R if R > 0 else np.zeros_like(q0)
+                q[rejected] = 0.0
             tok = tree.token_at(c)
             ratio = 1.0 if q[tok] <= 0 else min(1.0, p[tok] / q[tok])
-            margin = min(margin, abs(u[used] - ratio))
+            margins[used] = abs(u[used] - ratio)
             ok = q[tok] <= 0 or u[used] <= ratio
+            if used in flip:
+                ok = not ok
             used += 1
             if ok:
                 acc = c
                 break
             a = np.maximum(p - q, 0.0)
             p = a / a.sum()
+            rejected.append(tok)
+            R -= q0[tok]
         if acc is not None:
             path.append(acc)
             node = acc
@@ -68,26 +79,46 @@ def _walk64(tree, rows, q_rows, q_row_of, u, T, mask=None, max_commit=None):
         return path, tok, margin, t, cdf
 
 
-def _check_walk(dev_path, dev_tok, ora_path, ora_tok, tree, rows, q_rows, q_row_of, u, T, mask=None,
-                max_commit=None):
-    """Returns 'exact' or 'boundary'; asserts the device result is valid.  A
-    draw is near a boundary when its target is within 4 sqrt(V) f32 ulps of
-    1 of one (the spread of sequential f32 running sums over V terms)."""
-    path64, tok64, margin, t, cdf = _walk64(tree, rows, q_rows, q_row_of, u, T, mask, max_commit)
-    draw_eps = 4.0 * np.sqrt(len(rows[0])) * 2.0 ** -24
-    if margin < DEC_EPS:
-        return "boundary"
-    assert dev_path == ora_path == path64
+def _draw_ok(tok, tok64, t, cdf, draw_eps):
+    """(token valid, drawn away from a CDF boundary).  Near a boundary the
+    token may be either of the two that meet there."""
     if tok64 is None:
-        assert dev_tok is None and ora_tok is None
-        return "exact"
+        return tok is None, True
     lo = cdf[tok64 - 1] if tok64 > 0 else 0.0
     near = min(t - lo, cdf[tok64] - t) < draw_eps
     if not near:
-        assert dev_tok == ora_tok == tok64, (dev_tok, ora_tok, tok64)
-        return "exact"
-    # near a boundary: the device token must be one of the two meeting there
-    assert dev_tok in (tok64 - 1, tok64, tok64 + 1)
+        return tok == tok64, True
+    return tok in (tok64 - 1, tok64, tok64 + 1), False
+
+
+def _check_walk(dev_path, dev_tok, ora_path, ora_tok, tree, rows, q_rows, q_row_of, u, T, mask=None,
+                max_commit=None, wor=False):
+    """Returns 'exact' or 'boundary' and asserts that the device and the
+    oracle results are valid walks.  A decision is a near tie when |u -
+    min(1, p/q)| < DEC_EPS: both sides of it are then valid, and device and
+    oracle must each follow one of them exactly.  A draw is near a boundary
+    when its target is within 4 sqrt(V) f32 ulps of 1 of one (the spread of
+    sequential f32 running sums over V terms): the token is then one of the
+    two meeting there.  Everything else must agree exactly."""
+    path64, tok64, margins, t, cdf = _walk64(tree, rows, q_rows, q_row_of, u, T, mask, max_commit, wor=wor)
+    draw_eps = 4.0 * np.sqrt(len(rows[0])) * 2.0 ** -24
+    ties = [i for i, m in margins.items() if m < DEC_EPS]
+    if not ties:
+        assert dev_path == ora_path == path64, (dev_path, ora_path, path64)
+        ok_d, exact = _draw_ok(dev_tok, tok64, t, cdf, draw_eps)
+        ok_o, _ = _draw_ok(ora_tok, tok64, t, cdf, draw_eps)
+        assert ok_d and ok_o, (dev_tok, ora_tok, tok64)
+        if exact:
+            assert dev_tok == ora_tok == tok64
+            return "exact"
+        return "boundary"
+    # one or more near ties: every combination of their outcomes is valid
+    alts = []
+    for k in range(1 << len(ties)):
+        flip = frozenset(ties[j] for j in range(len(ties)) if (k >> j) & 1)
+        alts.append(_walk64(tree, rows, q_rows, q_row_of, u, T, mask, max_commit, flip=flip, wor=wor))
+    for path, tok in ((dev_path, dev_tok), (ora_path, ora_tok)):
+        assert any(path == a[0] and _draw_ok(tok, a[1], a[3], a[4], draw_eps)[0] for a in alts), (path, tok)
     return "boundary"
 
 
@@ -108,6 +139,23 @@ def _draft_rows(rng, k, V, scale=2.0):
     return out
 
 
+def _peaked_q(p, favour, rng, n_keep=6):
+    """A draft row that equals the target row p except on n_keep random
+    tokens, which keep a fifth of their mass; the mass taken from them goes
+    to the `favour` tokens (the drafts).  After a rejection the adjusted
+    distribution max(p - q, 0) is then supported on those n_keep tokens only,
+    so the resample lands well inside one of a few wide CDF steps even where
+    p itself is nearly flat (T = 1 over a large vocabulary)."""
+    q = np.asarray(p, np.float32).copy()
+    S = rng.choice(np.flatnonzero(q > 0), n_keep, replace=False)
+    S = np.setdiff1d(S, favour)
+    moved = float(np.sum(q[S]) * 0.8)
+    q[S] *= np.float32(0.2)
+    for f in favour:
+        q[f] += np.float32(moved / len(favour))
+    return q
+
+
 @pytest.mark.parametrize("over,k", [
     (dict(), 4),
     # Qwen2-shaped variant of the mixed-quantisation workload: QKV bias,
@@ -121,9 +169,17 @@ def test_rejection_linear_matches_oracle(hip, over, k, T):
     rng = np.random.default_rng(17 + k)
     L = len(prefix)
     kinds = {"exact": 0, "boundary": 0}
-    for trial in range(6):
+    for trial in range(10 if T > 0 else 6):
         q = _draft_rows(rng, k, V)
-        if trial % 2 == 0:
+        if trial >= 6:
+            # draft rows equal to the target's except on a few tokens, the
+            # drafts favoured: rejections resample from a few wide CDF steps
+            drafts = [int(v) for v in rng.integers(0, V, k)]
+            rows = hd.batched_logits(drafts)
+            hd.rollback_to(L)
+            for i in range(k):
+                q[i] = _peaked_q(O.softmax_t(rows[i], T), [drafts[i]], rng)
+        elif trial % 2 == 0:
             drafts = [int(O.sample_u(q[i], float(rng.random()))) for i in range(k)]
         else:
             # drafts that the target likes, so that acceptance runs deep
@@ -149,10 +205,10 @@ def test_rejection_linear_matches_oracle(hip, over, k, T):
             kinds[kind] += 1
             if kind == "exact":
                 assert commits == oc and n_acc == on and used == ou
-    # at T = 1 the tiny model's rows are nearly flat over 32000 tokens, so most
-    # draws sit within rounding of a CDF boundary (checked for validity only)
-    if T != 1.0:
-        assert kinds["exact"] >= 8, kinds
+    # at T = 1 the tiny model's rows are nearly flat over 32000 tokens, so a
+    # draw from them sits within rounding of a CDF boundary (checked for
+    # validity); the peaked draft rows give exact cases at every temperature
+    assert kinds["exact"] >= (4 if T == 1.0 else 8), kinds
 
 
 def test_rejection_linear_errors_keep_state(hip):
@@ -189,7 +245,7 @@ def test_rejection_tree_d2t_matches_oracle(hip, T, use_t2d):
         hd.draft_to_target([Vd])
     L = len(prefix)
     kinds = {"exact": 0, "boundary": 0}
-    for trial in range(3):
+    for trial in range(5 if use_t2d else 3):
         branching = (4, 3, 2, 2, 1, 1, 1)
         cands = [[int(d2t[v]) for v in rng.choice(Vd, b, replace=False)] for b in branching]
         lps = [list(np.sort(np.log(rng.dirichlet(np.ones(b))))[::-1].astype(np.float32)) for b in branching]
@@ -202,6 +258,16 @@ def test_rejection_tree_d2t_matches_oracle(hip, T, use_t2d):
         u = [float(x) for x in rng.random(n, dtype=np.float32)]
         rows, _ = hd.tree_logits_keep_kv((toks, pars))
         hd.rollback_to(L)
+        if trial >= 3:
+            # draft rows that are the masked target rows but for a few tokens,
+            # the node's children favoured (exact resamples at any temperature)
+            for i in range(n):
+                kids = [tree.token_at(c) for c in range(1, n) if tree.parent_of(c) == i]
+                r = np.array(rows[i], np.float32)
+                r[~mask] = -np.inf
+                qt = _peaked_q(O.softmax_t(r, T), kids or [int(d2t[0])], rng) if T > 0 else None
+                if qt is not None:
+                    q_d[i] = qt[d2t]
         path, tok, used = hd.verify_rejection_tree((toks, pars), q_d, q_row_of, u, T, use_t2d)
         assert hd.cache_len() == L - 1 + n
         hd.rollback_to(L)
@@ -218,8 +284,45 @@ def test_rejection_tree_d2t_matches_oracle(hip, T, use_t2d):
             assert used == oused
         if use_t2d and tok >= 0:
             assert mask[tok]
-    if T != 1.0:
+    # without the t2d mask the 24000 unreachable target tokens keep their
+    # nearly flat T = 1 mass, so those draws are checked for validity only
+    if T != 1.0 or use_t2d:
         assert kinds["exact"] >= 2, kinds
+
+
+@pytest.mark.parametrize("T", [1.0, 0.3])
+def test_rejection_tree_without_replacement_matches_oracle(hip, T):
+    """The without-replacement sibling rule (q zeroed at rejected tokens and
+    renormalised) on the device against the oracle, over a tree whose
+    siblings are distinct tokens."""
+    ocfg, hd, prefix = _pair(hip, prefix_len=40)
+    V = ocfg.vocab
+    rng = np.random.default_rng(321)
+    L = len(prefix)
+    kinds = {"exact": 0, "boundary": 0}
+    for trial in range(4):
+        cands = [[int(v) for v in rng.choice(V, b, replace=False)] for b in (5, 3, 2, 1)]
+        tree = O.build_cartesian_tree(prefix[-1], cands)
+        n = len(tree)
+        rows, _ = hd.tree_logits_keep_kv((tree.tokens(), tree.parents()))
+        hd.rollback_to(L)
+        q = _draft_rows(rng, n, V)
+        if trial % 2:
+            for i in range(n):
+                kids = [tree.token_at(c) for c in range(1, n) if tree.parent_of(c) == i]
+                q[i] = _peaked_q(O.softmax_t(rows[i], T), kids or [0], rng)
+        u = [float(x) for x in rng.random(n, dtype=np.float32)]
+        path, tok, used = hd.verify_rejection_tree((tree.tokens(), tree.parents()), q, list(range(n)), u, T,
+                                                   without_replacement=True)
+        hd.rollback_to(L)
+        opath, otok, oused = O.rejection_tree_accept(tree, list(rows), list(q), list(range(n)), u, T,
+                                                     without_replacement=True)
+        kind = _check_walk(path, tok if tok >= 0 else None, opath, otok, tree, list(rows), list(q), list(range(n)),
+                           u, T, wor=True)
+        kinds[kind] += 1
+        if kind == "exact":
+            assert used == oused
+    assert kinds["exact"] >= 1, kinds
 
 
 def test_rejection_tree_chain_equals_linear(hip):

@@ -108,3 +108,73 @@ def test_t2d_mask_removes_unreachable_targets():
     for _ in range(200):
         _, fin, _ = O.rejection_tree_accept(tree, [row], [q], [-1], [float(rng.random())], 1.0, t2d_mask=mask)
         assert mask[fin]
+
+
+# ---- siblings drawn without replacement ---------------------------------------------
+def _wor_candidates(qv, n, uvals):
+    """n distinct tokens drawn sequentially without replacement from q."""
+    q = np.asarray(qv, np.float64).copy()
+    out = []
+    for j in range(n):
+        c = np.cumsum(q) / q.sum()
+        t = int(min(np.searchsorted(c, float(uvals[j]), side="right"), len(c) - 1))
+        while q[t] <= 0:  # drift past the last positive entry
+            t -= 1
+        out.append(t)
+        q[t] = 0.0
+    return out
+
+
+def _first_token_distribution_wor(p, q, n_children, trials, rng, wor=True):
+    V = len(p)
+    logits = np.log(np.asarray(p, np.float64) + 1e-30).astype(np.float32)
+    qv = np.asarray(q, np.float32)
+    counts = np.zeros(V)
+    for _ in range(trials):
+        u = rng.random(n_children + 1, dtype=np.float32)
+        cands = _wor_candidates(qv, n_children, rng.random(n_children))
+        tree = O.DraftTree([99] + cands, [0] * (n_children + 1))
+        rows = [logits] * (n_children + 1)
+        path, fin, _ = O.rejection_tree_accept(tree, rows, [qv], [0] + [-1] * n_children, [float(x) for x in u],
+                                               1.0, without_replacement=wor)
+        tok = tree.token_at(path[1]) if len(path) > 1 else fin
+        counts[tok] += 1
+    return counts / trials
+
+
+@pytest.mark.parametrize("p,q,nc", [
+    ([0.5, 0.3, 0.15, 0.05], [0.25] * 4, 3),
+    ([0.7, 0.15, 0.1, 0.05], [0.05, 0.1, 0.15, 0.7], 3),
+    ([0.1, 0.2, 0.3, 0.4], [0.4, 0.3, 0.2, 0.1], 2),
+    ([0.05, 0.05, 0.6, 0.2, 0.1], [0.3, 0.3, 0.2, 0.1, 0.1], 4),
+])
+def test_without_replacement_rule_preserves_target(p, q, nc):
+    """Distinct siblings (drawn without replacement from q) with q zeroed at
+    each rejected token and renormalised: the committed token follows p."""
+    rng = np.random.default_rng(11)
+    freq = _first_token_distribution_wor(p, q, nc, 12000, rng)
+    assert _tv(freq, p) < 0.03, freq
+
+
+def test_iid_rule_on_distinct_siblings_is_biased():
+    """The i.i.d. rule applied to siblings drawn without replacement (the
+    mismatch the sibling flag exists for) moves the distribution off p."""
+    rng = np.random.default_rng(11)
+    p, q = [0.05, 0.05, 0.6, 0.2, 0.1], [0.3, 0.3, 0.2, 0.1, 0.1]
+    freq = _first_token_distribution_wor(p, q, 4, 12000, rng, wor=False)
+    assert _tv(freq, p) > 0.05, freq
+
+
+def test_without_replacement_chain_is_the_linear_walk():
+    """One child per node: nothing is ever renormalised, both rules agree."""
+    rng = np.random.default_rng(12)
+    V, k = 12, 4
+    rows = [rng.standard_normal(V).astype(np.float32) * 2 for _ in range(k + 1)]
+    q = [np.asarray(rng.dirichlet(np.ones(V)), np.float32) for _ in range(k)]
+    drafts = [int(O.sample_u(q[i], float(rng.random()))) for i in range(k)]
+    tree = O.DraftTree.linear(7, drafts)
+    for _ in range(30):
+        u = [float(x) for x in rng.random(k + 1, dtype=np.float32)]
+        a = O.rejection_tree_accept(tree, rows, q, list(range(k)) + [-1], u, 1.0)
+        b = O.rejection_tree_accept(tree, rows, q, list(range(k)) + [-1], u, 1.0, without_replacement=True)
+        assert a == b

@@ -227,3 +227,39 @@ def test_leviathan_never_emits_zero_mass_token():  # vanilla.rs:540-570
         d0 = O.sample_u(q, float(u[2]))
         commits, _, _ = O.rejection_linear_accept([tl, tl], [q], [d0], [float(x) for x in u[:2]], 1.0)
         assert commits[0] < 2
+
+
+# ---- commit composition with EOS (eagle.rs:664-732, eagle3.rs:758-782) ---------------
+def _eos_tree():
+    # root 5 -> {1: 10, 2: 11}; 1 -> {3: 12, 4: 13}; 3 -> {5: 14}; 2 -> {6: 15}
+    return O.DraftTree([5, 10, 11, 12, 13, 14, 15], [0, 0, 0, 1, 1, 3, 2])
+
+
+def test_commit_without_eos_keeps_path_and_bonus_in_tree():
+    t = _eos_tree()
+    best = [0, 1, 3]
+    com, stop, keep, bn = O.greedy_tree_commit(t, best, 14, eos=[99])
+    assert com == [10, 12, 14] and not stop and bn == 5 and keep == [0, 1, 3, 5]
+    com, stop, keep, bn = O.greedy_tree_commit(t, best, 14, eos=[99], strict=True)
+    assert com == [10, 12, 14] and not stop and bn is None and keep == [0, 1, 3]
+    com, stop, keep, bn = O.greedy_tree_commit(t, best, 77, eos=[])
+    assert com == [10, 12, 77] and keep == [0, 1, 3] and bn is None
+
+
+def test_commit_eos_in_path_truncates_and_skips_bonus():
+    t = _eos_tree()
+    com, stop, keep, bn = O.greedy_tree_commit(t, [0, 1, 3, 5], 40, eos=[12, 1000])
+    assert com == [10, 12] and stop and keep == [0, 1, 3] and bn is None
+    # EOS at the first accepted draft
+    com, stop, keep, bn = O.greedy_tree_commit(t, [0, 1, 3, 5], 40, eos=[10, 14])
+    assert com == [10] and stop and keep == [0, 1] and bn is None
+
+
+def test_commit_eos_bonus_stops_but_keeps_path():
+    t = _eos_tree()
+    # the bonus is EOS and also a child of the deepest node: the path is kept,
+    # the bonus node joins it (no EOS among the path's own tokens)
+    com, stop, keep, bn = O.greedy_tree_commit(t, [0, 1, 3], 14, eos=[14])
+    assert com == [10, 12, 14] and stop and keep == [0, 1, 3, 5] and bn == 5
+    com, stop, keep, bn = O.greedy_tree_commit(t, [0], 11, eos=[11])
+    assert com == [11] and stop and keep == [0, 2] and bn == 2
