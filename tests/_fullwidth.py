@@ -78,10 +78,14 @@ def rel_rows(a, b):
     return np.max(np.abs(a64 - b64), axis=-1) / np.maximum(np.max(np.abs(b64), axis=-1), 1e-30)
 
 
-def argmax_agreement(dev, ora):
+def argmax_agreement(dev, ora, max_near_frac=0.5):
     """Rows whose oracle top-2 margin exceeds twice the row's largest
-    device/oracle difference must have the same first-max argmax.  Returns
-    the indices of the rows that are nearer a tie than that."""
+    device/oracle difference must have the same first-max argmax; rows
+    nearer a tie than that may legitimately differ.  The near-tie rows are
+    returned, reported, and bounded: random-init rows over a large
+    vocabulary are nearly flat (the top-2 gap of ~1e5 Gaussian logits is a
+    few percent of their spread), so a fraction of rows is expected there,
+    but at least half of the rows (and at least one) must be checked."""
     near = []
     for i in range(dev.shape[0]):
         s = np.sort(ora[i].astype(np.float64))[::-1]
@@ -90,6 +94,10 @@ def argmax_agreement(dev, ora):
             assert O.argmax_fold(dev[i]) == O.argmax_fold(ora[i]), i
         else:
             near.append(i)
+    n = dev.shape[0]
+    print(f"argmax: {n - len(near)} of {n} rows checked, near ties {near}")
+    need = int(np.ceil((1.0 - max_near_frac) * n))
+    assert n - len(near) >= (max(1, need) if max_near_frac < 1.0 else need), (near, n)
     return near
 
 

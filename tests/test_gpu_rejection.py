@@ -76,7 +76,7 @@ def _walk64(tree, rows, q_rows, q_row_of, u, T, mask=None, max_commit=None, flip
         cdf = np.cumsum(p) / p.sum()
         t = float(u[used])
         tok = int(min(np.searchsorted(cdf, t, side="right"), len(cdf) - 1))
-        return path, tok, margin, t, cdf
+        return path, tok, margins, t, cdf
 
 
 def _draw_ok(tok, tok64, t, cdf, draw_eps):
