@@ -83,6 +83,9 @@ sd_status sd_model_create(const sd_config *cfg, sd_model **out) {
         auto h = std::make_unique<sd_model>();
         h->model = std::make_unique<sd::Model>(c);
         h->dec = std::make_unique<sd::Decoder>(h->model.get());
+        // set-up of the allocation-free entry points: this device's scratch
+        // address, resolved while the device is current (Model set it)
+        sd::noalloc_scratch(c.device);
         *out = h.release();
     });
 }
@@ -214,6 +217,20 @@ sd_status sd_model_qmatmul(sd_model *m, int32_t layer, int32_t kind, const float
         need(m);
         if (!x || !y) throw sd::ArgError("null argument");
         m->model->qmatmul(layer, kind, x, (int)rows, y);
+    });
+}
+
+sd_status sd_model_qmatmul_noalloc(sd_model *m, int32_t layer, int32_t kind, const float *x_dev, size_t rows,
+                                   float *y_dev, void *stream) {
+    return guard([&] {
+        need(m);
+        if (!x_dev || !y_dev) throw sd::ArgError("null argument");
+        if (rows < 1 || rows > 128) throw sd::ArgError("rows must be in [1, 128]");
+        setdev(m);
+        // resolved at sd_model_create for this device; a kept pointer, no allocation
+        void *scr = sd::noalloc_scratch(m->model->cfg.device);
+        m->model->qmatmul_into(layer, kind, x_dev, (int)rows, y_dev, (hipStream_t)stream, scr,
+                               sd::kNoAllocScratchBytes);
     });
 }
 

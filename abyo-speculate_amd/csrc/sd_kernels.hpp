@@ -11,6 +11,13 @@ struct BackendError : std::runtime_error {
     explicit BackendError(const std::string &m) : std::runtime_error(m) {}
 };
 
+// ---- sd_noalloc.hip: scratch of the allocation-free entry points ----
+// Device address of this GPU's file-scope scratch array (kNoAllocScratchBytes),
+// resolved with hipGetSymbolAddress on the first call for `device`, which must
+// be the current device; later calls return the kept address.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+void *noalloc_scratch(int device);
+
 // ---- sd_synth.hip ----
 void launch_synth_quant(int fmt, uint8_t *out, int64_t rows, int64_t K, uint64_t seed, float mult, hipStream_t st);
 void launch_synth_f32(float *out, int64_t n, uint64_t seed, float mult, hipStream_t st);

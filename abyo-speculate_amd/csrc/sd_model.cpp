@@ -429,6 +429,28 @@ void Model::qmatmul(int layer, int kind, const float *x, int M, float *y) {
     hipFree(dxp);
 }
 
+void Model::qmatmul_into(int layer, int kind, const float *x_dev, int M, float *y_dev, hipStream_t stream,
+                         void *staging, size_t staging_bytes) {
+    DevTensor &t = slot(*this, layer, kind);
+    if (!t.set() || t.fmt == F32) throw ArgError("qmatmul needs a quantised matrix tensor");
+    if (M < 1 || M > 128) throw ArgError("rows must be in [1, 128]");
+    if ((size_t)M * t.K * 2 > staging_bytes)
+        throw ArgError("rows * K * 2 = " + std::to_string((size_t)M * t.K * 2) + " bytes of staged activations exceed the " +
+                       std::to_string(staging_bytes) + "-byte scratch");
+    hipStream_t s = stream ? stream : st;
+    launch_to_frag16(x_dev, M, t.K, (uint16_t *)staging, t.K, s);
+    GemmParams p{};  // allow_split = 0: no split-K partials
+    p.seg[0] = seg_of(t, 0, y_dev, t.rows, 0, nullptr);
+    p.nseg = 1;
+    p.ntiles = t.rows / 16;
+    p.xp = (const uint16_t *)staging;
+    p.K = t.K;
+    p.M = M;
+    p.mode = GM_STORE;
+    launch_qgemm(p, s);
+    SD_HIP_CHECK(hipGetLastError());
+}
+
 // Times `iters` back-to-back launches of one dequant-matmul with HIP events on
 // the model's stream (activations: whatever the work buffers hold).  kind is a
 // matrix kind, or BENCH_QKV / BENCH_GATE_UP for the fused launches of a layer.

@@ -102,6 +102,11 @@ class Model {
 
     // raw matmul (test entry): y[M][N] = x[M][K] . W^T (x rounded to fp16)
     void qmatmul(int layer, int kind, const float *x, int M, float *y);
+    // the same product on device buffers, enqueued on `stream` (the model's
+    // own stream when null), with the fp16 activations staged in `staging`
+    // (staging_bytes >= M * K * 2); allocates nothing and does not wait
+    void qmatmul_into(int layer, int kind, const float *x_dev, int M, float *y_dev, hipStream_t stream,
+                      void *staging, size_t staging_bytes);
     // microbenchmark of one dequant-matmul launch: microseconds per launch
     enum { BENCH_QKV = 100, BENCH_GATE_UP = 101, BENCH_ALL_LAYERS = -2 };
     double bench_qmatmul(int layer, int kind, int M, int iters, double *bytes_out);

@@ -267,6 +267,19 @@ sd_status sd_profile_enable(sd_model *m, int32_t on);
  * entries written. */
 size_t sd_profile_read(sd_model *m, int32_t *cls, double *bytes, float *ms, size_t cap);
 sd_status sd_synchronize(sd_model *m);
+/* sd_model_qmatmul without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  x_dev [rows][K]
+ * f32 and y_dev [rows][N] f32 are device buffers owned by the caller; the
+ * fp16 activations are staged in a scratch array that every GPU the library
+ * runs on holds once, 4 MiB (rows * K * 2 bytes must fit: SD_ERR_ARG beyond;
+ * rows <= 128).  The call enqueues on `stream` (a hipStream_t; NULL = the
+ * handle's own stream) and returns without waiting.  All calls on one GPU
+ * share its scratch: calls that overlap on one GPU (other streams, other
+ * threads, other handles on that GPU) race, so serialise them. */
+sd_status sd_model_qmatmul_noalloc(sd_model *m, int32_t layer, int32_t kind, const float *x_dev, size_t rows,
+                                   float *y_dev, void *stream);
+
 /* Microbenchmark of one dequant-matmul launch of layer `layer`: kind is a
  * matrix kind, SD_BENCH_QKV (fused Q/K/V) or SD_BENCH_GATE_UP (fused gate/up +
  * SiLU), at `rows` activation rows; *us = mean microseconds per launch over
