@@ -21,8 +21,10 @@
 // Grid (kv head, key split, query tile).  A workgroup's 4 waves take 4
 // consecutive key ranges of keys_per_wave keys and one query tile (16 of the
 // n_rep query heads of the KV head times the M tokens); their partial softmax
-// states are merged in LDS in a fixed order, and the splits by a combine
-// kernel (skipped when one split covers all keys).  Up to 16 tokens,
+// states are merged in LDS in a fixed order, and the splits by the last
+// workgroup of the tile to finish (up to 16 tokens; a counter per tile, device-
+// scope partials) or by a combine kernel (more tokens), with the same
+// arithmetic; nothing to merge when one split covers all keys.  Up to 16 tokens,
 // keys_per_wave and the split boundaries depend on P only, so a query's
 // result does not depend on how many other queries share the call.
 #include <mutex>
@@ -316,11 +318,22 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
     step_pv<HD, QT>(S, b.v, bp, alpha, moved, tl);
 }
 
+// Device-scope (sc1) 8-byte accesses, for data that workgroups of one launch
+// hand to each other: a store is visible, and a load fresh, across the XCDs'
+// separate L2 caches without writing back or invalidating those caches.
+__device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const void *p) {
+    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Result of one query (lane (r16, g) holds d = dt*16 + 4g + i): with one
 // split the normalised row goes straight into the wo input (fp16, fragment
-// order); otherwise o / l as fp16 and (m, l) for the combine kernel, which
-// weighs split s by l_s * exp2(m_s - max m).
-template <int HD>
+// order); otherwise o / l as fp16 and (m, l) for the merge of the splits,
+// which weighs split s by l_s * exp2(m_s - max m).  DEV: the partials are
+// stored at device scope, for a merge inside the same launch.
+template <int HD, bool DEV = false>
 __device__ __forceinline__ void attn_emit(const AttnParams &p, int s, int head, int m, int g,
                                           const floatx4 (&o)[HD / 16], float mq, float l) {
     const float inv = 1.0f / l;
@@ -339,13 +352,71 @@ __device__ __forceinline__ void attn_emit(const AttnParams &p, int s, int head, 
 #pragma unroll
     for (int dt = 0; dt < HD / 16; dt++) {
         const float w = l > 0.f ? inv : 0.f;  // a query that saw no key of this split has l = 0
-        *(uintx2 *)(po + dt * 16 + 4 * g) =
-            uintx2{(uint32_t)f2h(o[dt][0] * w) | ((uint32_t)f2h(o[dt][1] * w) << 16),
-                   (uint32_t)f2h(o[dt][2] * w) | ((uint32_t)f2h(o[dt][3] * w) << 16)};
+        const uintx2 v{(uint32_t)f2h(o[dt][0] * w) | ((uint32_t)f2h(o[dt][1] * w) << 16),
+                       (uint32_t)f2h(o[dt][2] * w) | ((uint32_t)f2h(o[dt][3] * w) << 16)};
+        if constexpr (DEV) st_dev64(po + dt * 16 + 4 * g, (uint64_t)v.x | ((uint64_t)v.y << 32));
+        else *(uintx2 *)(po + dt * 16 + 4 * g) = v;
     }
     if (g == 0) {
-        p.part_ml[2 * pi] = mq;
-        p.part_ml[2 * pi + 1] = l;
+        if constexpr (DEV) {
+            st_dev64(p.part_ml + 2 * pi, (uint64_t)__float_as_uint(mq) | ((uint64_t)__float_as_uint(l) << 32));
+        } else {
+            p.part_ml[2 * pi] = mq;
+            p.part_ml[2 * pi + 1] = l;
+        }
+    }
+}
+
+// Merge of the splits by the last workgroup of a (KV head h, query tile qg)
+// to finish: thread (r = tid / 16, c = tid % 16) owns query qg * 16 + r and
+// dims [c HD/16, +HD/16).  The arithmetic, and its order, is k_attn_combine's:
+// out = sum_s w_s o_s / sum_s w_s in split order, w_s = l_s exp2(m_s - max m).
+constexpr int kFusedMaxSplits = 64;
+template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnParams &p, int h, int qg) {
+    constexpr int DPT = HD / 16;  // dims per thread, 4 or 8: one or two 8-byte loads per split
+    __shared__ float cml[16][kFusedMaxSplits][2];
+    const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
+    const int nq = p.M * p.n_rep, ns = p.nsplit;
+    const int q = qg * 16 + r;
+    const bool live = q < nq;
+    const int head = h * p.n_rep + (live ? q % p.n_rep : 0), m = live ? q / p.n_rep : 0;
+    const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
+    const int64_t pi0 = (int64_t)head * p.M + m;
+    for (int s = c; s < ns; s += 16) {
+        const uint64_t v = live ? ld_dev64(p.part_ml + 2 * (pi0 + s * stride)) : 0ull;
+        cml[r][s][0] = __uint_as_float((uint32_t)v);
+        cml[r][s][1] = __uint_as_float((uint32_t)(v >> 32));
+    }
+    __syncthreads();
+    if (!live) return;
+    float mx = -INFINITY;
+    for (int s = 0; s < ns; s++) mx = fmaxf(mx, cml[r][s][0]);
+    const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
+    float W = 0.f, acc[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; i++) acc[i] = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        // 8 splits' pieces requested at once
+        uint64_t ov[8][DPT / 4];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int k = 0; k < DPT / 4; k++) ov[j][k] = s0 + j < ns ? ld_dev64(po + (s0 + j) * stride * HD + 4 * k) : 0ull;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (s0 + j < ns) {
+                const float ms = cml[r][s0 + j][0];
+                const float w = ms == -INFINITY ? 0.f : cml[r][s0 + j][1] * exp2f(ms - mx);
+                W += w;
+#pragma unroll
+                for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DPT; i++) {
+        const int64_t k = (int64_t)head * HD + c * DPT + i;
+        p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc[i] / W);
     }
 }
 
@@ -441,17 +512,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int dt = 0; dt < NDT; dt++) sob[0][t][dt][lane] = S.o[t][dt];
     }
     __syncthreads();
-    if (wave != 0) return;
-
+    const bool fused = p.fused_combine != 0;
+    if (wave == 0) {
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
-        const int q = (qg * QT + t) * 16 + r16;
-        if (q >= nq) continue;
-        floatx4 y[NDT];
+        for (int t = 0; t < QT; t++) {
+            const int q = (qg * QT + t) * 16 + r16;
+            if (q >= nq) continue;
+            floatx4 y[NDT];
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] + sob[0][t][dt][lane];
-        attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
+            for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] + sob[0][t][dt][lane];
+            if (fused) attn_emit<HD, true>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
+            else attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
+        }
     }
+    if (!fused) return;
+
+    // ---- the last of the tile's nsplit workgroups to arrive merges the splits ----
+    // Wave 0 wrote the partials (device scope) and waits for those stores to
+    // complete before it counts the arrival; the last arrival resets the count
+    // for the next launch and reads every split's partials at device scope.
+    __shared__ int s_last;
+    if (wave == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0) {
+            int *cnt = p.split_cnt + (int64_t)h * gridDim.z + qg;
+            const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.nsplit - 1;
+            if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+    }
+    __syncthreads();
+    if (!s_last) return;
+    static_assert(QT == 1, "the merge covers one 16-query tile per workgroup");
+    attn_merge_tile<HD>(p, h, qg);
 }
 
 // ---- many queries (tree verify): query tiles across waves, keys shared in LDS ----
@@ -753,6 +846,12 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
         if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(256 * kTKS), attn_t_lds<128>(), st, p);
         else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(256 * kTKS), attn_t_lds<64>(), st, p);
     } else {
+        AttnParams a = p;
+        a.fused_combine = 0;
+        if (p.nsplit > 1 && p.split_cnt) {
+            if ((int64_t)p.n_kv * nqt > p.split_cnt_len) throw BackendError("attention: split counters too few");
+            a.fused_combine = p.nsplit <= kFusedMaxSplits;
+        }
         // One query tile per wave keeps a wave within 256 registers (two
         // double-buffered 32-key operand sets and its accumulators), so two
         // waves share each SIMD.  Query tiles become workgroups along z; with the
@@ -760,8 +859,9 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
         // workgroup of one head lands on the same XCD, so the query tiles re-read
         // that head's keys from its L2.
         const dim3 grid(p.n_kv, p.nsplit, nqt);
-        if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, p);
+        if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, a);
+        if (a.fused_combine) return;
     }
     if (p.nsplit > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p);
 }

@@ -44,6 +44,14 @@ struct AttnParams {
     float *part_ml;        // [nsplit][n_heads][M][2]
     uint16_t *out16;       // [M][out_ld] fp16 fragment layout (input of wo)
     int out_ld;
+    // Up to 16 rows with several splits: per-(KV head, query tile) arrival
+    // counts, zero between launches, through which the last split of a tile
+    // merges the splits inside the attention kernel (no combine launch).
+    // Null: the combine kernel runs.  Launches sharing one array must not
+    // overlap.
+    int *split_cnt;
+    int split_cnt_len;
+    int fused_combine;     // set by launch_attention
 };
 
 void launch_rope_kv(const RopeKvParams &p, hipStream_t st);

@@ -78,7 +78,7 @@ Model::~Model() {
                     (void *)d_src, (void *)xp, (void *)ap, (void *)act, (void *)q16,
                     (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
-                    (void *)aux_ids, (void *)ssq})
+                    (void *)aux_ids, (void *)ssq, (void *)split_cnt})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -120,6 +120,7 @@ void Model::alloc_buffers() {
     nsplit_max = attn_max_splits(c.n_kv_heads);
     part_o = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * c.head_dim);
     part_ml = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * 2);
+    split_cnt = dalloc<int>(c.n_heads);  // n_kv x (query tiles <= n_rep up to 16 rows), zero
     logits = dalloc<float>((size_t)Mx * c.vocab);
     hidden_out = dalloc<float>((size_t)Mx * c.hidden);
     last_row = dalloc<float>((size_t)c.vocab);
@@ -661,6 +662,8 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
             a.part_o = part_o;
             a.part_ml = part_ml;
+            a.split_cnt = split_cnt;
+            a.split_cnt_len = c.n_heads;
             a.out16 = ap;
             a.out_ld = ap_ld;
             if (prof_on) {

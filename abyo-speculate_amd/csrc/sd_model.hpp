@@ -137,6 +137,7 @@ class Model {
     float *cos_t = nullptr, *sin_t = nullptr;
     float *h = nullptr, *qkv = nullptr, *logits = nullptr, *hidden_out = nullptr, *last_row = nullptr;
     float *part_o = nullptr, *part_ml = nullptr, *amax_v = nullptr, *collect_buf = nullptr;
+    int *split_cnt = nullptr;  // attention's per-tile split arrival counts (zero between launches)
     int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
     uint64_t *d_mask = nullptr;
     // split-K partial sums of the M > 16 matmul (see GemmParams::allow_split)
