@@ -30,10 +30,11 @@
 // its precondition on the siblings holds; deterministic top-k siblings meet
 // neither.
 //
-// Sums here are parallel (per-thread sequential chunks, then a fixed-order
-// tree), so they can differ from the reference's sequential f32 sums in the
-// last bits; a decision can only differ when u lies within a few ulps of a
-// threshold.
+// The rows' softmax statistics and distributions are computed across the
+// GPU; the walk, one workgroup, then reads the distributions.  Sums here are
+// parallel (fixed-order trees over slices, tiles and lanes), so they can
+// differ from the reference's sequential f32 sums in the last bits; a
+// decision can only differ when u lies within a few ulps of a threshold.
 #include "sd_common.hpp"
 #include "sd_kernels_accept.hpp"
 
@@ -41,20 +42,64 @@ namespace sd {
 
 #pragma clang fp contract(off)
 
-// ---- per-row softmax statistics --------------------------------------------
-// grid rows, block 1024.  Online (max, sum of exp((l - max) * inv_t)) per
-// thread over a strided walk, merged in a fixed order.  Entries unreachable
-// through the t2d map (t2d_inv[x] < 0) count as -inf (mask_target_logits,
-// eagle3.rs:498-513).  Also the first-max argmax (greedy one-hot).
-__global__ __launch_bounds__(1024) void k_row_stats(const float *logits, int64_t ld, int V, float inv_t,
-                                                   const int *t2d_inv, float *row_m, float *row_s, int *row_am) {
-    const int r = blockIdx.x, t = threadIdx.x;
+// ---- per-row softmax statistics ----------------------------------------------
+// grid (rows, slices of kSlice entries), block kRsT.  Online (max, sum of
+// exp((l - max) * inv_t)) per thread over a strided walk of the slice, merged
+// in a fixed tree; the slices' states are merged in slice order by the last
+// workgroup of the row to finish (a per-row arrival count, device-scope
+// partials).  Entries unreachable through the t2d map (t2d_inv[x] < 0) count
+// as -inf (mask_target_logits, eagle3.rs:498-513).  Also the first-max argmax
+// (greedy one-hot).
+constexpr int kRsT = 256, kSlice = 8192;
+
+__device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const void *p) {
+    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t pack2(float a, uint32_t b) { return (uint64_t)__float_as_uint(a) | ((uint64_t)b << 32); }
+
+// (m1, s1) + (m2, s2) of the online softmax sum
+__device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s2, float inv_t) {
+    const float M = fmaxf(m1, m2);
+    float S = 0.f;
+    if (M > -INFINITY)
+        S = (m1 > -INFINITY ? s1 * expf((m1 - M) * inv_t) : 0.f) + (m2 > -INFINITY ? s2 * expf((m2 - M) * inv_t) : 0.f);
+    m1 = M;
+    s1 = S;
+}
+constexpr int kNoIdx = 0x7fffffff;
+// the earlier of two first-max candidates (i2 from the later range on ties)
+__device__ __forceinline__ void am_merge(float &v1, int &i1, float v2, int i2) {
+    if (i2 != kNoIdx && (i1 == kNoIdx || v2 > v1 || (v2 == v1 && i2 < i1))) {
+        v1 = v2;
+        i1 = i2;
+    }
+}
+
+__global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t ld, int V, float inv_t,
+                                                   const int *t2d_inv, uint64_t *part, int *cnt, float *row_m,
+                                                   float *row_s, int *row_am) {
+    const int r = blockIdx.x, sl = blockIdx.y, nsl = gridDim.y, t = threadIdx.x;
     const float *row = logits + (int64_t)r * ld;
+    const int x1 = min(V, (sl + 1) * kSlice);
     float m = -INFINITY, s = 0.f, bv = -INFINITY;
-    int bi = 0x7fffffff, bad = 0;
-    for (int x = t; x < V; x += 1024) {
-        float l = row[x];
-        if (t2d_inv && t2d_inv[x] < 0) l = -INFINITY;
+    int bi = kNoIdx, bad = 0;
+    // the thread's kPer entries x = slice start + t + kRsT i, all requested at once
+    constexpr int kPer = kSlice / kRsT;
+    float lv[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int x = sl * kSlice + t + kRsT * i;
+        lv[i] = x < x1 ? row[x] : -INFINITY;
+        if (t2d_inv && x < x1 && t2d_inv[x] < 0) lv[i] = -INFINITY;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int x = sl * kSlice + t + kRsT * i;
+        if (x >= x1) break;
+        const float l = lv[i];
         // a NaN or +inf entry makes the reference's sum non-finite (an error there)
         if (l != l || l == INFINITY) bad = 1;
         if (l > bv) {  // strictly greater: first max per thread (x increases)
@@ -68,49 +113,107 @@ __global__ __launch_bounds__(1024) void k_row_stats(const float *logits, int64_t
             s += expf((l - m) * inv_t);
         }
     }
-    __shared__ float sm[1024], ss[1024], sv[1024];
-    __shared__ int si[1024];
+    __shared__ float sm[kRsT], ss[kRsT], sv[kRsT];
+    __shared__ int si[kRsT];
+    __shared__ int s_last;
     const bool any_bad = __syncthreads_or(bad) != 0;
     sm[t] = m;
     ss[t] = s;
     sv[t] = bv;
     si[t] = bi;
     __syncthreads();
-    for (int o = 512; o > 0; o >>= 1) {
+    for (int o = kRsT / 2; o > 0; o >>= 1) {
         if (t < o) {
-            const float m1 = sm[t], m2 = sm[t + o];
-            const float M = fmaxf(m1, m2);
-            float S = 0.f;
-            if (M > -INFINITY) {
-                S = (m1 > -INFINITY ? ss[t] * expf((m1 - M) * inv_t) : 0.f) +
-                    (m2 > -INFINITY ? ss[t + o] * expf((m2 - M) * inv_t) : 0.f);
-            }
-            sm[t] = M;
-            ss[t] = S;
-            const float v2 = sv[t + o];
-            const int i2 = si[t + o];
-            if (i2 != 0x7fffffff && (v2 > sv[t] || (v2 == sv[t] && i2 < si[t]) || si[t] == 0x7fffffff)) {
-                sv[t] = v2;
-                si[t] = i2;
-            }
+            float m1 = sm[t], s1 = ss[t], v1 = sv[t];
+            int i1 = si[t];
+            ms_merge(m1, s1, sm[t + o], ss[t + o], inv_t);
+            am_merge(v1, i1, sv[t + o], si[t + o]);
+            sm[t] = m1;
+            ss[t] = s1;
+            sv[t] = v1;
+            si[t] = i1;
         }
         __syncthreads();
     }
     if (t == 0) {
-        row_m[r] = sm[0];
-        row_s[r] = any_bad ? NAN : ss[0];
-        row_am[r] = si[0] == 0x7fffffff ? 0 : si[0];
+        uint64_t *pp = part + ((int64_t)r * nsl + sl) * 2;
+        st_dev64(pp, pack2(sm[0], __float_as_uint(any_bad ? NAN : ss[0])));
+        st_dev64(pp + 1, pack2(sv[0], (uint32_t)si[0]));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partials are stored before the count
+        const int last = __hip_atomic_fetch_add(cnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsl - 1;
+        if (last) __hip_atomic_store(cnt + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // the row's slices, in slice order
+    if (t < nsl) {
+        const uint64_t a = ld_dev64(part + ((int64_t)r * nsl + t) * 2);
+        const uint64_t b = ld_dev64(part + ((int64_t)r * nsl + t) * 2 + 1);
+        sm[t] = __uint_as_float((uint32_t)a);
+        ss[t] = __uint_as_float((uint32_t)(a >> 32));
+        sv[t] = __uint_as_float((uint32_t)b);
+        si[t] = (int)(uint32_t)(b >> 32);
+    }
+    __syncthreads();
+    if (t == 0) {
+        float M = sm[0], S = ss[0], v = sv[0];
+        int i = si[0];
+        bool nan = S != S;
+        for (int k = 1; k < nsl; k++) {
+            nan = nan || ss[k] != ss[k];
+            ms_merge(M, S, sm[k], ss[k], inv_t);
+            am_merge(v, i, sv[k], si[k]);
+        }
+        row_m[r] = M;
+        row_s[r] = nan ? NAN : S;
+        row_am[r] = i == kNoIdx ? 0 : i;
+    }
+}
+
+// ---- the rows as distributions ----------------------------------------------
+// grid (rows, slices), block kRsT: prob[r][x] = softmax_with_temperature's
+// value (tokens.rs:15-55), 0 where the t2d map masks x; at T = 0 the one-hot
+// of the first max.
+__global__ __launch_bounds__(kRsT) void k_row_prob(const float *logits, int64_t ld, int V, float inv_t, int greedy,
+                                                  const int *t2d_inv, const float *row_m, const float *row_s,
+                                                  const int *row_am, float *prob) {
+    const int r = blockIdx.x, sl = blockIdx.y;
+    const float *row = logits + (int64_t)r * ld;
+    float *out = prob + (int64_t)r * V;
+    const float m = row_m[r], S = row_s[r];
+    const int am = row_am[r];
+    const int x1 = min(V, (sl + 1) * kSlice);
+    constexpr int kPer = kSlice / kRsT;
+    float lv[kPer];
+    bool live[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int x = sl * kSlice + threadIdx.x + kRsT * i;
+        live[i] = x < x1 && !(t2d_inv && t2d_inv[x] < 0);
+        lv[i] = live[i] && !greedy ? row[x] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int x = sl * kSlice + threadIdx.x + kRsT * i;
+        if (x >= x1) break;
+        float p;
+        if (!live[i]) p = 0.f;
+        else if (greedy) p = x == am ? 1.f : 0.f;
+        else p = expf((lv[i] - m) * inv_t) / S;
+        out[x] = p;
     }
 }
 
 // ---- the walk ----------------------------------------------------------------
-constexpr int WT = 1024;  // threads of the walk kernel
+constexpr int WT = 1024;       // threads of the walk kernel (16 waves)
+constexpr int kTile = 256;     // entries per tile: lane l of a wave holds x = 256 tile + l + 64 j, j < 4
+constexpr int kMaxTiles = 1024;  // vocabularies up to 262144
 constexpr int MAX_REJ = 16;
 
 struct WalkShared {
-    float red[WT];
-    float scan[WT];
-    int first[WT];
+    float tsum[kMaxTiles];  // per-tile sums of the last pass
+    float total;
     float Z[MAX_REJ];  // normalisers of the successive adjusted distributions at the current node
     float R[MAX_REJ];  // without replacement: the mass of q left before rejection r (R[0] = 1)
     int rej[MAX_REJ];  // without replacement: the rejected tokens at the current node
@@ -128,58 +231,135 @@ __device__ __forceinline__ float walk_q(const AcceptParams &a, const WalkShared 
     return W.R[r] > 0.f ? q0 / W.R[r] : 0.f;
 }
 
-// probability of x at `node` after `krej` rejections there
-__device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared &W, int node, int krej, int x) {
-    const float *row = a.logits + (int64_t)node * a.ld;
-    float p;
-    if (a.t2d_inv && a.t2d_inv[x] < 0) {
-        p = 0.f;
-    } else if (a.greedy) {
-        p = x == a.row_am[node] ? 1.f : 0.f;
-    } else {
-        p = expf((row[x] - a.row_m[node]) * a.inv_t) / a.row_s[node];
-    }
-    if (krej > 0) {
-        const int qr = a.q_row_of[node];
-        const float q0 = accept_q(a, qr, x);
-        for (int r = 0; r < krej; r++) p = fmaxf(p - walk_q(a, W, q0, r, x), 0.f) / W.Z[r];
-    }
+// probability of x after `krej` rejections at a node whose distribution is p0
+// (its prob row's entry) and whose draft row holds q0 = q(x)
+__device__ __forceinline__ float walk_val(const AcceptParams &a, const WalkShared &W, int krej, float p0, float q0,
+                                          int x) {
+    float p = p0;
+    for (int r = 0; r < krej; r++) p = fmaxf(p - walk_q(a, W, q0, r, x), 0.f) / W.Z[r];
     return p;
 }
+// the normaliser term of the adjusted distribution after rejection krej
+__device__ __forceinline__ float walk_adj(const AcceptParams &a, const WalkShared &W, int krej, float p0, float q0,
+                                          int x) {
+    return fmaxf(walk_val(a, W, krej, p0, q0, x) - walk_q(a, W, q0, krej, x), 0.f);
+}
+__device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared &W, int node, int krej, int x) {
+    const float p0 = a.prob[(int64_t)node * a.V + x];
+    return walk_val(a, W, krej, p0, krej > 0 ? accept_q(a, a.q_row_of[node], x) : 0.f, x);
+}
 
-// Sum over x of f(x) in a fixed order: thread t sums its contiguous chunk,
-// then a fixed tree.  Leaves each thread's chunk sum in W.scan[t] when scan is
-// set (an exclusive prefix over threads, for the CDF walk).
-template <typename F>
-__device__ float block_sum(WalkShared &W, int V, bool scan, F f) {
-    const int t = threadIdx.x;
-    const int chunk = (V + WT - 1) / WT;
-    const int x0 = t * chunk, x1 = min(V, x0 + chunk);
-    float s = 0.f;
-    for (int x = x0; x < x1; x++) s += f(x);
-    W.red[t] = s;
-    if (scan) W.scan[t] = s;
-    __syncthreads();
-    for (int o = WT / 2; o > 0; o >>= 1) {
-        if (t < o) W.red[t] = W.red[t] + W.red[t + o];
-        __syncthreads();
+// a wave's 64 values summed in a fixed order, lane 0's result
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return __shfl(v, 0);
+}
+// inclusive prefix over the wave's lanes
+__device__ __forceinline__ float wave_scan(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(v, o);
+        if (lane >= o) v += y;
     }
-    const float total = W.red[0];
-    if (scan) {
-        // exclusive prefix over thread chunks, thread order (sequential by
-        // one thread: 1024 adds, no reassociation across chunks)
-        if (t == 0) {
-            float acc = 0.f;
-            for (int i = 0; i < WT; i++) {
-                const float v = W.scan[i];
-                W.scan[i] = acc;
-                acc += v;
+    return v;
+}
+
+// Sum over x < V of the walk's values at `node` in a fixed order: tiles of
+// 256 entries (wave w takes tiles w, w + 16, ...; a lane its 4 entries in
+// order, then the wave's lanes), then the tiles.  zpass: the adjusted
+// distribution's unnormalised terms (walk_adj), else the current
+// distribution (walk_val).  Each wave requests kBatch tiles' entries before
+// it computes any of them.  Leaves the tile sums in W.tsum for walk_search.
+constexpr int kBatch = 8;
+__device__ __forceinline__ float walk_pass(WalkShared &W, const AcceptParams &a, int node, int krej, bool zpass) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int V = a.V, ntiles = (V + kTile - 1) / kTile;
+    const float *prow = a.prob + (int64_t)node * V;
+    const int qr = a.q_row_of[node];
+    const bool needq = zpass || krej > 0;
+    for (int tb = wave; tb < ntiles; tb += (WT / 64) * kBatch) {
+        float p0[kBatch][4], q0[kBatch][4];
+#pragma unroll
+        for (int b = 0; b < kBatch; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int x = (tb + (WT / 64) * b) * kTile + lane + 64 * j;
+                const bool ok = x < V;
+                p0[b][j] = ok ? prow[x] : 0.f;
+                q0[b][j] = ok && needq ? accept_q(a, qr, x) : 0.f;
             }
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int tl = tb + (WT / 64) * b;
+            if (tl >= ntiles) break;
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int x = tl * kTile + lane + 64 * j;
+                if (x < V)
+                    s += zpass ? walk_adj(a, W, krej, p0[b][j], q0[b][j], x) : walk_val(a, W, krej, p0[b][j], q0[b][j], x);
+            }
+            s = wave_sum(s);
+            if (lane == 0) W.tsum[tl] = s;
         }
-        __syncthreads();
     }
     __syncthreads();
-    return total;
+    if (wave == 0) {
+        float s = 0.f;
+        for (int tl = lane; tl < ntiles; tl += 64) s += W.tsum[tl];
+        s = wave_sum(s);
+        if (lane == 0) W.total = s;
+    }
+    __syncthreads();
+    return W.total;
+}
+
+// sample_from_distribution's search (tokens.rs:99-120) after a walk_pass of
+// the same f, by wave 0: the first x with f(x) > 0 whose running sum exceeds
+// target, the running sum taken over the tiles' sums and then entry by entry
+// inside a tile; -1 when none does (the reference's drift case).
+template <typename F> __device__ __forceinline__ int walk_search(const WalkShared &W, int V, float target, F f) {
+    const int lane = threadIdx.x & 63;
+    const int ntiles = (V + kTile - 1) / kTile;
+    const int per = (ntiles + 63) / 64;
+    const int t0 = min(ntiles, lane * per), t1 = min(ntiles, t0 + per);
+    float ls = 0.f;
+    for (int tl = t0; tl < t1; tl++) ls += W.tsum[tl];
+    const float incl = wave_scan(ls);
+    float acc = __shfl_up(incl, 1);
+    if (lane == 0) acc = 0.f;
+    // the lane whose tile range crosses the target: the tile and the sum before it
+    int tile = -1;
+    float before = 0.f;
+    for (int tl = t0; tl < t1; tl++) {
+        const float nx = acc + W.tsum[tl];
+        if (target < nx) {
+            tile = tl;
+            before = acc;
+            break;
+        }
+        acc = nx;
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(tile >= 0);
+    if (hit == 0) return -1;
+    const int src = __builtin_ctzll(hit);
+    tile = __shfl(tile, src);
+    float c = __shfl(before, src);
+    // entry by entry from that tile on (past it only when rounding moved the crossing)
+    for (int tl = tile; tl < ntiles; tl++) {
+#pragma unroll 1
+        for (int j = 0; j < 4; j++) {
+            const int x = tl * kTile + 64 * j + lane;
+            const float v = x < V ? f(x) : 0.f;
+            const float inc = wave_scan(v);
+            const uint64_t b = __builtin_amdgcn_ballot_w64(v > 0.f && target < c + inc);
+            if (b) return tl * kTile + 64 * j + __builtin_ctzll(b);
+            c = c + __shfl(inc, 63);
+        }
+    }
+    return -1;
 }
 
 // grid 1, block 1024
@@ -257,10 +437,7 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                 if (t == 0) W.status = ACC_ERR_ARG;
                 break;
             }
-            const int qr = a.q_row_of[node];
-            const float Z = block_sum(W, a.V, false, [&](int x) {
-                return fmaxf(walk_p(a, W, node, krej, x) - walk_q(a, W, accept_q(a, qr, x), krej, x), 0.f);
-            });
+            const float Z = walk_pass(W, a, node, krej, true);
             if (t == 0) {
                 if (!(Z > 0.f) || !isfinite(Z)) {
                     W.status = ACC_ERR_ADJUSTED;
@@ -274,31 +451,15 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
             continue;
         }
         // go == 1: sample_from_distribution (tokens.rs:99-120) over the current distribution
-        const float sum = block_sum(W, a.V, true, [&](int x) { return walk_p(a, W, node, krej, x); });
+        auto f = [&](int x) { return walk_p(a, W, node, krej, x); };
+        const float sum = walk_pass(W, a, node, krej, false);
         if (!(sum > 0.f) || !isfinite(sum)) {
             if (t == 0) W.status = ACC_ERR_SOFTMAX;
             break;
         }
-        const float target = W.u * sum;
-        {
-            const int chunk = (a.V + WT - 1) / WT;
-            const int x0 = t * chunk, x1 = min(a.V, x0 + chunk);
-            float acc = W.scan[t];
-            int hit = 0x7fffffff;
-            for (int x = x0; x < x1; x++) {
-                acc += walk_p(a, W, node, krej, x);
-                if (target < acc) {
-                    hit = x;
-                    break;
-                }
-            }
-            W.first[t] = hit;
-            __syncthreads();
-            for (int o = WT / 2; o > 0; o >>= 1) {
-                if (t < o) W.first[t] = min(W.first[t], W.first[t + o]);
-                __syncthreads();
-            }
-            if (t == 0) W.fin = W.first[0] == 0x7fffffff ? a.V - 1 : W.first[0];
+        if (t < 64) {
+            const int x = walk_search(W, a.V, W.u * sum, f);
+            if (t == 0) W.fin = x < 0 ? a.V - 1 : x;
         }
         break;
     }
@@ -311,12 +472,18 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     }
 }
 
-void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, const int *t2d_inv, float *row_m,
-                      float *row_s, int *row_am, hipStream_t st) {
-    hipLaunchKernelGGL(k_row_stats, dim3(rows), dim3(1024), 0, st, logits, ld, V, inv_t, t2d_inv, row_m, row_s, row_am);
+void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, int greedy, const int *t2d_inv,
+                      uint64_t *part, int *cnt, float *row_m, float *row_s, int *row_am, float *prob, hipStream_t st) {
+    if (V < 1 || V > kRowStatsMaxSlices * kSlice) throw BackendError("acceptance: vocabulary too large");
+    const dim3 grid(rows, (V + kSlice - 1) / kSlice);
+    hipLaunchKernelGGL(k_row_stats, grid, dim3(kRsT), 0, st, logits, ld, V, inv_t, t2d_inv, part, cnt, row_m, row_s,
+                       row_am);
+    hipLaunchKernelGGL(k_row_prob, grid, dim3(kRsT), 0, st, logits, ld, V, inv_t, greedy, t2d_inv, row_m, row_s,
+                       row_am, prob);
 }
 
 void launch_accept_walk(const AcceptParams &a, hipStream_t st) {
+    if (a.V > kMaxTiles * kTile) throw BackendError("acceptance: vocabulary too large");
     hipLaunchKernelGGL(k_accept_walk, dim3(1), dim3(WT), 0, st, a);
 }
 

@@ -419,6 +419,20 @@ sd_status sd_verify_rejection_linear(sd_model *m, const uint32_t *drafts, size_t
     });
 }
 
+sd_status sd_verify_rejection_linear_device_q(sd_model *m, const uint32_t *drafts, size_t k, const float *q_rows_dev,
+                                              const float *uniforms, size_t n_uniforms, float temperature,
+                                              size_t max_commit, uint32_t *commits, size_t *n_commit,
+                                              size_t *n_accepted, size_t *n_used) {
+    return guard([&] {
+        need_weights(m);
+        if ((k && (!drafts || !q_rows_dev)) || !uniforms || !commits || !n_commit || !n_accepted || !n_used)
+            throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_rejection_linear(drafts, k, q_rows_dev, uniforms, n_uniforms, temperature, max_commit, commits,
+                                        n_commit, n_accepted, n_used, true);
+    });
+}
+
 sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                    const float *q_rows, size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
                                    const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
@@ -432,6 +446,23 @@ sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const ui
         setdev(m);
         m->dec->verify_rejection_tree(tokens, parents, n, q_rows, q_rows_n, q_vocab, q_row_of, uniforms, n_uniforms,
                                       temperature, use_t2d, siblings, max_commit, path, path_len, token, n_used);
+    });
+}
+
+sd_status sd_verify_rejection_tree_device_q(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                            const float *q_rows_dev, size_t q_rows_n, size_t q_vocab,
+                                            const int32_t *q_row_of, const float *uniforms, size_t n_uniforms,
+                                            float temperature, int32_t use_t2d, int32_t siblings, size_t max_commit,
+                                            uint32_t *path, size_t *path_len, int32_t *token, size_t *n_used) {
+    return guard([&] {
+        need_weights(m);
+        if (!tokens || !parents || !q_row_of || !uniforms || !path || !path_len || !token || !n_used ||
+            (q_rows_n && !q_rows_dev))
+            throw sd::ArgError("null argument");
+        setdev(m);
+        m->dec->verify_rejection_tree(tokens, parents, n, q_rows_dev, q_rows_n, q_vocab, q_row_of, uniforms,
+                                      n_uniforms, temperature, use_t2d, siblings, max_commit, path, path_len, token,
+                                      n_used, true);
     });
 }
 

@@ -8,8 +8,7 @@ namespace sd {
 enum AcceptStatus : int { ACC_OK = 0, ACC_ERR_SOFTMAX = 1, ACC_ERR_ADJUSTED = 2, ACC_ERR_ARG = 3 };
 
 struct AcceptParams {
-    const float *logits;   // [n][ld] verify rows, row i = tree node i
-    int64_t ld;
+    const float *prob;     // [n][V] the verify rows as distributions (k_row_prob), row i = tree node i
     int V;                 // target vocabulary
     int n;                 // tree nodes (a chain for the linear walk)
     const int *parents;    // [n], parents[0] unused
@@ -40,8 +39,12 @@ __device__ __forceinline__ float accept_q(const AcceptParams &a, int qr, int x) 
     return a.q[(int64_t)qr * a.q_ld + x];
 }
 
-void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, const int *t2d_inv, float *row_m,
-                      float *row_s, int *row_am, hipStream_t st);
+// Softmax statistics (max, sum, first-max argmax) of `rows` logits rows and
+// the rows as distributions into prob [rows][V].  part: kRowStatsMaxSlices x 2
+// words per row; cnt: one zeroed int per row (left zeroed).
+constexpr int kRowStatsMaxSlices = 32;
+void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, int greedy, const int *t2d_inv,
+                      uint64_t *part, int *cnt, float *row_m, float *row_s, int *row_am, float *prob, hipStream_t st);
 void launch_accept_walk(const AcceptParams &a, hipStream_t st);
 
 }  // namespace sd

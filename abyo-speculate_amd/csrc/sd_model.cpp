@@ -78,7 +78,8 @@ Model::~Model() {
                     (void *)d_src, (void *)xp, (void *)ap, (void *)act, (void *)q16,
                     (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
-                    (void *)aux_ids, (void *)ssq, (void *)split_cnt})
+                    (void *)aux_ids, (void *)ssq, (void *)split_cnt, (void *)acc_part, (void *)acc_cnt,
+                    (void *)acc_prob})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -144,6 +145,8 @@ void Model::alloc_buffers() {
     acc_u = dalloc<float>(Mx);
     acc_tree = dalloc<int>((size_t)3 * Mx);
     acc_out = dalloc<int>((size_t)Mx + 4);
+    acc_part = dalloc<uint64_t>((size_t)Mx * 2 * kRowStatsMaxSlices);
+    acc_cnt = dalloc<int>(Mx);
     aux_h = dalloc<float>((size_t)kAuxRows * c.hidden);
     aux_x = dalloc<uint16_t>((size_t)(kAuxRows + 16) * c.hidden);
     aux_y = dalloc<float>((size_t)kAuxRows * c.vocab);
@@ -1277,19 +1280,43 @@ void Decoder::set_d2t(const int64_t *d2t, size_t n) {
     m.d2t_draft_vocab = (int)n;
 }
 
-void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
-                          size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature,
-                          int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used) {
+// Draft rows the caller already holds in device memory: they must be device
+// (or device-accessible managed) memory of this model's GPU.
+static void check_device_rows(const Model &m, const float *q, size_t n) {
+    if (n == 0) return;
+    if (!q) throw ArgError("draft rows: null device pointer");
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, q) != hipSuccess) {
+        (void)hipGetLastError();
+        throw ArgError("draft rows: not a device allocation");
+    }
+    if (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged)
+        throw ArgError("draft rows: not device memory");
+    if (at.device != m.cfg.device) throw ArgError("draft rows: memory of another device");
+}
+
+void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, bool q_on_device,
+                          size_t q_rows_n, size_t q_vocab, const int *q_row_of, const float *uniforms,
+                          float temperature, int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin,
+                          size_t &used) {
     Model &m = *model;
     const ModelCfg &c = m.cfg;
     if (m.logits_rows_last < n) throw BackendError("acceptance: fewer logits rows than tree nodes");
     const size_t qn = q_rows_n * q_vocab;
-    if (qn > m.acc_q_cap) {
+    if (!q_on_device && qn > m.acc_q_cap) {
         if (m.acc_q) SD_HIP_CHECK(hipFree(m.acc_q));
         m.acc_q = nullptr;
         m.acc_q_cap = 0;
         SD_HIP_CHECK(hipMalloc((void **)&m.acc_q, qn * sizeof(float) + 256));
         m.acc_q_cap = qn;
+    }
+    const size_t pn = (size_t)n * c.vocab;
+    if (pn > m.acc_prob_cap) {
+        if (m.acc_prob) SD_HIP_CHECK(hipFree(m.acc_prob));
+        m.acc_prob = nullptr;
+        m.acc_prob_cap = 0;
+        SD_HIP_CHECK(hipMalloc((void **)&m.acc_prob, pn * sizeof(float) + 256));
+        m.acc_prob_cap = pn;
     }
     // parents | tokens | q_row_of, uniforms and draft rows: one copy each
     std::vector<int> tree((size_t)3 * n);
@@ -1298,14 +1325,15 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     std::memcpy(tree.data() + 2 * n, q_row_of, n * sizeof(int));
     SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, tree.data(), tree.size() * sizeof(int), hipMemcpyHostToDevice, m.st));
     SD_HIP_CHECK(hipMemcpyAsync(m.acc_u, uniforms, n * sizeof(float), hipMemcpyHostToDevice, m.st));
-    if (qn) SD_HIP_CHECK(hipMemcpyAsync(m.acc_q, q_rows, qn * sizeof(float), hipMemcpyHostToDevice, m.st));
+    if (qn && !q_on_device)
+        SD_HIP_CHECK(hipMemcpyAsync(m.acc_q, q_rows, qn * sizeof(float), hipMemcpyHostToDevice, m.st));
     const bool greedy = temperature == 0.f;
     const float inv_t = greedy ? 1.f : 1.0f / temperature;
     const int *mask = use_t2d ? m.t2d_inv : nullptr;
-    launch_row_stats(m.logits, c.vocab, c.vocab, n, inv_t, mask, m.acc_m, m.acc_s, m.acc_am, m.st);
+    launch_row_stats(m.logits, c.vocab, c.vocab, n, inv_t, greedy ? 1 : 0, mask, m.acc_part, m.acc_cnt, m.acc_m,
+                     m.acc_s, m.acc_am, m.acc_prob, m.st);
     AcceptParams a{};
-    a.logits = m.logits;
-    a.ld = c.vocab;
+    a.prob = m.acc_prob;
     a.V = c.vocab;
     a.n = n;
     a.parents = m.acc_tree;
@@ -1317,7 +1345,7 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     a.inv_t = inv_t;
     a.greedy = greedy ? 1 : 0;
     a.t2d_inv = mask;
-    a.q = m.acc_q;
+    a.q = q_on_device ? q_rows : m.acc_q;
     a.q_ld = (int64_t)q_vocab;
     a.q_map = q_vocab == (size_t)c.vocab ? nullptr : m.t2d_inv;
     a.uniforms = m.acc_u;
@@ -1347,11 +1375,12 @@ static void check_temperature(float t) {
 
 void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const float *q_rows, const float *uniforms,
                                       size_t n_uniforms, float temperature, size_t max_commit, uint32_t *commits,
-                                      size_t *n_commit, size_t *n_accepted, size_t *n_used) {
+                                      size_t *n_commit, size_t *n_accepted, size_t *n_used, bool q_on_device) {
     Model &m = *model;
     check_temperature(temperature);
     if (n_uniforms < k + 1) throw ArgError("rejection verify needs k + 1 uniforms");
     if (k + 1 > (size_t)m.cfg.max_batch) throw ArgError("too many draft tokens for one verify pass");
+    if (q_on_device) check_device_rows(m, q_rows, k * (size_t)m.cfg.vocab);
     if (history.empty()) throw SamplingError("batched_logits with empty history");
     const uint32_t last = history.back();
     batched_logits(drafts, k, nullptr);
@@ -1371,7 +1400,8 @@ void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const fl
     std::vector<int> path;
     int fin;
     size_t used;
-    accept_walk(parents.data(), tokens.data(), n, q_rows, k, m.cfg.vocab, qrow.data(), uniforms, temperature, 0, 0,
+    accept_walk(parents.data(), tokens.data(), n, q_rows, q_on_device, k, m.cfg.vocab, qrow.data(), uniforms,
+                temperature, 0, 0,
                 max_commit, path, fin, used);
     size_t nc = 0;
     for (size_t i = 1; i < path.size(); i++) commits[nc++] = (uint32_t)tokens[path[i]];
@@ -1385,7 +1415,7 @@ void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *pare
                                     size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of,
                                     const float *uniforms, size_t n_uniforms, float temperature, int use_t2d,
                                     int siblings, size_t max_commit, uint32_t *path, size_t *path_len,
-                                    int32_t *token, size_t *n_used) {
+                                    int32_t *token, size_t *n_used, bool q_on_device) {
     Model &m = *model;
     check_temperature(temperature);
     if (siblings != 0 && siblings != 1) throw ArgError("sibling rule must be 0 (i.i.d.) or 1 (without replacement)");
@@ -1395,6 +1425,7 @@ void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *pare
     if (q_vocab != (size_t)m.cfg.vocab && (q_vocab != (size_t)m.d2t_draft_vocab || !m.t2d_inv))
         throw ArgError("draft rows must span the target vocabulary, or the d2t draft vocabulary after sd_set_d2t");
     if (use_t2d && !m.t2d_inv) throw ArgError("t2d masking needs sd_set_d2t");
+    if (q_on_device) check_device_rows(m, q_rows, q_rows_n * q_vocab);
     std::vector<bool> has_child(n, false);
     std::vector<int> nchild(n, 0);
     for (size_t i = 1; i < n; i++) {
@@ -1415,7 +1446,8 @@ void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *pare
     std::vector<int> p;
     int fin;
     size_t used;
-    accept_walk(par.data(), tok.data(), (int)n, q_rows, q_rows_n, q_vocab, qr.data(), uniforms, temperature, use_t2d,
+    accept_walk(par.data(), tok.data(), (int)n, q_rows, q_on_device, q_rows_n, q_vocab, qr.data(), uniforms,
+                temperature, use_t2d,
                 siblings, max_commit, p, fin, used);
     for (size_t i = 0; i < p.size(); i++) path[i] = (uint32_t)p[i];
     *path_len = p.size();

@@ -153,6 +153,10 @@ class Model {
     // draft rows, uniforms and results (draft rows grow on demand)
     float *acc_m = nullptr, *acc_s = nullptr, *acc_u = nullptr, *acc_q = nullptr;
     size_t acc_q_cap = 0;  // floats
+    uint64_t *acc_part = nullptr;  // row statistics' per-slice partials
+    int *acc_cnt = nullptr;        // their per-row arrival counts (zero between launches)
+    float *acc_prob = nullptr;     // the verify rows as distributions
+    size_t acc_prob_cap = 0;       // floats
     int *acc_am = nullptr, *acc_tree = nullptr, *acc_out = nullptr;
     // d2t map of an EAGLE-3 draft (eagle3.rs:377-397): target id -> draft id or -1
     int *t2d_inv = nullptr;
@@ -216,14 +220,16 @@ class Decoder {
                             uint32_t *committed, size_t *n_committed, size_t *keep_len, int32_t *stop);
     void argmax_rows(int32_t *out, size_t n);
     // batched_logits + the rejection walk of vanilla.rs:178-210 on the device
+    // (q_on_device: q_rows is a device pointer on the model's GPU, not uploaded)
     void verify_rejection_linear(const uint32_t *drafts, size_t k, const float *q_rows, const float *uniforms,
                                  size_t n_uniforms, float temperature, size_t max_commit, uint32_t *commits,
-                                 size_t *n_commit, size_t *n_accepted, size_t *n_used);
+                                 size_t *n_commit, size_t *n_accepted, size_t *n_used, bool q_on_device = false);
     // tree_logits_keep_kv + the tree rejection walk (sd_accept.hip)
     void verify_rejection_tree(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *q_rows,
                                size_t q_rows_n, size_t q_vocab, const int32_t *q_row_of, const float *uniforms,
                                size_t n_uniforms, float temperature, int use_t2d, int siblings, size_t max_commit,
-                               uint32_t *path, size_t *path_len, int32_t *token, size_t *n_used);
+                               uint32_t *path, size_t *path_len, int32_t *token, size_t *n_used,
+                               bool q_on_device = false);
     // EAGLE-3 vocabulary map (eagle3.rs:377-397, 476-513)
     void set_d2t(const int64_t *d2t, size_t n);
     std::vector<int64_t> d2t_host;
@@ -235,9 +241,9 @@ class Decoder {
   private:
     void forward_advance(const uint32_t *tokens, size_t n, bool all_rows);
     // the acceptance walk over logits rows [0, n) of the last pass
-    void accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, size_t q_rows_n,
-                     size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature, int use_t2d,
-                     int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
+    void accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, bool q_on_device,
+                     size_t q_rows_n, size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature,
+                     int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
     void truncate(size_t len);
     void tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden, int &prefix);
 };

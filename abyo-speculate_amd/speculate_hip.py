@@ -140,6 +140,9 @@ def load_library(path: str = LIB_PATH):
         "sd_verify_rejection_linear": ([P, P, SZ, P, P, SZ, ctypes.c_float, SZ, P, pSZ, pSZ, pSZ], I32),
         "sd_verify_rejection_tree": ([P, P, P, SZ, P, SZ, SZ, P, P, SZ, ctypes.c_float, I32, I32, SZ, P, pSZ, P,
                                       pSZ], I32),
+        "sd_verify_rejection_linear_device_q": ([P, P, SZ, P, P, SZ, ctypes.c_float, SZ, P, pSZ, pSZ, pSZ], I32),
+        "sd_verify_rejection_tree_device_q": ([P, P, P, SZ, P, SZ, SZ, P, P, SZ, ctypes.c_float, I32, I32, SZ, P, pSZ,
+                                               P, pSZ], I32),
         "sd_set_d2t": ([P, P, SZ], I32),
         "sd_draft_to_target": ([P, P, SZ, P], I32),
         "sd_t2d_mask": ([P, P, SZ], SZ),
@@ -272,6 +275,64 @@ class TreeCommit:
 
     def keep(self) -> List[int]:
         return self.path[:self.keep_len] + ([self.bonus_node] if self.bonus_node >= 0 else [])
+
+
+_hiprt = None
+
+
+def _hip_runtime():
+    """The HIP runtime the library is linked against (already loaded with it)."""
+    global _hiprt
+    if _hiprt is None:
+        load_library()
+        path = "libamdhip64.so"
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        rt = ctypes.CDLL(path)
+        rt.hipSetDevice.argtypes = [ctypes.c_int]
+        rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        rt.hipFree.argtypes = [ctypes.c_void_p]
+        rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        for fn in (rt.hipSetDevice, rt.hipMalloc, rt.hipFree, rt.hipMemcpy):
+            fn.restype = ctypes.c_int
+        _hiprt = rt
+    return _hiprt
+
+
+class DeviceArray:
+    """A host array copied into one GPU's memory with the library's HIP
+    runtime: the input of the *_device entry points (draft rows a GPU draft
+    model would leave on the device).  `ptr` is the device address; close()
+    frees it."""
+
+    def __init__(self, host: np.ndarray, device: int = 0):
+        self.host_shape, self.dtype = host.shape, host.dtype
+        a = np.ascontiguousarray(host)
+        rt = _hip_runtime()
+        self._p = ctypes.c_void_p()
+        if rt.hipSetDevice(device) != 0 or rt.hipMalloc(ctypes.byref(self._p), max(a.nbytes, 1)) != 0:
+            raise BackendError("hipMalloc failed")
+        if rt.hipMemcpy(self._p, a.ctypes.data_as(ctypes.c_void_p), a.nbytes, 1) != 0:
+            rt.hipFree(self._p)
+            raise BackendError("hipMemcpy failed")
+
+    @property
+    def ptr(self) -> int:
+        return int(self._p.value or 0)
+
+    def close(self):
+        if self._p.value:
+            _hip_runtime().hipFree(self._p)
+            self._p = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class HipQuantDecoder:
@@ -486,12 +547,22 @@ class HipQuantDecoder:
         q = np.ascontiguousarray(q_rows, np.float32)
         if d.size and q.shape != (d.size, self.cfg.vocab):
             raise ValueError("q_rows must be [k][vocab]")
+        return self._rejection_linear(_lib.sd_verify_rejection_linear, d, _ptr(q), uniforms, temperature, max_commit)
+
+    def verify_rejection_linear_device(self, drafts: Sequence[int], q_rows_dev: int, uniforms: Sequence[float],
+                                       temperature: float, max_commit: int = 0):
+        """verify_rejection_linear with the [k][vocab] f32 draft rows already in
+        this GPU's memory at address q_rows_dev (written and synchronised by
+        the caller)."""
+        return self._rejection_linear(_lib.sd_verify_rejection_linear_device_q, _u32(drafts),
+                                      ctypes.c_void_p(int(q_rows_dev)), uniforms, temperature, max_commit)
+
+    def _rejection_linear(self, fn, d, q_ptr, uniforms, temperature, max_commit):
         u = np.ascontiguousarray(uniforms, np.float32)
         commits = np.empty(d.size + 1, np.uint32)
         nc, na, nu = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
-        _check(_lib.sd_verify_rejection_linear(self._h, _ptr(d), d.size, _ptr(q), _ptr(u), u.size,
-                                               float(temperature), max_commit, _ptr(commits), ctypes.byref(nc),
-                                               ctypes.byref(na), ctypes.byref(nu)))
+        _check(fn(self._h, _ptr(d), d.size, q_ptr, _ptr(u), u.size, float(temperature), max_commit, _ptr(commits),
+                  ctypes.byref(nc), ctypes.byref(na), ctypes.byref(nu)))
         return [int(v) for v in commits[:nc.value]], int(na.value), int(nu.value)
 
     def verify_rejection_tree(self, tree, q_rows: np.ndarray, q_row_of: Sequence[int], uniforms: Sequence[float],
@@ -500,10 +571,24 @@ class HipQuantDecoder:
         """-> (path node indices, final token or -1, uniforms_used).  The
         sibling rule: i.i.d. siblings (q fixed) or, with without_replacement,
         siblings drawn without replacement (rejected tokens zeroed in q)."""
-        t, p = tree_arrays(tree)
         q = np.ascontiguousarray(q_rows, np.float32)
         if q.ndim != 2:
             raise ValueError("q_rows must be 2-D")
+        return self._rejection_tree(_lib.sd_verify_rejection_tree, tree, _ptr(q), q.shape[0], q.shape[1], q_row_of,
+                                    uniforms, temperature, use_t2d, max_commit, without_replacement)
+
+    def verify_rejection_tree_device(self, tree, q_rows_dev: int, q_rows_n: int, q_vocab: int,
+                                     q_row_of: Sequence[int], uniforms: Sequence[float], temperature: float,
+                                     use_t2d: bool = False, max_commit: int = 0, without_replacement: bool = False):
+        """verify_rejection_tree with the [q_rows_n][q_vocab] f32 draft rows
+        already in this GPU's memory at address q_rows_dev."""
+        return self._rejection_tree(_lib.sd_verify_rejection_tree_device_q, tree, ctypes.c_void_p(int(q_rows_dev)),
+                                    q_rows_n, q_vocab, q_row_of, uniforms, temperature, use_t2d, max_commit,
+                                    without_replacement)
+
+    def _rejection_tree(self, fn, tree, q_ptr, q_n, q_vocab, q_row_of, uniforms, temperature, use_t2d, max_commit,
+                        without_replacement):
+        t, p = tree_arrays(tree)
         qr = np.ascontiguousarray(q_row_of, np.int32)
         if qr.size != t.size:
             raise ValueError("q_row_of needs one entry per node")
@@ -511,11 +596,9 @@ class HipQuantDecoder:
         path = np.empty(t.size, np.uint32)
         plen, nu = ctypes.c_size_t(), ctypes.c_size_t()
         tok = ctypes.c_int32()
-        _check(_lib.sd_verify_rejection_tree(self._h, _ptr(t), _ptr(p), t.size, _ptr(q), q.shape[0], q.shape[1],
-                                             _ptr(qr), _ptr(u), u.size, float(temperature), 1 if use_t2d else 0,
-                                             1 if without_replacement else 0, max_commit, _ptr(path),
-                                             ctypes.byref(plen), ctypes.byref(tok),
-                                             ctypes.byref(nu)))
+        _check(fn(self._h, _ptr(t), _ptr(p), t.size, q_ptr, q_n, q_vocab, _ptr(qr), _ptr(u), u.size,
+                  float(temperature), 1 if use_t2d else 0, 1 if without_replacement else 0, max_commit, _ptr(path),
+                  ctypes.byref(plen), ctypes.byref(tok), ctypes.byref(nu)))
         return [int(v) for v in path[:plen.value]], int(tok.value), int(nu.value)
 
     def set_d2t(self, d2t: Sequence[int]):

@@ -244,6 +244,23 @@ sd_status sd_verify_rejection_tree(sd_model *m, const uint32_t *tokens, const ui
                                    const float *uniforms, size_t n_uniforms, float temperature, int32_t use_t2d,
                                    int32_t siblings, size_t max_commit, uint32_t *path, size_t *path_len,
                                    int32_t *token, size_t *n_used);
+/* The two rejection verifies above with the draft rows already in device
+ * memory (q_rows_dev: [k][vocab] or [q_rows_n][q_vocab] f32, device memory of
+ * this model's GPU, e.g. written there by the draft model), so that nothing
+ * of them crosses PCIe.  The rows must be complete before the call (the
+ * library reads them on its own stream).  SD_ERR_ARG for a pointer that is
+ * not device memory of this GPU.  No counterpart in the reference: it is the
+ * same walk as sd_verify_rejection_linear (vanilla.rs:178-210) /
+ * sd_verify_rejection_tree, for callers whose draft side runs on the GPU. */
+sd_status sd_verify_rejection_linear_device_q(sd_model *m, const uint32_t *drafts, size_t k, const float *q_rows_dev,
+                                              const float *uniforms, size_t n_uniforms, float temperature,
+                                              size_t max_commit, uint32_t *commits, size_t *n_commit,
+                                              size_t *n_accepted, size_t *n_used);
+sd_status sd_verify_rejection_tree_device_q(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
+                                            const float *q_rows_dev, size_t q_rows_n, size_t q_vocab,
+                                            const int32_t *q_row_of, const float *uniforms, size_t n_uniforms,
+                                            float temperature, int32_t use_t2d, int32_t siblings, size_t max_commit,
+                                            uint32_t *path, size_t *path_len, int32_t *token, size_t *n_used);
 /* EAGLE-3 vocabulary map (Eagle3DraftCandle's d2t, eagle3.rs:377-397): d2t[draft id]
  * = absolute target id; entries outside [0, vocab) are skipped; the inverse
  * keeps the last draft id of a target id (HashMap::insert). */

@@ -95,3 +95,45 @@ def test_tree60_p2048(hip, pair):
     assert np.all(herr < TOL), float(herr.max())
     argmax_agreement(got, ref)
     dec.rollback_to(P + 1)
+
+
+def test_rejection_m9_full_vocab(hip, pair):
+    """The rejection walk over 152064-entry rows (the row statistics' slices,
+    the walk's tiles) against the oracle's walk, with host and with
+    device-resident draft rows (the benchmark's Qwen2.5-7B workload)."""
+    from test_gpu_rejection import _check_walk, _draft_rows, _peaked_q
+    dec, om = pair
+    V, k = QWEN7B["vocab"], 8
+    rng = np.random.default_rng(91)
+    P = 300
+    hist = [int(v) for v in rng.integers(0, V, P + 1)]
+    dec.prime_synthetic(hist, 93)
+    L = P + 1
+    kinds = {"exact": 0, "boundary": 0}
+    for trial in range(6):
+        q = _draft_rows(rng, k, V)
+        drafts = [int(O.sample_u(q[i], float(rng.random()))) for i in range(k)]
+        rows = dec.batched_logits(drafts)
+        dec.rollback_to(L)
+        T = 1.0 if trial < 4 else 0.0
+        if trial in (2, 3):
+            for i in range(k):
+                q[i] = _peaked_q(O.softmax_t(rows[i], T), [drafts[i]], rng)
+        u = [float(x) for x in rng.random(k + 1, dtype=np.float32)]
+        commits, n_acc, used = dec.verify_rejection_linear(drafts, q, u, T)
+        dec.rollback_to(L)
+        with hip.DeviceArray(q) as qd:
+            assert dec.verify_rejection_linear_device(drafts, qd.ptr, u, T) == (commits, n_acc, used)
+        dec.rollback_to(L)
+        oc, on, ou = O.rejection_linear_accept(list(rows), list(q), drafts, u, T)
+        tree = O.DraftTree.linear(hist[-1], drafts)
+        dev_fin = commits[n_acc] if len(commits) > n_acc else None
+        ora_fin = oc[on] if len(oc) > on else None
+        # the oracle's sequential f32 CDF over 152064 entries drifts by up to
+        # V ulps of 1; the device's tree sums are held to the default window
+        kind = _check_walk(list(range(n_acc + 1)), dev_fin, list(range(on + 1)), ora_fin, tree, list(rows), list(q),
+                           list(range(k)) + [-1], u, T, ora_draw_eps=V * 2.0 ** -24)
+        kinds[kind] += 1
+        if kind == "exact":
+            assert commits == oc and n_acc == on and used == ou
+    assert kinds["exact"] >= 2, kinds

@@ -80,35 +80,43 @@ def _walk64(tree, rows, q_rows, q_row_of, u, T, mask=None, max_commit=None, flip
 
 
 def _draw_ok(tok, tok64, t, cdf, draw_eps):
-    """(token valid, drawn away from a CDF boundary).  Near a boundary the
-    token may be either of the two that meet there."""
+    """(token valid, drawn away from a CDF boundary).  Near a boundary (the
+    target within draw_eps of one) the token may be any token of positive
+    mass whose CDF step reaches into [t - draw_eps, t + draw_eps]."""
     if tok64 is None:
         return tok is None, True
+    if tok is None:
+        return False, True
     lo = cdf[tok64 - 1] if tok64 > 0 else 0.0
     near = min(t - lo, cdf[tok64] - t) < draw_eps
     if not near:
         return tok == tok64, True
-    return tok in (tok64 - 1, tok64, tok64 + 1), False
+    tlo = cdf[tok - 1] if tok > 0 else 0.0
+    return bool(cdf[tok] > tlo and tlo <= t + draw_eps and cdf[tok] >= t - draw_eps), False
 
 
 def _check_walk(dev_path, dev_tok, ora_path, ora_tok, tree, rows, q_rows, q_row_of, u, T, mask=None,
-                max_commit=None, wor=False):
+                max_commit=None, wor=False, ora_draw_eps=None):
     """Returns 'exact' or 'boundary' and asserts that the device and the
     oracle results are valid walks.  A decision is a near tie when |u -
     min(1, p/q)| < DEC_EPS: both sides of it are then valid, and device and
     oracle must each follow one of them exactly.  A draw is near a boundary
     when its target is within 4 sqrt(V) f32 ulps of 1 of one (the spread of
     sequential f32 running sums over V terms): the token is then one of the
-    two meeting there.  Everything else must agree exactly."""
+    two meeting there.  Everything else must agree exactly.  ora_draw_eps
+    widens the oracle's window: its sequential f32 running sum over a large
+    flat row drifts by up to V f32 ulps of 1 (the reference's own rounding),
+    while the device's tree sums stay within the default window."""
     path64, tok64, margins, t, cdf = _walk64(tree, rows, q_rows, q_row_of, u, T, mask, max_commit, wor=wor)
     draw_eps = 4.0 * np.sqrt(len(rows[0])) * 2.0 ** -24
+    ora_eps = draw_eps if ora_draw_eps is None else ora_draw_eps
     ties = [i for i, m in margins.items() if m < DEC_EPS]
     if not ties:
         assert dev_path == ora_path == path64, (dev_path, ora_path, path64)
-        ok_d, exact = _draw_ok(dev_tok, tok64, t, cdf, draw_eps)
-        ok_o, _ = _draw_ok(ora_tok, tok64, t, cdf, draw_eps)
+        ok_d, exact_d = _draw_ok(dev_tok, tok64, t, cdf, draw_eps)
+        ok_o, exact_o = _draw_ok(ora_tok, tok64, t, cdf, ora_eps)
         assert ok_d and ok_o, (dev_tok, ora_tok, tok64)
-        if exact:
+        if exact_d and exact_o:
             assert dev_tok == ora_tok == tok64
             return "exact"
         return "boundary"
@@ -117,8 +125,8 @@ def _check_walk(dev_path, dev_tok, ora_path, ora_tok, tree, rows, q_rows, q_row_
     for k in range(1 << len(ties)):
         flip = frozenset(ties[j] for j in range(len(ties)) if (k >> j) & 1)
         alts.append(_walk64(tree, rows, q_rows, q_row_of, u, T, mask, max_commit, flip=flip, wor=wor))
-    for path, tok in ((dev_path, dev_tok), (ora_path, ora_tok)):
-        assert any(path == a[0] and _draw_ok(tok, a[1], a[3], a[4], draw_eps)[0] for a in alts), (path, tok)
+    for path, tok, eps in ((dev_path, dev_tok, draw_eps), (ora_path, ora_tok, ora_eps)):
+        assert any(path == a[0] and _draw_ok(tok, a[1], a[3], a[4], eps)[0] for a in alts), (path, tok)
     return "boundary"
 
 
@@ -140,20 +148,31 @@ def _draft_rows(rng, k, V, scale=2.0):
 
 
 def _peaked_q(p, favour, rng, n_keep=6):
-    """A draft row that equals the target row p except on n_keep random
-    tokens, which keep a fifth of their mass; the mass taken from them goes
-    to the `favour` tokens (the drafts).  After a rejection the adjusted
-    distribution max(p - q, 0) is then supported on those n_keep tokens only,
-    so the resample lands well inside one of a few wide CDF steps even where
-    p itself is nearly flat (T = 1 over a large vocabulary)."""
-    q = np.asarray(p, np.float32).copy()
-    S = rng.choice(np.flatnonzero(q > 0), n_keep, replace=False)
-    S = np.setdiff1d(S, favour)
-    moved = float(np.sum(q[S]) * 0.8)
-    q[S] *= np.float32(0.2)
+    """A draft row that follows the target row p except on its n_keep most
+    likely tokens (other than the favour tokens, the drafts), which keep a
+    fifth of their mass; the favour tokens take the rest.  After a rejection
+    the adjusted distribution max(p - q, 0) is then supported on those n_keep
+    tokens only, so the resample lands well inside one of a few wide CDF
+    steps even where p itself is nearly flat (T = 1 over a large vocabulary).
+    Elsewhere q is p scaled up by a relative margin of 0.3 times the kept
+    mass: p - q then stays negative there however either side rounds p (the
+    reference's sequential f32 softmax sum over 152064 entries is off by
+    ~1e-5 relative; the kept mass is a few 1e-3 or more)."""
+    p = np.asarray(p, np.float64)
+    q = p.copy()
+    order = [int(x) for x in np.argsort(-p, kind="stable") if int(x) not in set(int(f) for f in favour)]
+    S = np.array(order[:n_keep])
+    pk = float(np.sum(p[S]))
+    rest = np.ones(p.size, bool)
+    rest[S] = False
+    rest[np.asarray(favour)] = False
+    q[rest] *= 1.0 + 0.3 * pk
+    q[S] *= 0.2
+    extra = 1.0 - float(np.sum(q))  # about half the kept mass
+    assert extra > 0
     for f in favour:
-        q[f] += np.float32(moved / len(favour))
-    return q
+        q[f] += extra / len(favour)
+    return q.astype(np.float32)
 
 
 @pytest.mark.parametrize("over,k", [
@@ -343,3 +362,50 @@ def test_rejection_tree_chain_equals_linear(hip):
         hd.rollback_to(L)
         assert path == list(range(n_acc + 1)) and used_t == used
         assert commits == drafts[:n_acc] + ([tok] if tok >= 0 else [])
+
+
+QWEN_SMALL = dict(arch="qwen2", n_kv_heads=4, mix="q5k_q80", n_layers=2, rms_eps=1e-6, rope_theta=1e6)
+
+
+def test_rejection_device_rows_match_host_rows(hip):
+    """The device-resident draft-row entry points run the same walk as the
+    host-row ones: identical results, uniform for uniform; a host pointer is
+    refused before the verify pass touches any state."""
+    ocfg, hd, prefix = _pair(hip, **QWEN_SMALL)
+    V, k = ocfg.vocab, 8
+    rng = np.random.default_rng(5)
+    L = len(prefix)
+    for T in (1.0, 0.3, 0.0):
+        for _ in range(3):
+            q = _draft_rows(rng, k, V)
+            drafts = [int(O.sample_u(q[i], float(rng.random()))) for i in range(k)]
+            u = [float(x) for x in rng.random(k + 1, dtype=np.float32)]
+            host = hd.verify_rejection_linear(drafts, q, u, T)
+            hd.rollback_to(L)
+            with hip.DeviceArray(q) as qd:
+                dev = hd.verify_rejection_linear_device(drafts, qd.ptr, u, T)
+            hd.rollback_to(L)
+            assert dev == host, (T, dev, host)
+    # a tree whose draft rows live in a d2t draft vocabulary
+    Vd = 8000
+    d2t = _seeded_d2t(rng, Vd, V)
+    hd.set_d2t(d2t)
+    cands = [[int(d2t[v]) for v in rng.choice(Vd, b, replace=False)] for b in (4, 3, 2, 1)]
+    toks, pars = hip.tree_prune(hip.tree_cartesian(prefix[-1], cands),
+                                [list(np.log(np.full(len(c), 1.0 / len(c))).astype(np.float32)) for c in cands], 24)
+    n = len(toks)
+    q_d = _draft_rows(rng, n, Vd)
+    u = [float(x) for x in rng.random(n, dtype=np.float32)]
+    for use_t2d in (False, True):
+        host = hd.verify_rejection_tree((toks, pars), q_d, list(range(n)), u, 1.0, use_t2d)
+        hd.rollback_to(L)
+        with hip.DeviceArray(q_d) as qd:
+            dev = hd.verify_rejection_tree_device((toks, pars), qd.ptr, n, Vd, list(range(n)), u, 1.0, use_t2d)
+        hd.rollback_to(L)
+        assert dev == host, (use_t2d, dev, host)
+    q = _draft_rows(rng, 2, V)
+    with pytest.raises(hip.ArgError):
+        hd.verify_rejection_linear_device([1, 2], q.ctypes.data, [0.5, 0.5, 0.5], 1.0)
+    with pytest.raises(hip.ArgError):
+        hd.verify_rejection_tree_device((toks, pars), q_d.ctypes.data, n, Vd, list(range(n)), u, 1.0)
+    assert hd.history() == prefix and hd.cache_len() == L
