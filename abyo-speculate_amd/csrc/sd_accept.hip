@@ -43,13 +43,13 @@ namespace sd {
 #pragma clang fp contract(off)
 
 // ---- per-row softmax statistics ----------------------------------------------
-// grid (rows, slices of kSlice entries), block kRsT.  Online (max, sum of
-// exp((l - max) * inv_t)) per thread over a strided walk of the slice, merged
-// in a fixed tree; the slices' states are merged in slice order by the last
-// workgroup of the row to finish (a per-row arrival count, device-scope
-// partials).  Entries unreachable through the t2d map (t2d_inv[x] < 0) count
-// as -inf (mask_target_logits, eagle3.rs:498-513).  Also the first-max argmax
-// (greedy one-hot).
+// grid (rows, slices of kSlice entries), block kRsT.  A slice's max M and sum
+// of exp((l - M) * inv_t) (two workgroup reductions: the max first, then the
+// sum relative to it); the slices' (max, sum) pairs are merged in slice order
+// by the last workgroup of the row to finish (a per-row arrival count,
+// device-scope partials).  Entries unreachable through the t2d map
+// (t2d_inv[x] < 0) count as -inf (mask_target_logits, eagle3.rs:498-513).
+// Also the first-max argmax (greedy one-hot).
 constexpr int kRsT = 256, kSlice = 8192;
 
 __device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
@@ -70,12 +70,33 @@ __device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s
     s1 = S;
 }
 constexpr int kNoIdx = 0x7fffffff;
-// the earlier of two first-max candidates (i2 from the later range on ties)
+// the earlier of two first-max candidates
 __device__ __forceinline__ void am_merge(float &v1, int &i1, float v2, int i2) {
     if (i2 != kNoIdx && (i1 == kNoIdx || v2 > v1 || (v2 == v1 && i2 < i1))) {
         v1 = v2;
         i1 = i2;
     }
+}
+
+// workgroup-wide reductions (kRsT threads = 4 waves): lanes by xor butterflies,
+// then the 4 waves in order; every thread gets the result
+__device__ __forceinline__ float wg_max(float v, float *sh) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ float wg_sum(float v, float *sh) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
 }
 
 __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t ld, int V, float inv_t,
@@ -84,8 +105,6 @@ __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t
     const int r = blockIdx.x, sl = blockIdx.y, nsl = gridDim.y, t = threadIdx.x;
     const float *row = logits + (int64_t)r * ld;
     const int x1 = min(V, (sl + 1) * kSlice);
-    float m = -INFINITY, s = 0.f, bv = -INFINITY;
-    int bi = kNoIdx, bad = 0;
     // the thread's kPer entries x = slice start + t + kRsT i, all requested at once
     constexpr int kPer = kSlice / kRsT;
     float lv[kPer];
@@ -95,41 +114,40 @@ __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t
         lv[i] = x < x1 ? row[x] : -INFINITY;
         if (t2d_inv && x < x1 && t2d_inv[x] < 0) lv[i] = -INFINITY;
     }
+    float bv = -INFINITY;
+    int bi = kNoIdx, bad = 0;
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
-        const int x = sl * kSlice + t + kRsT * i;
-        if (x >= x1) break;
         const float l = lv[i];
         // a NaN or +inf entry makes the reference's sum non-finite (an error there)
         if (l != l || l == INFINITY) bad = 1;
         if (l > bv) {  // strictly greater: first max per thread (x increases)
             bv = l;
-            bi = x;
-        }
-        if (l > m) {
-            s = s * expf((m - l) * inv_t) + 1.f;
-            m = l;
-        } else if (l > -INFINITY) {
-            s += expf((l - m) * inv_t);
+            bi = sl * kSlice + t + kRsT * i;
         }
     }
-    __shared__ float sm[kRsT], ss[kRsT], sv[kRsT];
+    __shared__ float sh[4];
+    __shared__ float sv[kRsT];
     __shared__ int si[kRsT];
     __shared__ int s_last;
     const bool any_bad = __syncthreads_or(bad) != 0;
-    sm[t] = m;
-    ss[t] = s;
+    const float M = wg_max(bv, sh);
+    float s = 0.f;
+    if (M > -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < kPer; i++)
+            if (lv[i] > -INFINITY) s += expf((lv[i] - M) * inv_t);
+    }
+    const float S = wg_sum(s, sh);
+    // first-max argmax: a fixed tree over the threads
     sv[t] = bv;
     si[t] = bi;
     __syncthreads();
     for (int o = kRsT / 2; o > 0; o >>= 1) {
         if (t < o) {
-            float m1 = sm[t], s1 = ss[t], v1 = sv[t];
+            float v1 = sv[t];
             int i1 = si[t];
-            ms_merge(m1, s1, sm[t + o], ss[t + o], inv_t);
             am_merge(v1, i1, sv[t + o], si[t + o]);
-            sm[t] = m1;
-            ss[t] = s1;
             sv[t] = v1;
             si[t] = i1;
         }
@@ -137,7 +155,7 @@ __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t
     }
     if (t == 0) {
         uint64_t *pp = part + ((int64_t)r * nsl + sl) * 2;
-        st_dev64(pp, pack2(sm[0], __float_as_uint(any_bad ? NAN : ss[0])));
+        st_dev64(pp, pack2(M, __float_as_uint(any_bad ? NAN : S)));
         st_dev64(pp + 1, pack2(sv[0], (uint32_t)si[0]));
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partials are stored before the count
         const int last = __hip_atomic_fetch_add(cnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsl - 1;
@@ -147,26 +165,28 @@ __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t
     __syncthreads();
     if (!s_last) return;
     // the row's slices, in slice order
+    __shared__ float pm[kRowStatsMaxSlices], ps[kRowStatsMaxSlices], pv[kRowStatsMaxSlices];
+    __shared__ int pi[kRowStatsMaxSlices];
     if (t < nsl) {
         const uint64_t a = ld_dev64(part + ((int64_t)r * nsl + t) * 2);
         const uint64_t b = ld_dev64(part + ((int64_t)r * nsl + t) * 2 + 1);
-        sm[t] = __uint_as_float((uint32_t)a);
-        ss[t] = __uint_as_float((uint32_t)(a >> 32));
-        sv[t] = __uint_as_float((uint32_t)b);
-        si[t] = (int)(uint32_t)(b >> 32);
+        pm[t] = __uint_as_float((uint32_t)a);
+        ps[t] = __uint_as_float((uint32_t)(a >> 32));
+        pv[t] = __uint_as_float((uint32_t)b);
+        pi[t] = (int)(uint32_t)(b >> 32);
     }
     __syncthreads();
     if (t == 0) {
-        float M = sm[0], S = ss[0], v = sv[0];
-        int i = si[0];
-        bool nan = S != S;
+        float Mr = pm[0], Sr = ps[0], v = pv[0];
+        int i = pi[0];
+        bool nan = Sr != Sr;
         for (int k = 1; k < nsl; k++) {
-            nan = nan || ss[k] != ss[k];
-            ms_merge(M, S, sm[k], ss[k], inv_t);
-            am_merge(v, i, sv[k], si[k]);
+            nan = nan || ps[k] != ps[k];
+            ms_merge(Mr, Sr, pm[k], ps[k], inv_t);
+            am_merge(v, i, pv[k], pi[k]);
         }
-        row_m[r] = M;
-        row_s[r] = nan ? NAN : S;
+        row_m[r] = Mr;
+        row_s[r] = nan ? NAN : Sr;
         row_am[r] = i == kNoIdx ? 0 : i;
     }
 }
@@ -211,7 +231,12 @@ constexpr int kTile = 256;     // entries per tile: lane l of a wave holds x = 2
 constexpr int kMaxTiles = 1024;  // vocabularies up to 262144
 constexpr int MAX_REJ = 16;
 
+constexpr int kMaxNodes = 256;
 struct WalkShared {
+    // the tree and its per-node inputs, staged once: the walk's serial part
+    // (thread 0) then reads LDS instead of waiting on memory for each node
+    int par[kMaxNodes], tok[kMaxNodes], qrow[kMaxNodes];
+    float uni[kMaxNodes], rs[kMaxNodes];
     float tsum[kMaxTiles];  // per-tile sums of the last pass
     float total;
     float Z[MAX_REJ];  // normalisers of the successive adjusted distributions at the current node
@@ -246,7 +271,7 @@ __device__ __forceinline__ float walk_adj(const AcceptParams &a, const WalkShare
 }
 __device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared &W, int node, int krej, int x) {
     const float p0 = a.prob[(int64_t)node * a.V + x];
-    return walk_val(a, W, krej, p0, krej > 0 ? accept_q(a, a.q_row_of[node], x) : 0.f, x);
+    return walk_val(a, W, krej, p0, krej > 0 ? accept_q(a, W.qrow[node], x) : 0.f, x);
 }
 
 // a wave's 64 values summed in a fixed order, lane 0's result
@@ -268,28 +293,48 @@ __device__ __forceinline__ float wave_scan(float v) {
 
 // Sum over x < V of the walk's values at `node` in a fixed order: tiles of
 // 256 entries (wave w takes tiles w, w + 16, ...; a lane its 4 entries in
-// order, then the wave's lanes), then the tiles.  zpass: the adjusted
+// order, then the wave's lanes), then the tiles.  ZPASS: the adjusted
 // distribution's unnormalised terms (walk_adj), else the current
-// distribution (walk_val).  Each wave requests kBatch tiles' entries before
-// it computes any of them.  Leaves the tile sums in W.tsum for walk_search.
-constexpr int kBatch = 8;
-__device__ __forceinline__ float walk_pass(WalkShared &W, const AcceptParams &a, int node, int krej, bool zpass) {
+// distribution (walk_val).  QM: how q(x) is read -- 0 not at all, 1 from a
+// target-vocabulary row, 2 through the t2d map.  Each wave requests kBatch
+// tiles' entries (clamped into the row, so that every load is issued
+// unconditionally) before it computes any of them.  Leaves the tile sums in
+// W.tsum for walk_search.
+constexpr int kBatch = 6;
+template <bool ZPASS, int QM>
+__device__ __forceinline__ void walk_tiles(WalkShared &W, const AcceptParams &a, int node, int krej) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int V = a.V, ntiles = (V + kTile - 1) / kTile;
     const float *prow = a.prob + (int64_t)node * V;
-    const int qr = a.q_row_of[node];
-    const bool needq = zpass || krej > 0;
+    const int qr = W.qrow[node];
+    const float *qrow = QM ? a.q + (int64_t)(qr < 0 ? 0 : qr) * a.q_ld : nullptr;
     for (int tb = wave; tb < ntiles; tb += (WT / 64) * kBatch) {
         float p0[kBatch][4], q0[kBatch][4];
+        int d[kBatch][4];
 #pragma unroll
         for (int b = 0; b < kBatch; b++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int x = (tb + (WT / 64) * b) * kTile + lane + 64 * j;
-                const bool ok = x < V;
-                p0[b][j] = ok ? prow[x] : 0.f;
-                q0[b][j] = ok && needq ? accept_q(a, qr, x) : 0.f;
+                const int x = min((tb + (WT / 64) * b) * kTile + lane + 64 * j, V - 1);
+                p0[b][j] = prow[x];
+                if constexpr (QM == 1) q0[b][j] = qrow[x];
+                if constexpr (QM == 2) d[b][j] = a.q_map[x];
             }
+        if constexpr (QM == 2) {
+#pragma unroll
+            for (int b = 0; b < kBatch; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float v = qrow[d[b][j] < 0 ? 0 : d[b][j]];
+                    q0[b][j] = d[b][j] < 0 ? 0.f : v;
+                }
+        }
+        if constexpr (QM == 0) {
+#pragma unroll
+            for (int b = 0; b < kBatch; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) q0[b][j] = 0.f;
+        }
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
             const int tl = tb + (WT / 64) * b;
@@ -298,12 +343,26 @@ __device__ __forceinline__ float walk_pass(WalkShared &W, const AcceptParams &a,
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int x = tl * kTile + lane + 64 * j;
-                if (x < V)
-                    s += zpass ? walk_adj(a, W, krej, p0[b][j], q0[b][j], x) : walk_val(a, W, krej, p0[b][j], q0[b][j], x);
+                const float v = ZPASS ? walk_adj(a, W, krej, p0[b][j], q0[b][j], x)
+                                      : walk_val(a, W, krej, p0[b][j], q0[b][j], x);
+                s += x < V ? v : 0.f;
             }
             s = wave_sum(s);
             if (lane == 0) W.tsum[tl] = s;
         }
+    }
+}
+__device__ __forceinline__ float walk_pass(WalkShared &W, const AcceptParams &a, int node, int krej, bool zpass) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ntiles = (a.V + kTile - 1) / kTile;
+    const int qm = !(zpass || krej > 0) ? 0 : a.q_map ? 2 : 1;
+    if (zpass) {
+        if (qm == 2) walk_tiles<true, 2>(W, a, node, krej);
+        else walk_tiles<true, 1>(W, a, node, krej);
+    } else {
+        if (qm == 0) walk_tiles<false, 0>(W, a, node, krej);
+        else if (qm == 2) walk_tiles<false, 2>(W, a, node, krej);
+        else walk_tiles<false, 1>(W, a, node, krej);
     }
     __syncthreads();
     if (wave == 0) {
@@ -366,6 +425,13 @@ template <typename F> __device__ __forceinline__ int walk_search(const WalkShare
 __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     __shared__ WalkShared W;
     const int t = threadIdx.x;
+    for (int i = t; i < a.n; i += WT) {
+        W.par[i] = a.parents[i];
+        W.tok[i] = a.tokens[i];
+        W.qrow[i] = a.q_row_of[i];
+        W.uni[i] = a.uniforms[i];
+        W.rs[i] = a.row_s[i];
+    }
     if (t == 0) {
         W.node = 0;
         W.used = 0;
@@ -384,7 +450,7 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
         if (t == 0) {
             W.go = 0;  // 0: descend done / 1: sample at node / 2: normaliser pass needed / 3: stop
             const int node = W.node;
-            const float S = a.row_s[node];
+            const float S = W.rs[node];
             if (!a.greedy && (!(S > 0.f) || !isfinite(S))) {
                 W.status = ACC_ERR_SOFTMAX;
                 W.go = 3;
@@ -395,13 +461,13 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                 int seen = 0;  // children already tested at this node (= krej)
                 int accepted = -1;
                 for (; c < a.n; c++) {
-                    if (a.parents[c] != node) continue;
+                    if (W.par[c] != node) continue;
                     if (seen++ < W.krej) continue;
-                    const float u = a.uniforms[W.used++];
-                    const int tok = a.tokens[c];
+                    const float u = W.uni[W.used++];
+                    const int tok = W.tok[c];
                     const float p = walk_p(a, W, node, W.krej, tok);
                     if (W.krej == 0) W.R[0] = 1.f;
-                    const float q = walk_q(a, W, accept_q(a, a.q_row_of[node], tok), W.krej, tok);
+                    const float q = walk_q(a, W, accept_q(a, W.qrow[node], tok), W.krej, tok);
                     // modified_rejection_step (vanilla.rs:59-73)
                     const bool acc = q <= 0.f || u <= fminf(p / q, 1.f);
                     if (acc) {
@@ -411,7 +477,7 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                     W.go = 2;  // rejected: the adjusted distribution's normaliser is needed
                     if (W.krej < MAX_REJ) {
                         W.rej[W.krej] = tok;
-                        if (W.krej + 1 < MAX_REJ) W.R[W.krej + 1] = W.R[W.krej] - accept_q(a, a.q_row_of[node], tok);
+                        if (W.krej + 1 < MAX_REJ) W.R[W.krej + 1] = W.R[W.krej] - accept_q(a, W.qrow[node], tok);
                     }
                     break;
                 }
@@ -422,7 +488,7 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                     W.go = 0;
                 } else if (W.go != 2) {
                     W.go = 1;  // no child left to test (or a leaf): final draw
-                    W.u = a.uniforms[W.used++];
+                    W.u = W.uni[W.used++];
                 }
             }
         }
@@ -484,6 +550,7 @@ void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float in
 
 void launch_accept_walk(const AcceptParams &a, hipStream_t st) {
     if (a.V > kMaxTiles * kTile) throw BackendError("acceptance: vocabulary too large");
+    if (a.n < 1 || a.n > kMaxNodes) throw BackendError("acceptance: too many tree nodes");
     hipLaunchKernelGGL(k_accept_walk, dim3(1), dim3(WT), 0, st, a);
 }
 

@@ -76,12 +76,13 @@ Model::~Model() {
                     (void *)hidden_out, (void *)last_row, (void *)part_o, (void *)part_ml, (void *)amax_v,
                     (void *)collect_buf, (void *)amax_i, (void *)argmax, (void *)d_ids,
                     (void *)d_src, (void *)xp, (void *)ap, (void *)act, (void *)q16,
-                    (void *)acc_m, (void *)acc_s, (void *)acc_u, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
+                    (void *)acc_m, (void *)acc_s, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
                     (void *)aux_ids, (void *)ssq, (void *)split_cnt, (void *)acc_part, (void *)acc_cnt,
                     (void *)acc_prob})
         F(p);
     if (h_stage) hipHostFree(h_stage);
+    if (acc_stage) hipHostFree(acc_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
     for (hipEvent_t e : ev_pool) hipEventDestroy(e);
     if (st) hipStreamDestroy(st);
@@ -142,8 +143,7 @@ void Model::alloc_buffers() {
     acc_m = dalloc<float>(Mx);
     acc_s = dalloc<float>(Mx);
     acc_am = dalloc<int>(Mx);
-    acc_u = dalloc<float>(Mx);
-    acc_tree = dalloc<int>((size_t)3 * Mx);
+    acc_tree = dalloc<int>((size_t)4 * Mx);  // parents | tokens | q_row_of | uniforms of one walk
     acc_out = dalloc<int>((size_t)Mx + 4);
     acc_part = dalloc<uint64_t>((size_t)Mx * 2 * kRowStatsMaxSlices);
     acc_cnt = dalloc<int>(Mx);
@@ -153,6 +153,7 @@ void Model::alloc_buffers() {
     aux_ids = dalloc<int>(kAuxRows);
     h_stage_bytes = (size_t)Mx * (3 * sizeof(int) + 2 * sizeof(uint64_t)) + 256;
     SD_HIP_CHECK(hipHostMalloc((void **)&h_stage, h_stage_bytes, hipHostMallocDefault));
+    SD_HIP_CHECK(hipHostMalloc((void **)&acc_stage, ((size_t)5 * Mx + 8) * sizeof(int), hipHostMallocDefault));
     SD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev, hipEventDisableTiming));
 }
 
@@ -1318,13 +1319,15 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
         SD_HIP_CHECK(hipMalloc((void **)&m.acc_prob, pn * sizeof(float) + 256));
         m.acc_prob_cap = pn;
     }
-    // parents | tokens | q_row_of, uniforms and draft rows: one copy each
-    std::vector<int> tree((size_t)3 * n);
-    std::memcpy(tree.data(), parents, n * sizeof(int));
-    std::memcpy(tree.data() + n, tokens, n * sizeof(int));
-    std::memcpy(tree.data() + 2 * n, q_row_of, n * sizeof(int));
-    SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, tree.data(), tree.size() * sizeof(int), hipMemcpyHostToDevice, m.st));
-    SD_HIP_CHECK(hipMemcpyAsync(m.acc_u, uniforms, n * sizeof(float), hipMemcpyHostToDevice, m.st));
+    // parents | tokens | q_row_of | uniforms through the pinned acceptance
+    // stage in one copy (the previous walk synchronised before returning, so
+    // the stage is free), the draft rows in another unless on the device
+    int *in = m.acc_stage;
+    std::memcpy(in, parents, n * sizeof(int));
+    std::memcpy(in + n, tokens, n * sizeof(int));
+    std::memcpy(in + 2 * n, q_row_of, n * sizeof(int));
+    std::memcpy(in + 3 * n, uniforms, n * sizeof(float));
+    SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, in, (size_t)4 * n * sizeof(int), hipMemcpyHostToDevice, m.st));
     if (qn && !q_on_device)
         SD_HIP_CHECK(hipMemcpyAsync(m.acc_q, q_rows, qn * sizeof(float), hipMemcpyHostToDevice, m.st));
     const bool greedy = temperature == 0.f;
@@ -1348,14 +1351,14 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     a.q = q_on_device ? q_rows : m.acc_q;
     a.q_ld = (int64_t)q_vocab;
     a.q_map = q_vocab == (size_t)c.vocab ? nullptr : m.t2d_inv;
-    a.uniforms = m.acc_u;
+    a.uniforms = (const float *)(m.acc_tree + 3 * n);
     a.max_commit = (int)max_commit;
     a.wor = wor;
     a.out_path = m.acc_out + 4;
     a.out_info = m.acc_out;
     launch_accept_walk(a, m.st);
-    std::vector<int> out((size_t)n + 4);
-    SD_HIP_CHECK(hipMemcpyAsync(out.data(), m.acc_out, out.size() * sizeof(int), hipMemcpyDeviceToHost, m.st));
+    int *out = m.acc_stage + 4 * c.max_batch;
+    SD_HIP_CHECK(hipMemcpyAsync(out, m.acc_out, ((size_t)n + 4) * sizeof(int), hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
     const int status = out[3];
     if (status == ACC_ERR_SOFTMAX) throw SamplingError("softmax produced a non-positive or non-finite sum");
@@ -1363,7 +1366,7 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     if (status != ACC_OK) throw SamplingError("acceptance walk: too many rejections at one node");
     const int plen = out[0];
     if (plen < 1 || plen > n) throw BackendError("acceptance walk: bad path length");
-    path.assign(out.begin() + 4, out.begin() + 4 + plen);
+    path.assign(out + 4, out + 4 + plen);
     fin = out[1];
     used = (size_t)out[2];
 }

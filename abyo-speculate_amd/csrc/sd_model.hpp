@@ -151,7 +151,7 @@ class Model {
     }
     // rejection-sampling acceptance: per-row softmax statistics, the tree,
     // draft rows, uniforms and results (draft rows grow on demand)
-    float *acc_m = nullptr, *acc_s = nullptr, *acc_u = nullptr, *acc_q = nullptr;
+    float *acc_m = nullptr, *acc_s = nullptr, *acc_q = nullptr;
     size_t acc_q_cap = 0;  // floats
     uint64_t *acc_part = nullptr;  // row statistics' per-slice partials
     int *acc_cnt = nullptr;        // their per-row arrival counts (zero between launches)
@@ -174,6 +174,7 @@ class Model {
     int *aux_ids = nullptr;
     // pinned staging for small H2D transfers
     int *h_stage = nullptr;
+    int *acc_stage = nullptr;  // pinned: a walk's inputs [4 max_batch] and outputs [max_batch + 4]
     size_t h_stage_bytes = 0;
     hipEvent_t stage_ev = nullptr;  // recorded after the last copy out of h_stage
     void stage_wait();               // host waits until h_stage may be rewritten

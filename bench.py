@@ -123,6 +123,18 @@ def timed_leg(dec, step, args):
     return t, prof, acc / args.steps
 
 
+def wall_per_step(dec, step, args):
+    """Seconds per step of step() (warm-up, then the leg's step count), no profile."""
+    for _ in range(args.warmup):
+        step()
+    dec.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dec.synchronize()
+    return (time.perf_counter() - t0) / args.steps
+
+
 def leg_summary(t, prof, tokens_per_step, extra):
     g = gemm_rows(prof, ("qkv", "wo", "gate_up", "down", "lm_head"))
     b = sum(e[1] for e in g)
@@ -373,7 +385,16 @@ def main():
         q_d = draft_rows(erng, ne, Vd)
         u = [float(x) for x in erng.random(ne, dtype=np.float32)]
 
+        # the draft rows stay on the device, where a GPU draft model leaves them
+        q_dev = S.DeviceArray(q_d)
+
         def step_e3():
+            path, tok, used = dec.verify_rejection_tree_device(etree, q_dev.ptr, ne, Vd, list(range(ne)), u, 1.0)
+            dec.commit_tree_path(etree, path)
+            dec.rollback_to(n1)
+            return len(path)
+
+        def step_e3_host():
             path, tok, used = dec.verify_rejection_tree(etree, q_d, list(range(ne)), u, 1.0)
             dec.commit_tree_path(etree, path)
             dec.rollback_to(n1)
@@ -381,12 +402,16 @@ def main():
 
         log(f"EAGLE-3 verify: {ne}-node tree at KV {EAGLE3_PREFIX}, d2t {Vd} -> {cfg.vocab}, rejection at T=1")
         t_e3, eprof, plen = timed_leg(dec, step_e3, args)
-        log(f"EAGLE-3 verify: {t_e3 * 1e6:.1f} us/step")
+        t_e3h = wall_per_step(dec, step_e3_host, args)
+        q_dev.close()
+        log(f"EAGLE-3 verify: {t_e3 * 1e6:.1f} us/step (draft rows uploaded per step: {t_e3h * 1e6:.1f})")
         result["eagle3_tree64"] = leg_summary(
             t_e3, eprof, plen,
             {"nodes": ne, "kv_positions": EAGLE3_PREFIX, "draft_vocab": Vd,
+             "us_host_draft_rows": round(t_e3h * 1e6, 1),
              "what": "tree forward (K1 M=64, tree attention over 8192 positions), rejection walk over the d2t-mapped "
-                     "draft rows (64 x 32000 f32 uploaded per step), compaction of the accepted path"})
+                     "draft rows (64 x 32000 f32 resident on the device; us_host_draft_rows: uploaded from pageable "
+                     "host memory per step), compaction of the accepted path"})
     dec.close()
 
     if not args.no_extra:
@@ -403,19 +428,38 @@ def main():
         qdrafts = [int(qrng.choice(qcfg.vocab, p=r.astype(np.float64) / r.astype(np.float64).sum())) for r in q]
         uq = [float(x) for x in qrng.random(QWEN_K + 1, dtype=np.float32)]
 
+        q_dev = S.DeviceArray(q)
+
         def step_q():
+            commits, n_acc, used = qd.verify_rejection_linear_device(qdrafts, q_dev.ptr, uq, 1.0)
+            qd.rollback_to(n0q)
+            return len(commits)
+
+        def step_q_host():
             commits, n_acc, used = qd.verify_rejection_linear(qdrafts, q, uq, 1.0)
             qd.rollback_to(n0q)
             return len(commits)
 
+        def step_q_greedy():
+            qd.verify_greedy_linear(qdrafts)
+            qd.rollback_to(n0q)
+            return 0
+
         log(f"Qwen2.5-7B verify: M={QWEN_K + 1} at KV {QWEN_PREFIX}, rejection at T=1")
         t_q, qprof, ncom = timed_leg(qd, step_q, args)
-        log(f"Qwen2.5-7B verify: {t_q * 1e6:.1f} us/step")
+        t_qh = wall_per_step(qd, step_q_host, args)
+        t_qg = wall_per_step(qd, step_q_greedy, args)
+        q_dev.close()
+        log(f"Qwen2.5-7B verify: {t_q * 1e6:.1f} us/step (draft rows uploaded per step: {t_qh * 1e6:.1f}; "
+            f"greedy acceptance: {t_qg * 1e6:.1f})")
         result["qwen7b_m9"] = leg_summary(
             t_q, qprof, ncom,
             {"M": QWEN_K + 1, "kv_positions": QWEN_PREFIX,
+             "us_host_draft_rows": round(t_qh * 1e6, 1), "us_greedy_acceptance": round(t_qg * 1e6, 1),
+             "rejection_overhead_us": round((t_q - t_qg) * 1e6, 1),
              "what": "linear verify of 8 drafts (K1 M=9 on Q5_K / Q8_0 with QKV bias), rejection walk over "
-                     "8 x 152064 f32 draft rows uploaded per step"})
+                     "8 x 152064 f32 draft rows resident on the device (us_host_draft_rows: uploaded from pageable "
+                     "host memory per step; rejection_overhead_us: over the same verify with greedy acceptance)"})
         qd.close()
 
     if not args.no_cpu:
