@@ -175,50 +175,30 @@ def measured_traffic(leg: str):
 
 
 def cpu_baseline():
-    """Oracle CPU dequant-matmul on a bounded sample, scaled to one M=5 verify step."""
+    """The CPU restatement of candle's quantised matmul path (Q8_K activations,
+    integer block dot products, AVX2, OpenMP over rows) in whole layers -- norms,
+    Q/K/V, RoPE, attention over 512 cached positions, wo, SwiGLU MLP, residuals --
+    timed on a bounded sample and scaled to one M=5 verify step."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     if not os.path.exists(O.LIB_PATH):
         import build_oracle
         build_oracle.build()
+    import cpu_baseline as CB
     cfg = O.ModelConfig(arch="llama", mix="q4_k_m", seed=SEED, ctx_len=1024, **LLAMA8B)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
-    x = np.random.default_rng(1).standard_normal((5, cfg.ffn)).astype(np.float32)
-    L = O.lib()
-
-    def prepare(layer, kind):
-        fmt, raw = O.synth_tensor(cfg, layer, kind)
-        N, K = cfg.shape(kind)
-        return fmt, raw, N, K, np.ascontiguousarray(x[:, :K]), np.empty((5, N), np.float32)
-
-    def run(mats):
-        t0 = time.perf_counter()
-        for fmt, raw, N, K, xs, y in mats:
-            L.or_qmatmul(fmt, O._p(raw), N, K, O._p(xs), 5, O._p(y))
-        return time.perf_counter() - t0
-
-    kinds = (O.K_ATTN_Q, O.K_ATTN_K, O.K_ATTN_V, O.K_ATTN_O, O.K_FFN_GATE, O.K_FFN_UP, O.K_FFN_DOWN)
-    q6 = [prepare(0, k) for k in kinds]   # layer 0: Q6_K attn_v / ffn_down
-    q4 = [prepare(4, k) for k in kinds]   # layer 4: all Q4_K
-    lm = [prepare(-1, O.K_OUTPUT)]
-    # repeat the sample until about 12 s of CPU work, report the mean per repetition
-    reps, t_q6, t_q4, t_lm = 0, 0.0, 0.0, 0.0
     t_start = time.perf_counter()
-    while reps < 2 or time.perf_counter() - t_start < CPU_SAMPLE_S:
-        t_q6 += run(q6)
-        t_q4 += run(q4)
-        t_lm += run(lm)
-        reps += 1
-    t_q6, t_q4, t_lm = t_q6 / reps, t_q4 / reps, t_lm / reps
-    log(f"cpu baseline: {reps} repetitions; Q6_K-mix layer {t_q6 * 1e3:.1f} ms, Q4_K layer {t_q4 * 1e3:.1f} ms, "
-        f"lm_head {t_lm * 1e3:.1f} ms")
-    n_q6 = sum(1 for i in range(cfg.n_layers) if O.use_more_bits(i, cfg.n_layers))
-    step_s = n_q6 * t_q6 + (cfg.n_layers - n_q6) * t_q4 + t_lm
-    return {"value": round(step_s * 1e6, 1), "unit": "us/verify (M=5)", "cores": threads, "kind": "port",
-            "sample": f"oracle C dequant-matmul (f32 dequant, f64 accumulate, OpenMP over rows) at M=5 on one "
-                      f"Q6_K-mix layer, one Q4_K layer and the Q4_K lm_head of the same synthetic weights, "
-                      f"{reps} repetitions ({time.perf_counter() - t_start:.1f} s), mean scaled to "
-                      f"{n_q6}+{cfg.n_layers - n_q6} layers + lm_head; attention and norms not included"}
+    r = CB.time_step_sample(cfg, 512, 5, CPU_SAMPLE_S)
+    log(f"cpu baseline: {r['reps']} repetitions; Q6_K-mix layer {r['q6_layer_s'] * 1e3:.1f} ms, Q4_K layer "
+        f"{r['q4_layer_s'] * 1e3:.1f} ms, lm_head {r['lm_head_s'] * 1e3:.1f} ms")
+    return {"value": round(r["step_s"] * 1e6, 1), "unit": "us/verify (M=5)", "cores": CB.threads(), "kind": "port",
+            "cpu": CB.cpu_model(),
+            "sample": f"CPU restatement of candle's CPU QMatMul path (per-row Q8_K activation quantisation, "
+                      f"integer Q4_K/Q6_K x Q8_K block dot products with f32 scaling, AVX2, OpenMP over output "
+                      f"rows) in whole layers at M=5 over 512 cached positions (f32 attention, RMSNorm, RoPE, "
+                      f"SwiGLU, residuals): one Q6_K-mix layer, one Q4_K layer and the final norm + Q4_K lm_head "
+                      f"of the same synthetic weights, {r['reps']} repetitions "
+                      f"({time.perf_counter() - t_start:.1f} s), mean scaled to {r['n_q6_layers']}+"
+                      f"{cfg.n_layers - r['n_q6_layers']} layers + lm_head"}
 
 
 def main():
