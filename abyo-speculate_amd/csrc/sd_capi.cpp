@@ -6,6 +6,7 @@
 #include "speculate_hip.h"
 #include "sd_model.hpp"
 #include "sd_common.hpp"
+#include "sd_draft.hpp"
 #include "sd_gguf.hpp"
 #include "sd_qcodes.hpp"
 #include "sd_tiles.hpp"
@@ -17,6 +18,10 @@ struct sd_model {
 
 struct sd_gguf {
     std::unique_ptr<sd::GgufFile> file;
+};
+
+struct sd_draft3 {
+    std::unique_ptr<sd::Draft3> d;
 };
 
 static thread_local std::string g_err;
@@ -680,6 +685,91 @@ sd_status sd_tree_prune(const uint32_t *tokens, const uint32_t *parents, size_t 
         std::memcpy(out_tokens, t.tokens.data(), t.size() * 4);
         std::memcpy(out_parents, t.parents.data(), t.size() * 4);
         *n_out = t.size();
+    });
+}
+
+
+/* ---- EAGLE-3 draft (crates/speculate/src/methods/eagle3.rs) ---- */
+static void need3(const sd_draft3 *d) {
+    if (!d || !d->d) throw sd::ArgError("null draft handle");
+}
+
+sd_status sd_draft3_create(const sd_draft3_config *cfg, sd_draft3 **out) {
+    return guard([&] {
+        if (!cfg || !out) throw sd::ArgError("null argument");
+        *out = nullptr;
+        sd::Draft3Cfg c;
+        c.hidden = cfg->hidden;
+        c.n_heads = cfg->n_heads;
+        c.n_kv_heads = cfg->n_kv_heads;
+        c.ffn = cfg->ffn;
+        c.draft_vocab = cfg->draft_vocab;
+        c.target_vocab = cfg->target_vocab;
+        c.rms_eps = cfg->rms_eps;
+        c.rope_theta = cfg->rope_theta;
+        c.max_pos = cfg->max_pos;
+        c.device = cfg->device;
+        auto h = std::make_unique<sd_draft3>();
+        h->d = std::make_unique<sd::Draft3>(c);
+        *out = h.release();
+    });
+}
+
+void sd_draft3_destroy(sd_draft3 *d) { delete d; }
+
+size_t sd_draft3_tensor_bytes(const sd_draft3 *d, int32_t kind) {
+    if (!d || !d->d || kind < 0 || kind >= sd::D3_NUM) return 0;
+    return d->d->tensor_bytes(kind);
+}
+
+sd_status sd_draft3_set_tensor(sd_draft3 *d, int32_t kind, const void *data, size_t bytes) {
+    return guard([&] {
+        need3(d);
+        d->d->set_tensor(kind, data, bytes);
+    });
+}
+
+sd_status sd_draft3_get_tensor(const sd_draft3 *d, int32_t kind, void *data, size_t bytes) {
+    return guard([&] {
+        need3(d);
+        if (!data) throw sd::ArgError("null data");
+        d->d->get_tensor(kind, data, bytes);
+    });
+}
+
+sd_status sd_draft3_synthesize(sd_draft3 *d, uint64_t seed, float weight_std) {
+    return guard([&] {
+        need3(d);
+        d->d->synthesize(seed, weight_std);
+    });
+}
+
+sd_status sd_draft3_reset(sd_draft3 *d) {
+    return guard([&] {
+        need3(d);
+        d->d->reset();
+    });
+}
+
+sd_status sd_draft3_forward(sd_draft3 *d, const float *hidden_in, size_t n_in, const float *input_emb,
+                            size_t position, float *out_hidden, float *out_logits) {
+    return guard([&] {
+        need3(d);
+        if (!hidden_in || !input_emb) throw sd::ArgError("null argument");
+        if (position > (size_t)INT32_MAX) throw sd::ArgError("position out of range");
+        d->d->step_host(hidden_in, n_in, input_emb, (int)position, out_hidden, out_logits);
+    });
+}
+
+sd_status sd_draft3_round(sd_draft3 *d, sd_model *m, const uint32_t *layers, size_t depth, const int32_t *top_k,
+                          int32_t *target_ids, int32_t *draft_ids, float *log_probs) {
+    return guard([&] {
+        need3(d);
+        need_weights(m);
+        if (!layers || !top_k || !target_ids || !draft_ids || !log_probs) throw sd::ArgError("null argument");
+        if (depth < 1 || depth > (size_t)sd::kDraftMaxSteps) throw sd::ArgError("draft depth out of range");
+        setdev(m);
+        d->d->round(*m->model, *m->dec, layers, (int)depth, top_k, target_ids, draft_ids, log_probs);
     });
 }
 

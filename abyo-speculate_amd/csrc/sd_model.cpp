@@ -130,7 +130,9 @@ void Model::alloc_buffers() {
     amax_v = dalloc<float>((size_t)Mx * amax_ld);
     amax_i = dalloc<int>((size_t)Mx * amax_ld);
     argmax = dalloc<int>(Mx);
-    collect_buf = dalloc<float>((size_t)c.n_layers * c.hidden);
+    // rows of last_hidden_states_multi: one per requested layer, repeats allowed
+    collect_cap = std::max(c.n_layers, 16);
+    collect_buf = dalloc<float>((size_t)collect_cap * c.hidden);
     // ids | pos | (unused) | mask in one block laid out as the pinned staging
     // buffer, so that one copy uploads a forward's inputs
     d_ids = dalloc<int>((size_t)3 * Mx + (Mx & 1) + (size_t)4 * Mx);
@@ -193,6 +195,7 @@ static DevTensor &slot(Model &m, int layer, int kind) {
 }
 
 void Model::set_tensor(int layer, int kind, int fmt, const void *host, size_t bytes) {
+    fwd_count++;
     DevTensor &t = slot(*this, layer, kind);
     int rows, K;
     tensor_shape(cfg, kind, rows, K);
@@ -291,6 +294,7 @@ static int mix_fmt(int mix, int n_layers, int layer, int kind) {
 }
 
 void Model::synthesize(int mix, uint64_t seed, float stdv) {
+    fwd_count++;
     SD_HIP_CHECK(hipSetDevice(cfg.device));
     const float mult = (float)((double)stdv * std::sqrt(3.0) / 65536.0);
     auto make = [&](int layer, int kind) {
@@ -336,6 +340,7 @@ void Model::synthesize(int mix, uint64_t seed, float stdv) {
 }
 
 void Model::fill_kv_synthetic(int P, uint64_t seed) {
+    fwd_count++;
     if (P < 0 || P > cfg.ctx_len) throw ArgError("prefix longer than the KV capacity");
     const float mult = (float)(std::sqrt(3.0) / 65536.0);
     launch_fill_kv(kv, cfg.n_layers, cfg.n_kv_heads, cap, cfg.head_dim, P, seed, mult, st);
@@ -546,6 +551,7 @@ GemmParams Model::bench_params(int layer, int kind, int M, double *bytes_out) {
 
 void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P,
                     int logits_mode, bool want_hidden, const std::vector<int> &collect, float *collect_out) {
+    fwd_count++;
     const ModelCfg &c = cfg;
     if (M < 1 || M > c.max_batch) throw ArgError("forward: M out of range");
     if (P + M > c.ctx_len) throw ArgError("forward: KV capacity exceeded");
@@ -780,7 +786,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         launch_argmax_reduce(amax_v, amax_i, p.amax_ld, rows, argmax, st);
         logits_rows_last = rows;
     }
-    if (!collect.empty()) {
+    if (!collect.empty() && collect_out) {
         SD_HIP_CHECK(hipMemcpyAsync(collect_out, collect_buf, collect.size() * H * 4, hipMemcpyDeviceToHost, st));
     }
 }
@@ -830,6 +836,7 @@ void Model::embed_rows(const int *ids, int n, float *out_host) {
 }
 
 void Model::compact_tail(int P, const std::vector<int> &src) {
+    fwd_count++;
     const int n = (int)src.size();
     if (n == 0) return;
     SD_HIP_CHECK(hipSetDevice(cfg.device));
@@ -923,6 +930,7 @@ void Decoder::reset() {
     history.clear();
     cache_len = 0;
     last_valid = false;
+    collect_hist = 0;
 }
 
 void Decoder::truncate(size_t len) {
@@ -953,8 +961,9 @@ void Decoder::forward_advance(const uint32_t *tokens, size_t n, bool all_rows) {
         pos.resize(M);
         for (int i = 0; i < M; i++) pos[i] = cache_len + i;
         causal_masks(M, mw, nw);
+        const bool keep = n == 1 && !collect_keep.empty();
         m.forward(ids.data(), pos.data(), mw.data(), nw, M, cache_len, last_chunk ? (all_rows ? 2 : 1) : 0, false,
-                  {}, nullptr);
+                  keep ? collect_keep : std::vector<int>{}, nullptr);
         cache_len += M;
         done += M;
     }
@@ -968,6 +977,10 @@ void Decoder::observe(const uint32_t *ids, size_t n) {
     if (n == 0) return;
     forward_advance(ids, n, false);
     history.insert(history.end(), ids, ids + n);
+    if (n == 1 && !collect_keep.empty()) {
+        collect_hist = history.size();
+        collect_fwd = model->fwd_count;
+    }
     SD_HIP_CHECK(hipStreamSynchronize(model->st));
 }
 
@@ -1140,6 +1153,7 @@ void Decoder::observe_returning_last_hidden(const uint32_t *ids, size_t n, float
 void Decoder::last_hidden_states_multi(const uint32_t *layers, size_t nl, float *out_final, float *out_layers) {
     if (history.empty()) throw SamplingError("last_hidden_states_multi with empty history");
     Model &m = *model;
+    if (nl > (size_t)m.collect_cap) throw ArgError("too many collected layers");
     std::vector<int> col(nl);
     for (size_t i = 0; i < nl; i++) {
         if (layers[i] >= (uint32_t)m.cfg.n_layers)
@@ -1154,10 +1168,44 @@ void Decoder::last_hidden_states_multi(const uint32_t *layers, size_t nl, float 
     std::vector<float> tmp(nl * (size_t)m.cfg.hidden);
     m.forward(&id, &pos, &mk, 1, 1, cache_len, 0, true, col, tmp.data());
     cache_len += 1;
+    collect_keep = col;
+    collect_hist = history.size();
+    collect_fwd = m.fwd_count;
     if (out_final)
         SD_HIP_CHECK(hipMemcpyAsync(out_final, m.hidden_out, (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
     if (out_layers) std::memcpy(out_layers, tmp.data(), tmp.size() * 4);
+}
+
+// last_hidden_states_multi with the rows left on the device: [nl][hidden] f32
+// in collect_buf, ready on the model's stream (the caller does not wait)
+const float *Decoder::collect_hidden_device(const uint32_t *layers, size_t nl) {
+    if (history.empty()) throw SamplingError("last_hidden_states_multi with empty history");
+    Model &m = *model;
+    if (nl > (size_t)m.collect_cap) throw ArgError("too many collected layers");
+    std::vector<int> col(nl);
+    for (size_t i = 0; i < nl; i++) {
+        if (layers[i] >= (uint32_t)m.cfg.n_layers)
+            throw BackendError("collect_layers[" + std::to_string(i) + "] = " + std::to_string(layers[i]) +
+                               " out of range (n_layers=" + std::to_string(m.cfg.n_layers) + ")");
+        col[i] = (int)layers[i];
+    }
+    // the rows of this token from the one-token forward that appended it
+    // (observe) or from the last collection: the same M=1 forward at the same
+    // position over the same cache, so the same values
+    if (collect_hist == history.size() && collect_fwd == m.fwd_count && collect_keep == col &&
+        cache_len == (int)history.size())
+        return m.collect_buf;
+    const uint32_t last = history.back();
+    truncate(history.size() - 1);
+    int id = (int)last, pos = cache_len;
+    uint64_t mk = 1;
+    m.forward(&id, &pos, &mk, 1, 1, cache_len, 0, true, col, nullptr);
+    cache_len += 1;
+    collect_keep = col;
+    collect_hist = history.size();
+    collect_fwd = m.fwd_count;
+    return m.collect_buf;
 }
 
 // ---- device acceptance -----------------------------------------------------

@@ -137,6 +137,8 @@ class Model {
     float *cos_t = nullptr, *sin_t = nullptr;
     float *h = nullptr, *qkv = nullptr, *logits = nullptr, *hidden_out = nullptr, *last_row = nullptr;
     float *part_o = nullptr, *part_ml = nullptr, *amax_v = nullptr, *collect_buf = nullptr;
+    int collect_cap = 0;     // rows of collect_buf
+    uint64_t fwd_count = 0;  // forwards, weight and cache writes so far (the collected rows' validity stamp)
     int *split_cnt = nullptr;  // attention's per-tile split arrival counts (zero between launches)
     int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
     uint64_t *d_mask = nullptr;
@@ -180,11 +182,12 @@ class Model {
     void stage_wait();               // host waits until h_stage may be rewritten
     void stage_done();
 
+    // token table in GGUF row order (F32 tables are row-major either way)
+    const uint8_t *embed_table() const { return gw[K_TOK_EMBD].fmt == F32 ? gw[K_TOK_EMBD].d : gw[K_TOK_EMBD].gguf; }
+
   private:
     void alloc_buffers();
     void run_gemm(GemmParams &p, int cls, double bytes);
-    // token table in GGUF row order (F32 tables are row-major either way)
-    const uint8_t *embed_table() const { return gw[K_TOK_EMBD].fmt == F32 ? gw[K_TOK_EMBD].d : gw[K_TOK_EMBD].gguf; }
     uint16_t *kc(int layer) const { return kv + (int64_t)layer * 2 * cfg.n_kv_heads * cap * cfg.head_dim; }
     uint16_t *vc(int layer) const { return kc(layer) + (int64_t)cfg.n_kv_heads * cap * cfg.head_dim; }
 };
@@ -212,6 +215,15 @@ class Decoder {
     void last_hidden_state(float *out);
     void observe_returning_last_hidden(const uint32_t *ids, size_t n, float *out);
     void last_hidden_states_multi(const uint32_t *layers, size_t nl, float *out_final, float *out_layers);
+    const float *collect_hidden_device(const uint32_t *layers, size_t nl);
+    // The layers of the last collection; a one-token observe collects them
+    // as it goes, so that the next collection for that token (the EAGLE-3
+    // round after the bonus token's observe) reads them instead of running
+    // the same M=1 forward again.  Valid while the history length and the
+    // model's forward count are the ones recorded.
+    std::vector<int> collect_keep;
+    size_t collect_hist = 0;
+    uint64_t collect_fwd = 0;
 
     // device acceptance
     void verify_greedy_linear(const uint32_t *drafts, size_t k, uint32_t *commits, size_t *n_commit,

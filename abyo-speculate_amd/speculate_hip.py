@@ -91,6 +91,19 @@ class Config:
         return SdConfig(**{k: getattr(self, k) for k, _ in SdConfig._fields_})
 
 
+class Draft3Config(ctypes.Structure):
+    """sd_draft3_config: Eagle3DraftConfig (crates/speculate/src/methods/eagle3.rs:88-120)"""
+    _fields_ = [("hidden", ctypes.c_int32), ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
+                ("ffn", ctypes.c_int32), ("draft_vocab", ctypes.c_int32), ("target_vocab", ctypes.c_int32),
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("max_pos", ctypes.c_int32),
+                ("device", ctypes.c_int32)]
+
+
+# tensor kinds of sd_draft3_set_tensor (the checkpoint's names, eagle3.rs:133-152, 411-425)
+D3_FC, D3_Q, D3_K, D3_V, D3_O, D3_GATE, D3_UP, D3_DOWN, D3_LM_HEAD = range(9)
+D3_INPUT_NORM, D3_HIDDEN_NORM, D3_POST_NORM, D3_NORM, D3_D2T = range(9, 14)
+DRAFT3_MAX_STEPS, DRAFT3_MAX_TOPK = 16, 8
+
 _lib = None
 
 
@@ -165,6 +178,15 @@ def load_library(path: str = LIB_PATH):
         "sd_gguf_tensor_count": ([P], SZ),
         "sd_gguf_tensor_info": ([P, ctypes.c_char_p, P, P, P, P], I32),
         "sd_model_load_gguf": ([P, P], I32),
+        "sd_draft3_create": ([ctypes.POINTER(Draft3Config), ctypes.POINTER(P)], I32),
+        "sd_draft3_destroy": ([P], None),
+        "sd_draft3_tensor_bytes": ([P, I32], SZ),
+        "sd_draft3_set_tensor": ([P, I32, P, SZ], I32),
+        "sd_draft3_get_tensor": ([P, I32, P, SZ], I32),
+        "sd_draft3_synthesize": ([P, U64, ctypes.c_float], I32),
+        "sd_draft3_reset": ([P], I32),
+        "sd_draft3_forward": ([P, P, SZ, P, SZ, P, P], I32),
+        "sd_draft3_round": ([P, P, P, SZ, P, P, P, P], I32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -657,6 +679,92 @@ class HipQuantDecoder:
 
 
 # ---- draft-tree builders (host only) ----
+def default_layers_for(n_layers: int) -> List[int]:
+    """Eagle3RunConfig::default_layers_for (eagle3.rs:540-546): [1, n/2 - 1, n - 4]"""
+    return [0, 0, 0] if n_layers < 4 else [1, n_layers // 2 - 1, n_layers - 4]
+
+
+class HipEagle3Draft:
+    """Eagle3DraftCandle (crates/speculate/src/methods/eagle3.rs:307-516) resident
+    on one GPU: f16 tensors, the draft's own KV cache (at most 16 steps between
+    resets), and a whole draft round of run_eagle3 (:598-673) on the device."""
+
+    def __init__(self, hidden: int = 4096, n_heads: int = 32, n_kv_heads: int = 8, ffn: int = 14336,
+                 draft_vocab: int = 32000, target_vocab: int = 128256, rms_eps: float = 1e-5,
+                 rope_theta: float = 500000.0, max_pos: int = 2048, device: int = 0):
+        load_library()
+        self.hidden, self.draft_vocab, self.target_vocab = hidden, draft_vocab, target_vocab
+        c = Draft3Config(hidden, n_heads, n_kv_heads, ffn, draft_vocab, target_vocab, rms_eps, rope_theta, max_pos,
+                         device)
+        self._h = ctypes.c_void_p()
+        _check(_lib.sd_draft3_create(ctypes.byref(c), ctypes.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.sd_draft3_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor_bytes(self, kind: int) -> int:
+        return int(_lib.sd_draft3_tensor_bytes(self._h, kind))
+
+    def set_tensor(self, kind: int, data: np.ndarray):
+        """weights [out][in] and norms [hidden] as f16; D3_D2T as int64 [draft_vocab]"""
+        a = np.ascontiguousarray(data, np.int64 if kind == D3_D2T else np.float16)
+        _check(_lib.sd_draft3_set_tensor(self._h, kind, _ptr(a), a.nbytes))
+
+    def get_tensor(self, kind: int) -> np.ndarray:
+        n = self.tensor_bytes(kind)
+        a = np.empty(n // (8 if kind == D3_D2T else 2), np.int64 if kind == D3_D2T else np.float16)
+        _check(_lib.sd_draft3_get_tensor(self._h, kind, _ptr(a), a.nbytes))
+        return a
+
+    def synthesize(self, seed: int, std: float = 0.02):
+        _check(_lib.sd_draft3_synthesize(self._h, seed, std))
+
+    def reset(self):
+        _check(_lib.sd_draft3_reset(self._h))
+
+    def forward_hidden(self, hidden_states: np.ndarray, input_emb: np.ndarray, position: int,
+                       want_logits: bool = True):
+        """forward_hidden (:433-450) + apply_norm_lm_head (:451-454): hidden_states
+        of 3 * hidden (fc applied) or hidden; -> (pre-norm midlayer output
+        [hidden], draft logits [draft_vocab] or None), both f16 values as f32"""
+        h = np.ascontiguousarray(hidden_states, np.float32).reshape(-1)
+        e = np.ascontiguousarray(input_emb, np.float32).reshape(-1)
+        if e.size != self.hidden:
+            raise ArgError("input_emb must be hidden wide")
+        out = np.empty(self.hidden, np.float32)
+        lg = np.empty(self.draft_vocab, np.float32) if want_logits else None
+        _check(_lib.sd_draft3_forward(self._h, _ptr(h), h.size, _ptr(e), position, _ptr(out), _ptr(lg)))
+        return out, lg
+
+    def round(self, target: "HipQuantDecoder", layers: Sequence[int], depth: int, top_k) \
+            -> Tuple[List[List[int]], List[List[float]], List[List[int]]]:
+        """The draft half of one run_eagle3 iteration (:598-673) against target:
+        -> (per-step top-k target ids, their log-probs, their draft ids)"""
+        ks = [int(top_k)] * depth if np.isscalar(top_k) else [int(k) for k in top_k]
+        if len(ks) != depth:
+            raise ArgError("one top_k per draft step")
+        lay = _u32(layers)
+        if lay.size != 3:
+            raise SamplingError(f"EAGLE-3 expects 3 layers, got {lay.size}")
+        k = np.asarray(ks, np.int32)
+        ids = np.zeros((max(depth, 1), DRAFT3_MAX_TOPK), np.int32)
+        dids = np.zeros_like(ids)
+        lps = np.zeros(ids.shape, np.float32)
+        _check(_lib.sd_draft3_round(self._h, target._h, _ptr(lay), depth, _ptr(k), _ptr(ids), _ptr(dids),
+                                    _ptr(lps)))
+        return ([[int(v) for v in ids[s, :ks[s]]] for s in range(depth)],
+                [[float(v) for v in lps[s, :ks[s]]] for s in range(depth)],
+                [[int(v) for v in dids[s, :ks[s]]] for s in range(depth)])
+
+
 def tree_cartesian(root: int, head_top_k: Sequence[Sequence[int]]) -> Tuple[np.ndarray, np.ndarray]:
     """build_cartesian_tree (methods/medusa.rs:172-193) -> (tokens, parents)."""
     L = load_library()

@@ -214,7 +214,8 @@ def main():
         __graft_entry__.build()
     S.load_library()
 
-    ctx = max(args.prefix + 8, args.tree_prefix + 64, 0 if args.no_extra else EAGLE3_PREFIX + 72) + 64
+    ctx = max(args.prefix + 8, args.tree_prefix + 64,
+              0 if args.no_extra else EAGLE3_PREFIX + 72 + 8 * (args.steps + args.warmup)) + 64
     cfg = S.Config(arch=S.ARCH_LLAMA, ctx_len=ctx, max_batch=64, **LLAMA8B)
     log(f"creating decoder (ctx {ctx}) and synthesising Q4_K_M weights")
     dec = S.HipQuantDecoder(cfg)
@@ -392,6 +393,59 @@ def main():
              "what": "tree forward (K1 M=64, tree attention over 8192 positions), rejection walk over the d2t-mapped "
                      "draft rows (64 x 32000 f32 resident on the device; us_host_draft_rows: uploaded from pageable "
                      "host memory per step), compaction of the accepted path"})
+
+        # ---------------- EAGLE-3 draft round on the device (the producer of that tree) ----------------
+        log("EAGLE-3 draft: LLaMA3.1-8B-shaped f16 draft (hidden 4096, FFN 14336, 32000-token head), synthesised")
+        # RoPE tables past the 8192 committed positions (the checkpoint's 2048 would end the round there)
+        dr = S.HipEagle3Draft(target_vocab=cfg.vocab, max_pos=EAGLE3_PREFIX + 64 + 8 * (args.steps + args.warmup))
+        dr.synthesize(SEED + 7, 0.02)
+        dr.set_tensor(S.D3_D2T, d2t)
+        ks = (4, 3, 2, 2, 1, 1, 1)
+        layers = S.default_layers_for(cfg.n_layers)
+
+        def step_draft():
+            ids, lp, _ = dr.round(dec, layers, len(ks), list(ks))
+            return len(ids)
+
+        # the first round computes the committed token's rows (an M=1 forward over 8192 positions); from then
+        # on a one-token observe collects them as it goes, and repeated rounds at one state reuse them
+        t_dr = wall_per_step(dec, step_draft, args)
+
+        # the whole run_eagle3 iteration (eagle3.rs:586-790): draft round, Cartesian tree pruned to 64 nodes,
+        # tree verify with greedy acceptance, commit of the accepted path, observe of the bonus token
+        root = [hist[-1]]
+        grown = [0]
+
+        def step_loop():
+            ids, lp, _ = dr.round(dec, layers, len(ks), list(ks))
+            tree = S.tree_prune(S.tree_cartesian(root[0], ids), lp, 64)
+            path, bonus, _ = dec.verify_greedy_tree(tree)
+            dec.commit_tree_path(tree, path)
+            dec.observe([bonus])
+            root[0] = bonus
+            grown[0] += len(path)
+            return len(path)
+
+        t_loop = wall_per_step(dec, step_loop, args)
+        per_it = grown[0] / (args.warmup + args.steps)
+        dec.rollback_to(n1)
+        wb = sum(dr.tensor_bytes(k) for k in range(S.D3_FC + 1, S.D3_LM_HEAD + 1))
+        rb = dr.tensor_bytes(S.D3_FC) + len(ks) * wb
+        log(f"EAGLE-3 draft round: {t_dr * 1e6:.1f} us (depth {len(ks)}, top-k {ks}, layers {layers}); "
+            f"whole iteration {t_loop * 1e6:.1f} us, {per_it:.2f} tokens each")
+        result["eagle3_draft_round"] = {
+            "us": round(t_dr * 1e6, 1), "depth": len(ks), "top_k": list(ks), "layers": layers,
+            "draft_weight_bytes": int(rb),
+            "draft_weight_gbps_incl_collect": round(rb / t_dr / 1e9, 1),
+            "iteration_us": round(t_loop * 1e6, 1), "tokens_per_iteration": round(per_it, 3),
+            "iteration_tokens_per_s": round(per_it / t_loop, 1),
+            "what": "us: one draft round of run_eagle3 on the device -- the committed token's hidden states after 3 "
+                    "layers (collected by the one-token observe that appended it), 7 midlayer steps (fc on the "
+                    "first), norm + lm_head over 32000 ids, top-k, log-probs and d2t, one host copy of the results; "
+                    "iteration_us: the whole loop iteration -- that round, the Cartesian tree pruned to 64 nodes, "
+                    "tree verify over ~8200 positions with greedy acceptance, commit of the path, observe of the bonus "
+                    "(random weights: the target accepts ~nothing, so about one token per iteration)"}
+        dr.close()
     dec.close()
 
     if not args.no_extra:

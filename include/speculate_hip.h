@@ -157,7 +157,8 @@ sd_status sd_last_hidden_state(sd_model *m, float *out);
 /* TreeDecoder::observe_returning_last_hidden (quantized_llama.rs:174-191): out [hidden]. */
 sd_status sd_observe_returning_last_hidden(sd_model *m, const uint32_t *ids, size_t n, float *out);
 /* TreeDecoder::last_hidden_states_multi (quantized_llama.rs:221-250):
- * out_final [hidden], out_layers [n_layers_requested][hidden]. */
+ * out_final [hidden], out_layers [n_layers_requested][hidden].  Layers may repeat;
+ * at most max(n_layers, 16) of them (SD_ERR_ARG beyond). */
 sd_status sd_last_hidden_states_multi(sd_model *m, const uint32_t *layers, size_t n_layers, float *out_final,
                                       float *out_layers);
 /* TreeDecoder::apply_lm_head (quantized_llama.rs:112-122): hidden [rows][hidden] -> out [rows][vocab].
@@ -386,6 +387,56 @@ sd_status sd_tree_cartesian(uint32_t root, const uint32_t *cand, const uint32_t 
 sd_status sd_tree_prune(const uint32_t *tokens, const uint32_t *parents, size_t n, const float *log_probs,
                         const uint32_t *branching, size_t depth, size_t max_total, uint32_t *out_tokens,
                         uint32_t *out_parents, size_t *n_out);
+
+/* ---- EAGLE-3 draft (the draft side feeding the tree) ------------------------- */
+/* Eagle3DraftCandle (crates/speculate/src/methods/eagle3.rs:307-516) on the
+ * device: the f16 midlayer, norm + lm_head, the per-step top-k, log-probs and
+ * d2t of run_eagle3 (:598-673).  Tensors are the checkpoint's (f16, row-major
+ * [out][in]); d2t is int64 [draft_vocab]. */
+typedef struct sd_draft3 sd_draft3;
+typedef struct {
+    int32_t hidden, n_heads, n_kv_heads, ffn, draft_vocab, target_vocab;
+    float rms_eps, rope_theta;
+    int32_t max_pos; /* rows of the RoPE tables (Eagle3DraftConfig::max_position_embeddings) */
+    int32_t device;
+} sd_draft3_config;
+enum {
+    SD_D3_FC = 0, SD_D3_Q, SD_D3_K, SD_D3_V, SD_D3_O, SD_D3_GATE, SD_D3_UP, SD_D3_DOWN, SD_D3_LM_HEAD,
+    SD_D3_INPUT_NORM, SD_D3_HIDDEN_NORM, SD_D3_POST_NORM, SD_D3_NORM, SD_D3_D2T
+};
+sd_status sd_draft3_create(const sd_draft3_config *cfg, sd_draft3 **out);
+void sd_draft3_destroy(sd_draft3 *d);
+/* bytes of one tensor kind (0 for a bad handle or kind) */
+size_t sd_draft3_tensor_bytes(const sd_draft3 *d, int32_t kind);
+/* Eagle3DraftCandle::from_var_builder (:353-410): one tensor at a time */
+sd_status sd_draft3_set_tensor(sd_draft3 *d, int32_t kind, const void *data, size_t bytes);
+sd_status sd_draft3_get_tensor(const sd_draft3 *d, int32_t kind, void *data, size_t bytes);
+/* seeded synthetic weights (N(0, std) f16 matrices, norms 1 + N(0, 0.1), d2t
+ * distinct target ids): benchmarks and tests */
+sd_status sd_draft3_synthesize(sd_draft3 *d, uint64_t seed, float weight_std);
+/* Eagle3DraftCandle::reset (:416-418): clears the draft's own KV cache */
+sd_status sd_draft3_reset(sd_draft3 *d);
+/* forward_hidden (:433-450) + apply_norm_lm_head (:451-454) of one step:
+ * hidden_in f32 [n_in] with n_in = 3 * hidden (fc applied) or hidden (the
+ * previous step's output), input_emb f32 [hidden]; out_hidden [hidden] (the
+ * pre-norm midlayer output, f16 values), out_logits [draft_vocab] (f16 values)
+ * or NULL.  Appends the step to the draft's cache (at most 16 steps between
+ * resets). */
+sd_status sd_draft3_forward(sd_draft3 *d, const float *hidden_in, size_t n_in, const float *input_emb,
+                            size_t position, float *out_hidden, float *out_logits);
+/* One draft round of run_eagle3 (:598-673) against the target m, on the
+ * device with no host round trip between steps: the hidden states after
+ * `layers` (3 of them) of m's last committed token
+ * (TreeDecoder::last_hidden_states_multi), then `depth` (<= 16) steps, each
+ * embedding the current token through m's token table, running the midlayer
+ * and norm + lm_head, and taking the top top_k[s] (<= 8) draft ids by value
+ * (index ascending on ties, medusa.rs:477-487) with their log-probs
+ * l - logsumexp(l) and their d2t target ids; the top-1 target id is the next
+ * step's token.  Outputs [depth][8] each (entries past top_k[s] unset).
+ * The decoder's history and cache are as before the call.  Positions run
+ * from the history length; they must stay below max_pos (SD_ERR_ARG). */
+sd_status sd_draft3_round(sd_draft3 *d, sd_model *m, const uint32_t *layers, size_t depth, const int32_t *top_k,
+                          int32_t *target_ids, int32_t *draft_ids, float *log_probs);
 
 #ifdef __cplusplus
 }
