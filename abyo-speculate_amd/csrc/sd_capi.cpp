@@ -20,6 +20,9 @@ struct sd_gguf {
     std::unique_ptr<sd::GgufFile> file;
 };
 
+struct sd_draft2 {
+    std::unique_ptr<sd::Draft2> d;
+};
 struct sd_draft3 {
     std::unique_ptr<sd::Draft3> d;
 };
@@ -770,6 +773,91 @@ sd_status sd_draft3_round(sd_draft3 *d, sd_model *m, const uint32_t *layers, siz
         if (depth < 1 || depth > (size_t)sd::kDraftMaxSteps) throw sd::ArgError("draft depth out of range");
         setdev(m);
         d->d->round(*m->model, *m->dec, layers, (int)depth, top_k, target_ids, draft_ids, log_probs);
+    });
+}
+
+
+/* ---- EAGLE-2 draft (crates/speculate/src/methods/eagle.rs) ---- */
+static void need2(const sd_draft2 *d) {
+    if (!d || !d->d) throw sd::ArgError("null draft handle");
+}
+
+sd_status sd_draft2_create(const sd_draft2_config *cfg, sd_draft2 **out) {
+    return guard([&] {
+        if (!cfg || !out) throw sd::ArgError("null argument");
+        *out = nullptr;
+        sd::Draft2Cfg c;
+        c.hidden = cfg->hidden;
+        c.n_heads = cfg->n_heads;
+        c.n_kv_heads = cfg->n_kv_heads;
+        c.ffn = cfg->ffn;
+        c.vocab = cfg->vocab;
+        c.rms_eps = cfg->rms_eps;
+        c.rope_theta = cfg->rope_theta;
+        c.max_pos = cfg->max_pos;
+        c.device = cfg->device;
+        auto h = std::make_unique<sd_draft2>();
+        h->d = std::make_unique<sd::Draft2>(c);
+        *out = h.release();
+    });
+}
+
+void sd_draft2_destroy(sd_draft2 *d) { delete d; }
+
+size_t sd_draft2_tensor_bytes(const sd_draft2 *d, int32_t kind) {
+    if (!d || !d->d || kind < 0 || kind >= sd::D2_NUM) return 0;
+    return d->d->tensor_bytes(kind);
+}
+
+sd_status sd_draft2_set_tensor(sd_draft2 *d, int32_t kind, const void *data, size_t bytes) {
+    return guard([&] {
+        need2(d);
+        d->d->set_tensor(kind, data, bytes);
+    });
+}
+
+sd_status sd_draft2_get_tensor(const sd_draft2 *d, int32_t kind, void *data, size_t bytes) {
+    return guard([&] {
+        need2(d);
+        if (!data) throw sd::ArgError("null data");
+        d->d->get_tensor(kind, data, bytes);
+    });
+}
+
+sd_status sd_draft2_synthesize(sd_draft2 *d, uint64_t seed, float weight_std) {
+    return guard([&] {
+        need2(d);
+        d->d->synthesize(seed, weight_std);
+    });
+}
+
+sd_status sd_draft2_reset(sd_draft2 *d) {
+    return guard([&] {
+        need2(d);
+        d->d->reset();
+    });
+}
+
+sd_status sd_draft2_forward(sd_draft2 *d, const float *target_hidden, size_t n, uint32_t token, size_t position,
+                            float *out_hidden) {
+    return guard([&] {
+        need2(d);
+        if (!target_hidden) throw sd::ArgError("null argument");
+        if (n != (size_t)d->d->cfg.hidden) throw sd::ArgError("target_hidden must be hidden wide");
+        if (position > (size_t)INT32_MAX) throw sd::ArgError("position out of range");
+        d->d->step_host(target_hidden, token, (int)position, out_hidden);
+    });
+}
+
+sd_status sd_draft2_round(sd_draft2 *d, sd_model *m, const float *target_hidden, size_t depth, const int32_t *top_k,
+                          int32_t *ids, float *log_probs) {
+    return guard([&] {
+        need2(d);
+        need_weights(m);
+        if (!target_hidden || !top_k || !ids || !log_probs) throw sd::ArgError("null argument");
+        if (depth < 1 || depth > (size_t)sd::kDraftMaxSteps) throw sd::ArgError("draft depth out of range");
+        setdev(m);
+        d->d->round(*m->model, *m->dec, target_hidden, (int)depth, top_k, ids, log_probs);
     });
 }
 

@@ -101,9 +101,15 @@ __global__ __launch_bounds__(64 * kGvWaves) void k_gemv16(DraftGemv p) {
     }
     const int n = base + r;
     if (n >= p.N) return;
-    if constexpr (MODE == DG_STORE) p.y16[n] = f2h(v);
-    else if constexpr (MODE == DG_ADD) p.y16[n] = f2h(v + h2f(p.res16[n]));
-    else p.y32[n] = v;  // DG_LOGITS: the f16 logit widened
+    if constexpr (MODE == DG_STORE) {
+        p.y16[n] = f2h(v);
+    } else if constexpr (MODE == DG_ADD) {
+        const uint16_t y = f2h(v + h2f(p.res16[n]));
+        p.y16[n] = y;
+        if (p.y32) p.y32[n] = h2f(y);  // the same f16 value widened, when asked for
+    } else {
+        p.y32[n] = v;  // DG_LOGITS: the f16 logit widened
+    }
 }
 
 void launch_gemv16(int mode, const DraftGemv &p, hipStream_t st) {
@@ -172,6 +178,18 @@ void launch_rmsnorm16(const DraftNorm &p, int rows, hipStream_t st) {
     else if (per <= 16) hipLaunchKernelGGL(k_rmsnorm16<16>, g, b, 0, st, p);
     else if (per <= 32) hipLaunchKernelGGL(k_rmsnorm16<32>, g, b, 0, st, p);
     else throw BackendError("draft norm width");
+}
+
+// ---- one row of an f16 table, the row id on the device ------------------------------
+__global__ void k_gather16(const uint16_t *table, int64_t rows, int H, const int32_t *id, uint16_t *out) {
+    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    const int64_t r = *id;
+    if (i >= H || r < 0 || r >= rows) return;
+    *(uintx4 *)(out + i) = *(const uintx4 *)(table + r * H + i);
+}
+void launch_gather16(const uint16_t *table, int64_t rows, int H, const int32_t *id, uint16_t *out, hipStream_t st) {
+    if (H % 8) throw BackendError("draft gather: width must be a multiple of 8");
+    hipLaunchKernelGGL(k_gather16, dim3((H / 8 + 255) / 256), dim3(256), 0, st, table, rows, H, id, out);
 }
 
 // ---- f32 -> f16 ------------------------------------------------------------------
@@ -312,8 +330,8 @@ void launch_draft_attn(const DraftAttn &p, hipStream_t st) {
 // -inf, as the reference's sum of exp(-inf - -inf) is), lse = ln S + M, and
 // the top k of the slices' candidates.  Outputs the draft ids, l_i - lse, the
 // target ids through d2t, and the top-1 target id as the next step's token.
-constexpr int kTkT = 256, kTkPer = 4, kTkSlice = kTkT * kTkPer, kTkMaxSlices = 64;
-static_assert(kTkSlice * kTkMaxSlices >= 65536, "draft top-k slices");
+constexpr int kTkT = 256, kTkPer = 4, kTkSlice = kTkT * kTkPer, kTkMaxSlices = 256, kTkLaneSlices = kTkMaxSlices / 64;
+static_assert(kTkSlice * kTkMaxSlices >= 262144, "draft top-k slices");
 __device__ __forceinline__ bool tk_before(float v1, int i1, float v2, int i2) {
     const bool n1 = v1 != v1, n2 = v2 != v2;
     if (n1 || n2) return n1 == n2 ? i1 < i2 : n2;
@@ -414,28 +432,43 @@ __global__ __launch_bounds__(kTkT) void k_draft_topk(DraftTopk p) {
     }
     __syncthreads();
     if (!s_last || wave != 0) return;
-    // the merge, one wave: lane l holds slice l's partials
-    float cv[kDraftMaxTopk];
-    int ci[kDraftMaxTopk];
-    float m_l = -INFINITY, s_l = 0.f;
-    if (lane < nsl) {
-        int sb;
-        tk_ld64(p.part + (int64_t)lane * (1 + kDraftMaxTopk), m_l, sb);
-        s_l = __int_as_float(sb);
-    }
+    // the merge, one wave: lane l holds slices l, l + 64, ... (kTkLaneSlices of them)
+    float cv[kTkLaneSlices * kDraftMaxTopk];
+    int ci[kTkLaneSlices * kDraftMaxTopk];
+    float m_l[kTkLaneSlices], s_l[kTkLaneSlices];
 #pragma unroll
-    for (int r = 0; r < kDraftMaxTopk; r++) {
-        cv[r] = NAN;
-        ci[r] = kTkNone;
-        if (lane < nsl && r < p.k) tk_ld64(p.part + (int64_t)lane * (1 + kDraftMaxTopk) + 1 + r, cv[r], ci[r]);
-        if (ci[r] < 0 || ci[r] >= p.V) ci[r] = kTkNone;
+    for (int q = 0; q < kTkLaneSlices; q++) {
+        const int w = lane + 64 * q;
+        m_l[q] = -INFINITY;
+        s_l[q] = 0.f;
+        if (w < nsl) {
+            int sb;
+            tk_ld64(p.part + (int64_t)w * (1 + kDraftMaxTopk), m_l[q], sb);
+            s_l[q] = __int_as_float(sb);
+        }
+#pragma unroll
+        for (int r = 0; r < kDraftMaxTopk; r++) {
+            float a = NAN;
+            int b = kTkNone;
+            if (w < nsl && r < p.k) tk_ld64(p.part + (int64_t)w * (1 + kDraftMaxTopk) + 1 + r, a, b);
+            cv[q * kDraftMaxTopk + r] = a;
+            ci[q * kDraftMaxTopk + r] = (b < 0 || b >= p.V) ? kTkNone : b;
+        }
     }
-    float M = m_l;
+    float M = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kTkLaneSlices; q++) M = fmaxf(M, m_l[q]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
     float S = 0.f;  // in slice order, the same on every lane
     for (int w = 0; w < nsl; w++) {
-        const float mw = __shfl(m_l, w), sw = __shfl(s_l, w);
+        float mw = 0.f, sw = 0.f;
+#pragma unroll
+        for (int q = 0; q < kTkLaneSlices; q++)
+            if (w >> 6 == q) {
+                mw = __shfl(m_l[q], w & 63);
+                sw = __shfl(s_l[q], w & 63);
+            }
         if (mw != -INFINITY) S += sw * expf(mw - M);
     }
     if (M == -INFINITY) S = NAN;
@@ -446,7 +479,7 @@ __global__ __launch_bounds__(kTkT) void k_draft_topk(DraftTopk p) {
         float bv = NAN;
         int bi = kTkNone;
 #pragma unroll
-        for (int j = 0; j < kDraftMaxTopk; j++) {
+        for (int j = 0; j < kTkLaneSlices * kDraftMaxTopk; j++) {
             const bool elig = ci[j] != kTkNone && (li2 < 0 || tk_before(lv2, li2, cv[j], ci[j]));
             if (elig && tk_before(cv[j], ci[j], bv, bi)) {
                 bv = cv[j];
@@ -458,17 +491,18 @@ __global__ __launch_bounds__(kTkT) void k_draft_topk(DraftTopk p) {
         li2 = bi;
         if (lane == 0) {
             const bool ok = bi >= 0 && bi < p.V;
+            const int tgt = ok ? (p.d2t ? p.d2t[bi] : bi) : -1;
             p.out_draft[r] = ok ? bi : -1;
             p.out_lp[r] = ok ? bv - lse : NAN;
-            p.out_target[r] = ok ? p.d2t[bi] : -1;
-            if (r == 0) *p.next_token = ok ? p.d2t[bi] : 0;
+            p.out_target[r] = tgt;
+            if (r == 0) *p.next_token = ok ? tgt : 0;
         }
     }
 }
 void launch_draft_topk(const DraftTopk &p, hipStream_t st) {
     if (p.k < 1 || p.k > kDraftMaxTopk || p.k > p.V) throw BackendError("draft top-k: k out of range");
     const int nsl = (p.V + kTkSlice - 1) / kTkSlice;
-    if (nsl > kTkMaxSlices || !p.part || !p.cnt) throw BackendError("draft top-k: vocabulary over 65536 or no scratch");
+    if (nsl > kTkMaxSlices || !p.part || !p.cnt) throw BackendError("draft top-k: vocabulary over 262144 or no scratch");
     hipLaunchKernelGGL(k_draft_topk, dim3(nsl), dim3(kTkT), 0, st, p);
 }
 

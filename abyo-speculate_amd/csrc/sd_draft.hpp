@@ -1,7 +1,9 @@
-// EAGLE-3 draft on the device (crates/speculate/src/methods/eagle3.rs):
-// the f16 midlayer, norm + lm_head, per-step top-k / log-probs and d2t, run
-// on the target model's stream so that a whole draft round needs no host
-// round trip (sd_draft.hip holds the kernels, sd_draft.cpp this class).
+// EAGLE drafts on the device: EAGLE-3 (crates/speculate/src/methods/eagle3.rs:
+// the f16 midlayer, norm + lm_head, per-step top-k / log-probs and d2t) and
+// EAGLE-2 (methods/eagle.rs: fc over [hidden, embedding], one Llama block,
+// the target's lm_head), run on the target model's stream so that a whole
+// draft round needs no host round trip (sd_draft.hip holds the kernels,
+// sd_draft.cpp these classes).
 #pragma once
 #include <stdint.h>
 
@@ -39,6 +41,8 @@ struct DraftNorm {
     float eps;
 };
 void launch_rmsnorm16(const DraftNorm &p, int rows, hipStream_t st);
+// out[0, H) = table[*id][0, H) (f16 rows; nothing written for an id out of range)
+void launch_gather16(const uint16_t *table, int64_t rows, int H, const int32_t *id, uint16_t *out, hipStream_t st);
 void launch_to_f16(const float *x, int64_t n, uint16_t *y, hipStream_t st);
 
 // RoPE of q and this step's k, the append of k and v to the draft cache, and
@@ -56,7 +60,7 @@ void launch_draft_attn(const DraftAttn &p, hipStream_t st);
 struct DraftTopk {
     const float *logits;  // [V]
     int V, k;
-    const int32_t *d2t;   // [V] target ids
+    const int32_t *d2t;   // [V] target ids (null: the ids themselves)
     int32_t *out_draft, *out_target;
     float *out_lp;
     int32_t *next_token;  // the top-1 target id (the next step's embedding row)
@@ -128,6 +132,69 @@ class Draft3 {
     int32_t *o_ids = nullptr, *o_dids = nullptr;    // [kDraftMaxSteps][kDraftMaxTopk]
     float *o_lp = nullptr;
     int cur = 0;  // which hid[] holds the current step's input
+    int steps = 0;
+    hipStream_t own = nullptr;
+};
+
+// ---- EAGLE-2 (EagleDraftCandle, eagle.rs:306-428) ----------------------------------
+struct Draft2Cfg {
+    int hidden = 4096, n_heads = 32, n_kv_heads = 8, ffn = 14336, vocab = 128256;
+    float rms_eps = 1e-5f, rope_theta = 500000.f;
+    int max_pos = 2048;
+    int device = 0;
+    int head_dim() const { return hidden / n_heads; }
+};
+
+// Tensor kinds of the checkpoint (eagle.rs:126-131, 279-286, 349-361)
+enum Draft2Tensor : int {
+    D2_EMBED = 0, D2_FC, D2_Q, D2_K, D2_V, D2_O, D2_GATE, D2_UP, D2_DOWN, D2_POST_NORM, D2_NUM
+};
+
+class Draft2 {
+  public:
+    explicit Draft2(const Draft2Cfg &c);
+    ~Draft2();
+    Draft2Cfg cfg;
+
+    // f16 weights [out][in] (embed_tokens [vocab][hidden]) / post_attention_layernorm [hidden]
+    void set_tensor(int kind, const void *host, size_t bytes);
+    void get_tensor(int kind, void *host, size_t bytes) const;
+    size_t tensor_bytes(int kind) const;
+    void synthesize(uint64_t seed, float std);
+    bool ready() const;
+
+    // EagleDraftCandle::forward (eagle.rs:390-427) of one position:
+    // target_hidden f32 [hidden] (the target's final-norm hidden state, or the
+    // previous step's output), the token id, the RoPE position; appends to the
+    // draft's cache (reset() clears it); out f32 [hidden] (f16 values)
+    void step_host(const float *target_hidden, uint32_t token, int position, float *out);
+    void reset() { steps = 0; }
+
+    // The draft half of one run_eagle iteration (eagle.rs:519-575) against
+    // `target`: the committed token's final-norm hidden state (host f32),
+    // then `depth` steps, each a draft forward, the target's lm_head on its
+    // output, top_k[s] ids by value (index ascending on ties) with their
+    // log-probs; the top-1 id and the step's output feed the next step.
+    // Outputs [depth][kDraftMaxTopk].
+    void round(Model &target, Decoder &dec, const float *target_hidden, int depth, const int *top_k, int32_t *ids,
+               float *log_probs);
+
+  private:
+    void step_device(int position, hipStream_t st);
+    size_t off[D2_NUM] = {}, len[D2_NUM] = {};
+    bool have[D2_NUM] = {};
+    uint16_t *w = nullptr;  // every f16 tensor (Q, K, V adjacent; GATE, UP adjacent)
+    uint16_t *cos16 = nullptr, *sin16 = nullptr, *kc = nullptr, *vc = nullptr;
+    // work: comb [2H] = [input hidden | token embedding], xs [H] (fc), qkv,
+    // att [nh hd], after [H], xn [H], act [ffn]; the step's output goes to
+    // comb[0, H) (the next step's input) and out32 [H]
+    uint16_t *comb = nullptr, *xs = nullptr, *qkv = nullptr, *att = nullptr, *after = nullptr, *xn = nullptr,
+             *act = nullptr, *xp = nullptr;
+    float *hin32 = nullptr, *out32 = nullptr, *logits = nullptr;
+    int32_t *tok = nullptr, *o_ids = nullptr, *o_dids = nullptr;
+    float *o_lp = nullptr;
+    uint64_t *tk_part = nullptr;
+    int *tk_cnt = nullptr;
     int steps = 0;
     hipStream_t own = nullptr;
 };

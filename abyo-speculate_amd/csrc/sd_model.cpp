@@ -820,6 +820,20 @@ void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
     }
 }
 
+void Model::lm_head_device(const uint16_t *xp, int M, float *out, hipStream_t s) {
+    if (M < 1 || M > 16) throw ArgError("lm_head_device: 1 to 16 rows");
+    const DevTensor &W = cfg.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
+    GemmParams p{};
+    p.seg[0] = seg_of(W, 0, out, cfg.vocab, 0, nullptr);
+    p.nseg = 1;
+    p.ntiles = W.rows / 16;
+    p.xp = xp;
+    p.K = cfg.hidden;
+    p.M = M;
+    p.mode = GM_STORE;
+    launch_qgemm(p, s);
+}
+
 void Model::embed_rows(const int *ids, int n, float *out_host) {
     const ModelCfg &c = cfg;
     SD_HIP_CHECK(hipSetDevice(c.device));

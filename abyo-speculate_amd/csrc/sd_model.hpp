@@ -117,6 +117,9 @@ class Model {
     void forward(const int *ids, const int *pos, const uint64_t *mask, int mask_words, int M, int P, int logits_mode,
                  bool want_hidden, const std::vector<int> &collect, float *collect_out);
     void lm_head_rows(const float *hidden_host, int rows, float *out_host);
+    // the lm_head product of M <= 16 rows already on the device, fp16 in the
+    // matmul's fragment order (launch_to_frag16), into out [M][vocab] on `s`
+    void lm_head_device(const uint16_t *xp, int M, float *out, hipStream_t s);
     void embed_rows(const int *ids, int n, float *out_host);
     void compact_tail(int P, const std::vector<int> &src);
 

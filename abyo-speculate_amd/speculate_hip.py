@@ -99,6 +99,15 @@ class Draft3Config(ctypes.Structure):
                 ("device", ctypes.c_int32)]
 
 
+class Draft2Config(ctypes.Structure):
+    """sd_draft2_config: EagleDraftConfig (crates/speculate/src/methods/eagle.rs:56-65)"""
+    _fields_ = [("hidden", ctypes.c_int32), ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
+                ("ffn", ctypes.c_int32), ("vocab", ctypes.c_int32), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("max_pos", ctypes.c_int32), ("device", ctypes.c_int32)]
+
+
+# tensor kinds of sd_draft2_set_tensor (eagle.rs:126-131, 279-286, 349-361)
+D2_EMBED, D2_FC, D2_Q, D2_K, D2_V, D2_O, D2_GATE, D2_UP, D2_DOWN, D2_POST_NORM = range(10)
 # tensor kinds of sd_draft3_set_tensor (the checkpoint's names, eagle3.rs:133-152, 411-425)
 D3_FC, D3_Q, D3_K, D3_V, D3_O, D3_GATE, D3_UP, D3_DOWN, D3_LM_HEAD = range(9)
 D3_INPUT_NORM, D3_HIDDEN_NORM, D3_POST_NORM, D3_NORM, D3_D2T = range(9, 14)
@@ -178,6 +187,15 @@ def load_library(path: str = LIB_PATH):
         "sd_gguf_tensor_count": ([P], SZ),
         "sd_gguf_tensor_info": ([P, ctypes.c_char_p, P, P, P, P], I32),
         "sd_model_load_gguf": ([P, P], I32),
+        "sd_draft2_create": ([ctypes.POINTER(Draft2Config), ctypes.POINTER(P)], I32),
+        "sd_draft2_destroy": ([P], None),
+        "sd_draft2_tensor_bytes": ([P, I32], SZ),
+        "sd_draft2_set_tensor": ([P, I32, P, SZ], I32),
+        "sd_draft2_get_tensor": ([P, I32, P, SZ], I32),
+        "sd_draft2_synthesize": ([P, U64, ctypes.c_float], I32),
+        "sd_draft2_reset": ([P], I32),
+        "sd_draft2_forward": ([P, P, SZ, ctypes.c_uint32, SZ, P], I32),
+        "sd_draft2_round": ([P, P, P, SZ, P, P, P], I32),
         "sd_draft3_create": ([ctypes.POINTER(Draft3Config), ctypes.POINTER(P)], I32),
         "sd_draft3_destroy": ([P], None),
         "sd_draft3_tensor_bytes": ([P, I32], SZ),
@@ -682,6 +700,76 @@ class HipQuantDecoder:
 def default_layers_for(n_layers: int) -> List[int]:
     """Eagle3RunConfig::default_layers_for (eagle3.rs:540-546): [1, n/2 - 1, n - 4]"""
     return [0, 0, 0] if n_layers < 4 else [1, n_layers // 2 - 1, n_layers - 4]
+
+
+class HipEagleDraft:
+    """EagleDraftCandle (crates/speculate/src/methods/eagle.rs:306-428), the
+    EAGLE-2 draft, resident on one GPU: f16 tensors including its own token
+    table, the draft's KV cache (at most 16 steps between resets), and a whole
+    draft round of run_eagle (:519-575) on the device, with the target's
+    lm_head for the draft logits."""
+
+    def __init__(self, hidden: int = 4096, n_heads: int = 32, n_kv_heads: int = 8, ffn: int = 14336,
+                 vocab: int = 128256, rms_eps: float = 1e-5, rope_theta: float = 500000.0, max_pos: int = 2048,
+                 device: int = 0):
+        load_library()
+        self.hidden, self.vocab = hidden, vocab
+        c = Draft2Config(hidden, n_heads, n_kv_heads, ffn, vocab, rms_eps, rope_theta, max_pos, device)
+        self._h = ctypes.c_void_p()
+        _check(_lib.sd_draft2_create(ctypes.byref(c), ctypes.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.sd_draft2_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor_bytes(self, kind: int) -> int:
+        return int(_lib.sd_draft2_tensor_bytes(self._h, kind))
+
+    def set_tensor(self, kind: int, data: np.ndarray):
+        a = np.ascontiguousarray(data, np.float16)
+        _check(_lib.sd_draft2_set_tensor(self._h, kind, _ptr(a), a.nbytes))
+
+    def get_tensor(self, kind: int) -> np.ndarray:
+        a = np.empty(self.tensor_bytes(kind) // 2, np.float16)
+        _check(_lib.sd_draft2_get_tensor(self._h, kind, _ptr(a), a.nbytes))
+        return a
+
+    def synthesize(self, seed: int, std: float = 0.02):
+        _check(_lib.sd_draft2_synthesize(self._h, seed, std))
+
+    def reset(self):
+        _check(_lib.sd_draft2_reset(self._h))
+
+    def forward(self, target_hidden: np.ndarray, token: int, position: int) -> np.ndarray:
+        """EagleDraftCandle::forward (:390-427) of one position -> [hidden] (f16 values as f32)"""
+        h = np.ascontiguousarray(target_hidden, np.float32).reshape(-1)
+        out = np.empty(self.hidden, np.float32)
+        _check(_lib.sd_draft2_forward(self._h, _ptr(h), h.size, int(token), position, _ptr(out)))
+        return out
+
+    def round(self, target: "HipQuantDecoder", target_hidden: np.ndarray, depth: int, top_k) \
+            -> Tuple[List[List[int]], List[List[float]]]:
+        """The draft half of one run_eagle iteration (:519-575) against target:
+        -> (per-step top-k ids, their log-probs)"""
+        ks = [int(top_k)] * depth if np.isscalar(top_k) else [int(k) for k in top_k]
+        if len(ks) != depth:
+            raise ArgError("one top_k per draft step")
+        h = np.ascontiguousarray(target_hidden, np.float32).reshape(-1)
+        if h.size != self.hidden:
+            raise ArgError("target_hidden must be hidden wide")
+        k = np.asarray(ks, np.int32)
+        ids = np.zeros((max(depth, 1), DRAFT3_MAX_TOPK), np.int32)
+        lps = np.zeros(ids.shape, np.float32)
+        _check(_lib.sd_draft2_round(self._h, target._h, _ptr(h), depth, _ptr(k), _ptr(ids), _ptr(lps)))
+        return ([[int(v) for v in ids[s, :ks[s]]] for s in range(depth)],
+                [[float(v) for v in lps[s, :ks[s]]] for s in range(depth)])
 
 
 class HipEagle3Draft:

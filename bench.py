@@ -446,6 +446,30 @@ def main():
                     "tree verify over ~8200 positions with greedy acceptance, commit of the path, observe of the bonus "
                     "(random weights: the target accepts ~nothing, so about one token per iteration)"}
         dr.close()
+
+        # ---------------- EAGLE-2 draft round on the device (EAGLE-LLaMA3-Instruct-8B shapes) ----------------
+        log("EAGLE-2 draft: LLaMA3-8B-shaped f16 draft (own 128256-token table, the target's lm_head), synthesised")
+        d2 = S.HipEagleDraft(vocab=cfg.vocab, max_pos=EAGLE3_PREFIX + 256)
+        d2.synthesize(SEED + 9, 0.02)
+        ks2 = (4, 3, 2, 2, 1, 1)
+        th = dec.last_hidden_state()
+
+        def step_draft2():
+            ids, lp = d2.round(dec, th, len(ks2), list(ks2))
+            return len(ids)
+
+        t_d2 = wall_per_step(dec, step_draft2, args)
+        wb2 = sum(d2.tensor_bytes(k) for k in range(S.D2_FC, S.D2_POST_NORM + 1))
+        lmb = cfg.vocab * cfg.hidden // 256 * 144  # Q4_K: 144 bytes per 256 weights
+        log(f"EAGLE-2 draft round: {t_d2 * 1e6:.1f} us (depth {len(ks2)}, top-k {ks2})")
+        result["eagle2_draft_round"] = {
+            "us": round(t_d2 * 1e6, 1), "depth": len(ks2), "top_k": list(ks2),
+            "draft_weight_bytes_per_step": int(wb2), "target_lm_head_bytes_per_step": lmb,
+            "what": "one draft round of run_eagle on the device from the committed token's final-norm hidden state "
+                    "(8193 positions): per step the draft's embedding row, fc over [hidden, embedding], one f16 "
+                    "Llama block, the target's Q4_K lm_head (128256 x 4096) on the output, top-k over 128256 "
+                    "logits with log-probs; the tree60 leg's branching (4,3,2,2,1,1)"}
+        d2.close()
     dec.close()
 
     if not args.no_extra:

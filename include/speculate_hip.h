@@ -438,6 +438,52 @@ sd_status sd_draft3_forward(sd_draft3 *d, const float *hidden_in, size_t n_in, c
 sd_status sd_draft3_round(sd_draft3 *d, sd_model *m, const uint32_t *layers, size_t depth, const int32_t *top_k,
                           int32_t *target_ids, int32_t *draft_ids, float *log_probs);
 
+/* EagleDraftCandle (crates/speculate/src/methods/eagle.rs:306-428), the
+ * EAGLE-2 draft, on the device: its own token table, fc over [target hidden,
+ * token embedding], one Llama block without input norm, f16 throughout; its
+ * logits come from the target's lm_head (apply_lm_head). */
+typedef struct sd_draft2 sd_draft2;
+typedef struct {
+    int32_t hidden, n_heads, n_kv_heads, ffn, vocab; /* vocab: the target's (<= 262144) */
+    float rms_eps, rope_theta;
+    int32_t max_pos; /* rows of the RoPE tables (EagleDraftConfig::max_position_embeddings) */
+    int32_t device;
+} sd_draft2_config;
+enum {
+    SD_D2_EMBED = 0, SD_D2_FC, SD_D2_Q, SD_D2_K, SD_D2_V, SD_D2_O, SD_D2_GATE, SD_D2_UP, SD_D2_DOWN,
+    SD_D2_POST_NORM
+};
+sd_status sd_draft2_create(const sd_draft2_config *cfg, sd_draft2 **out);
+void sd_draft2_destroy(sd_draft2 *d);
+/* bytes of one tensor kind (0 for a bad handle or kind) */
+size_t sd_draft2_tensor_bytes(const sd_draft2 *d, int32_t kind);
+/* EagleDraftCandle::from_var_builder (:343-371): f16 row-major tensors
+ * ([out][in]; embed_tokens [vocab][hidden]; post_attention_layernorm [hidden]) */
+sd_status sd_draft2_set_tensor(sd_draft2 *d, int32_t kind, const void *data, size_t bytes);
+sd_status sd_draft2_get_tensor(const sd_draft2 *d, int32_t kind, void *data, size_t bytes);
+/* seeded synthetic weights (N(0, std) f16 matrices and table, norm 1 + N(0, 0.1)) */
+sd_status sd_draft2_synthesize(sd_draft2 *d, uint64_t seed, float weight_std);
+/* EagleDraftCandle::reset (:373-375): clears the draft's own KV cache */
+sd_status sd_draft2_reset(sd_draft2 *d);
+/* EagleDraftCandle::forward (:390-427) of one position: target_hidden f32
+ * [hidden] (the target's final-norm hidden state or the previous step's
+ * output), token < vocab, the RoPE position (< max_pos); out f32 [hidden]
+ * (f16 values).  Appends the step to the draft's cache (at most 16 steps
+ * between resets). */
+sd_status sd_draft2_forward(sd_draft2 *d, const float *target_hidden, size_t n, uint32_t token, size_t position,
+                            float *out_hidden);
+/* The draft half of one run_eagle iteration (:519-575) against the target m,
+ * on the device: `depth` (<= 16) steps from target_hidden (f32 [hidden], the
+ * committed token's final-norm hidden state, as observe_returning_last_hidden
+ * returns it) and m's last committed token, each a draft forward, m's lm_head
+ * on its output, and the top top_k[s] (<= 8) ids by value (index ascending on
+ * ties) with their log-probs l - logsumexp(l); the top-1 id and the step's
+ * output feed the next step.  Outputs [depth][8] (entries past top_k[s]
+ * unset).  m's history and cache are untouched; positions run from the
+ * history length and must stay below max_pos (SD_ERR_ARG). */
+sd_status sd_draft2_round(sd_draft2 *d, sd_model *m, const float *target_hidden, size_t depth, const int32_t *top_k,
+                          int32_t *ids, float *log_probs);
+
 #ifdef __cplusplus
 }
 #endif
