@@ -421,6 +421,71 @@ template <typename F> __device__ __forceinline__ int walk_search(const WalkShare
     return -1;
 }
 
+// ---- a chain's passes, precomputed across the GPU ---------------------------------
+// grid (n, tile groups), block kLtT: wave w of group y sums tiles
+// (y * 4 + w) * kBatch + b, b < kBatch, of row r exactly as walk_tiles does
+// (a lane's 4 entries in order, then wave_sum).  Phase 0: for a node with a
+// child, max(0, p - q) (the normaliser pass of its first rejection), for the
+// leaf p itself (its final draw); phase 1, after phase 0: max(0, p - q) / Z
+// with Z totalled as walk_pass totals (the draw after the rejection).
+constexpr int kLtT = 256;
+template <int PHASE> __global__ __launch_bounds__(kLtT) void k_linear_tiles(AcceptParams a, float *lin) {
+    const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int V = a.V, n = a.n, ntiles = (V + kTile - 1) / kTile;
+    const bool leaf = r == n - 1;
+    if (PHASE == 1 && leaf) return;
+    const float *prow = a.prob + (int64_t)r * V;
+    const float *qrow = a.q + (int64_t)(leaf ? 0 : a.q_row_of[r]) * a.q_ld;
+    float Z = 1.f;
+    if (PHASE == 1) {
+        const float *zt = lin + (int64_t)r * ntiles;
+        float s = 0.f;
+        for (int tl = lane; tl < ntiles; tl += 64) s += zt[tl];
+        Z = wave_sum(s);
+    }
+    float *out = PHASE == 1 ? lin + (int64_t)(n + r) * ntiles : leaf ? lin + 2LL * n * ntiles : lin + (int64_t)r * ntiles;
+    const int tb = ((int)blockIdx.y * (kLtT / 64) + wave) * kBatch;
+    float p0[kBatch][4], q0[kBatch][4];
+#pragma unroll
+    for (int b = 0; b < kBatch; b++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int x = min((tb + b) * kTile + lane + 64 * j, V - 1);
+            p0[b][j] = prow[x];
+            q0[b][j] = leaf ? 0.f : qrow[x];
+        }
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+        const int tl = tb + b;
+        if (tl >= ntiles) break;
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int x = tl * kTile + lane + 64 * j;
+            const float v = leaf ? p0[b][j] : PHASE == 0 ? fmaxf(p0[b][j] - q0[b][j], 0.f)
+                                                         : fmaxf(p0[b][j] - q0[b][j], 0.f) / Z;
+            s += x < V ? v : 0.f;
+        }
+        s = wave_sum(s);
+        if (lane == 0) out[tl] = s;
+    }
+}
+
+// wave 0: a row of precomputed tile sums into W.tsum and its total (walk_pass's order)
+__device__ __forceinline__ float walk_load_tiles(WalkShared &W, const float *src, int ntiles) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int tl = threadIdx.x; tl < ntiles; tl += WT) W.tsum[tl] = src[tl];
+    __syncthreads();
+    if (wave == 0) {
+        float s = 0.f;
+        for (int tl = lane; tl < ntiles; tl += 64) s += W.tsum[tl];
+        s = wave_sum(s);
+        if (lane == 0) W.total = s;
+    }
+    __syncthreads();
+    return W.total;
+}
+
 // grid 1, block 1024
 __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     __shared__ WalkShared W;
@@ -503,7 +568,9 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
                 if (t == 0) W.status = ACC_ERR_ARG;
                 break;
             }
-            const float Z = walk_pass(W, a, node, krej, true);
+            const int ntl = (a.V + kTile - 1) / kTile;
+            const float Z = a.lin && krej == 0 ? walk_load_tiles(W, a.lin + (int64_t)node * ntl, ntl)
+                                               : walk_pass(W, a, node, krej, true);
             if (t == 0) {
                 if (!(Z > 0.f) || !isfinite(Z)) {
                     W.status = ACC_ERR_ADJUSTED;
@@ -518,7 +585,10 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
         }
         // go == 1: sample_from_distribution (tokens.rs:99-120) over the current distribution
         auto f = [&](int x) { return walk_p(a, W, node, krej, x); };
-        const float sum = walk_pass(W, a, node, krej, false);
+        const int ntl = (a.V + kTile - 1) / kTile;
+        const float sum = a.lin && krej == 1 ? walk_load_tiles(W, a.lin + (int64_t)(a.n + node) * ntl, ntl)
+                          : a.lin && krej == 0 && node == a.n - 1 ? walk_load_tiles(W, a.lin + 2LL * a.n * ntl, ntl)
+                                                                  : walk_pass(W, a, node, krej, false);
         if (!(sum > 0.f) || !isfinite(sum)) {
             if (t == 0) W.status = ACC_ERR_SOFTMAX;
             break;
@@ -546,6 +616,17 @@ void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float in
                        row_am);
     hipLaunchKernelGGL(k_row_prob, grid, dim3(kRsT), 0, st, logits, ld, V, inv_t, greedy, t2d_inv, row_m, row_s,
                        row_am, prob);
+}
+
+size_t linear_tiles_floats(int n, int V) { return (size_t)(2 * n + 1) * ((V + kTile - 1) / kTile); }
+
+void launch_linear_tiles(const AcceptParams &a, float *lin, hipStream_t st) {
+    if (a.V > kMaxTiles * kTile) throw BackendError("acceptance: vocabulary too large");
+    if (a.n < 1 || a.n > kMaxNodes || a.q_map) throw BackendError("acceptance: linear tiles need a chain in the target vocabulary");
+    const int ntiles = (a.V + kTile - 1) / kTile, per = (kLtT / 64) * kBatch;
+    const dim3 grid(a.n, (ntiles + per - 1) / per);
+    hipLaunchKernelGGL(k_linear_tiles<0>, grid, dim3(kLtT), 0, st, a, lin);
+    hipLaunchKernelGGL(k_linear_tiles<1>, grid, dim3(kLtT), 0, st, a, lin);
 }
 
 void launch_accept_walk(const AcceptParams &a, hipStream_t st) {

@@ -28,6 +28,12 @@ struct AcceptParams {
                            // token's q is zeroed and q renormalised before the next sibling
     int *out_path;         // [n] accepted node indices, root first
     int *out_info;         // [4]: path length, final token (-1 none), uniforms used, status
+    // A chain (node i's child is i + 1) with draft rows in the target
+    // vocabulary may carry every pass its walk can make, precomputed across
+    // the GPU by launch_linear_tiles: per node the tile sums of max(0, p - q)
+    // and of max(0, p - q) / Z, and the leaf's tile sums of p.  Null: the walk
+    // makes its passes itself.
+    const float *lin;
 };
 
 // q(x) of draft row qr
@@ -46,5 +52,9 @@ constexpr int kRowStatsMaxSlices = 32;
 void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, int greedy, const int *t2d_inv,
                       uint64_t *part, int *cnt, float *row_m, float *row_s, int *row_am, float *prob, hipStream_t st);
 void launch_accept_walk(const AcceptParams &a, hipStream_t st);
+// the precomputed passes of a chain's walk into lin [(2 n + 1) x tiles]
+// (AcceptParams::lin; a.prob, a.q, a.q_row_of, a.V, a.n as for the walk)
+size_t linear_tiles_floats(int n, int V);
+void launch_linear_tiles(const AcceptParams &a, float *lin, hipStream_t st);
 
 }  // namespace sd

@@ -79,7 +79,7 @@ Model::~Model() {
                     (void *)acc_m, (void *)acc_s, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
                     (void *)aux_ids, (void *)ssq, (void *)split_cnt, (void *)acc_part, (void *)acc_cnt,
-                    (void *)acc_prob})
+                    (void *)acc_prob, (void *)acc_lin})
         F(p);
     if (h_stage) hipHostFree(h_stage);
     if (acc_stage) hipHostFree(acc_stage);
@@ -1029,10 +1029,14 @@ void Decoder::batched_logits(const uint32_t *drafts, size_t k, float *out) {
     comb.push_back(last);
     comb.insert(comb.end(), drafts, drafts + k);
     forward_advance(comb.data(), comb.size(), true);
-    if (out)
-        SD_HIP_CHECK(hipMemcpyAsync(out, m.logits, (k + 1) * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
     history.insert(history.end(), drafts, drafts + k);
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    if (out) {
+        SD_HIP_CHECK(hipMemcpyAsync(out, m.logits, (k + 1) * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
+        SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    }
+    // without `out` the rows stay on the device for the caller's own kernels,
+    // queued behind the forward on the same stream (the device-acceptance
+    // entry points, which synchronise once at their end)
 }
 
 void Decoder::rollback_to(size_t len) {
@@ -1361,7 +1365,7 @@ static void check_device_rows(const Model &m, const float *q, size_t n) {
 void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, bool q_on_device,
                           size_t q_rows_n, size_t q_vocab, const int *q_row_of, const float *uniforms,
                           float temperature, int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin,
-                          size_t &used) {
+                          size_t &used, bool linear) {
     Model &m = *model;
     const ModelCfg &c = m.cfg;
     if (m.logits_rows_last < n) throw BackendError("acceptance: fewer logits rows than tree nodes");
@@ -1418,6 +1422,19 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     a.wor = wor;
     a.out_path = m.acc_out + 4;
     a.out_info = m.acc_out;
+    if (linear && !a.q_map && !wor) {
+        // a chain: every pass the walk can make, computed across the GPU first
+        const size_t ln = linear_tiles_floats(n, c.vocab);
+        if (ln > m.acc_lin_cap) {
+            if (m.acc_lin) SD_HIP_CHECK(hipFree(m.acc_lin));
+            m.acc_lin = nullptr;
+            m.acc_lin_cap = 0;
+            SD_HIP_CHECK(hipMalloc((void **)&m.acc_lin, ln * sizeof(float) + 256));
+            m.acc_lin_cap = ln;
+        }
+        launch_linear_tiles(a, m.acc_lin, m.st);
+        a.lin = m.acc_lin;
+    }
     launch_accept_walk(a, m.st);
     int *out = m.acc_stage + 4 * c.max_batch;
     SD_HIP_CHECK(hipMemcpyAsync(out, m.acc_out, ((size_t)n + 4) * sizeof(int), hipMemcpyDeviceToHost, m.st));
@@ -1466,8 +1483,7 @@ void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const fl
     int fin;
     size_t used;
     accept_walk(parents.data(), tokens.data(), n, q_rows, q_on_device, k, m.cfg.vocab, qrow.data(), uniforms,
-                temperature, 0, 0,
-                max_commit, path, fin, used);
+                temperature, 0, 0, max_commit, path, fin, used, true);
     size_t nc = 0;
     for (size_t i = 1; i < path.size(); i++) commits[nc++] = (uint32_t)tokens[path[i]];
     if (fin >= 0) commits[nc++] = (uint32_t)fin;

@@ -133,7 +133,9 @@ void sd_reset(sd_model *m);                                   /* Decoder::reset,
 sd_status sd_observe(sd_model *m, const uint32_t *ids, size_t n);
 /* Decoder::next_logits (quantized_llama.rs:528-551): out [vocab]. */
 sd_status sd_next_logits(sd_model *m, float *out);
-/* Decoder::batched_logits (quantized_llama.rs:553-583): out [(k+1)][vocab]; history += drafts. */
+/* Decoder::batched_logits (quantized_llama.rs:553-583): out [(k+1)][vocab]; history += drafts.
+ * out NULL: the rows stay on the device (sd_last_argmax, the acceptance entry
+ * points) and the call returns once the forward is queued. */
 sd_status sd_batched_logits(sd_model *m, const uint32_t *drafts, size_t k, float *out);
 /* Decoder::rollback_to (quantized_llama.rs:585-599). */
 sd_status sd_rollback_to(sd_model *m, size_t len);
