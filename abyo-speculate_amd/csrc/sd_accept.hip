@@ -35,6 +35,7 @@
 // parallel (fixed-order trees over slices, tiles and lanes), so they can
 // differ from the reference's sequential f32 sums in the last bits; a
 // decision can only differ when u lies within a few ulps of a threshold.
+#include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels_accept.hpp"
 
@@ -430,6 +431,7 @@ template <typename F> __device__ __forceinline__ int walk_search(const WalkShare
 // with Z totalled as walk_pass totals (the draw after the rejection).
 constexpr int kLtT = 256;
 template <int PHASE> __global__ __launch_bounds__(kLtT) void k_linear_tiles(AcceptParams a, float *lin) {
+    warm_kernargs<sizeof(AcceptParams)>();
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int V = a.V, n = a.n, ntiles = (V + kTile - 1) / kTile;
     const bool leaf = r == n - 1;
@@ -488,6 +490,7 @@ __device__ __forceinline__ float walk_load_tiles(WalkShared &W, const float *src
 
 // grid 1, block 1024
 __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
+    warm_kernargs<sizeof(AcceptParams)>();
     __shared__ WalkShared W;
     const int t = threadIdx.x;
     for (int i = t; i < a.n; i += WT) {

@@ -60,6 +60,7 @@ __device__ __forceinline__ float qkv_at(const RopeKvParams &p, int m, int col) {
 
 // grid (M, n_heads + n_kv), block hd/2 threads
 __global__ void k_rope_kv(RopeKvParams p) {
+    warm_kernargs<sizeof(RopeKvParams)>();
     const int m = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
     const int half = p.hd / 2;
     if (i >= half) return;
@@ -422,6 +423,7 @@ template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnPara
 
 template <int HD, int QT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnParams p) {
+    warm_kernargs<sizeof(AttnParams)>();
     constexpr int NDT = HD / 16;
     const int h = blockIdx.x, s = blockIdx.y, qg = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -624,6 +626,7 @@ template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTKS * kTStages
 
 template <int HD>
 __global__ __launch_bounds__(256 * kTKS) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {
+    warm_kernargs<sizeof(AttnParams)>();
     constexpr int NDT = HD / 16, QT = kTQW, SW = 8 * HD;  // SW: 16-byte pieces of one stage
     extern __shared__ uintx4 lds[];
     const int h = blockIdx.x, s = blockIdx.y, qb = blockIdx.z;
@@ -719,6 +722,7 @@ __global__ __launch_bounds__(256 * kTKS) __attribute__((amdgpu_waves_per_eu(2)))
 // grid (n_heads, M), block hd threads; splits are merged in index order:
 // out = sum_s w_s o_s / sum_s w_s, w_s = l_s * exp2(m_s - max m).
 __global__ __launch_bounds__(128) void k_attn_combine(AttnParams p) {
+    warm_kernargs<sizeof(AttnParams)>();
     const int head = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const int HD = p.hd, ns = p.nsplit;
     const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split

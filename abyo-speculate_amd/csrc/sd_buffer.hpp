@@ -36,4 +36,18 @@ __device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t vo, uint32_t so) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
 }
 
+// A kernel's argument block reaches its waves through the scalar cache.  A
+// kernel that reads a large parameter struct field by field, with branches
+// between the reads, waits one memory round trip (~0.5 us) per cache line it
+// first touches.  Touching every 64-byte line of the first BYTES bytes at once
+// fills them in a single round trip; later reads of any field then hit.
+template <int BYTES> __device__ __forceinline__ void warm_kernargs() {
+    typedef const uint32_t __attribute__((address_space(4))) cu32;
+    const cu32 *ka = (const cu32 *)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < (BYTES + 63) / 64; i++) acc ^= ka[16 * i];
+    asm volatile("" ::"s"(acc));  // waits for every line once, here
+}
+
 }  // namespace sd

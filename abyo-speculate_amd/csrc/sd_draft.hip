@@ -34,6 +34,7 @@ typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
 constexpr int kGvWaves = 4, kGvRows = 8, kGvChunk = 512;
 template <int MODE>
 __global__ __launch_bounds__(64 * kGvWaves) void k_gemv16(DraftGemv p) {
+    warm_kernargs<sizeof(DraftGemv)>();
     __shared__ float red[kGvWaves][kGvRows];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int row[kGvRows];
@@ -135,6 +136,7 @@ void launch_gemv16(int mode, const DraftGemv &p, hipStream_t st) {
 constexpr int kNormT = 1024;
 template <int PER>  // elements per thread: H <= 1024 PER
 __global__ __launch_bounds__(kNormT) void k_rmsnorm16(DraftNorm p) {
+    warm_kernargs<sizeof(DraftNorm)>();
     const int r = blockIdx.x;
     const uint16_t *x16 = p.x16[r];
     const float *x32 = p.x32[r];
@@ -211,6 +213,7 @@ void launch_to_f16(const float *x, int64_t n, uint16_t *y, hipStream_t st) {
 // rotation pairs (i, i + hd/2) for i = lane and lane + 64.
 constexpr int kAttnPairs = 2;  // head_dim up to 256
 __global__ __launch_bounds__(64) void k_draft_attn(DraftAttn p) {
+    warm_kernargs<sizeof(DraftAttn)>();
     const int h = blockIdx.x, lane = threadIdx.x;
     const int rep = p.n_heads / p.n_kv, kv = h / rep;
     const int hd = p.hd, half = hd / 2, T = p.step + 1;
@@ -359,6 +362,7 @@ __device__ __forceinline__ void tk_ld64(const uint64_t *p, float &a, int &b) {
 }
 constexpr int kTkNone = 0x7fffffff;
 __global__ __launch_bounds__(kTkT) void k_draft_topk(DraftTopk p) {
+    warm_kernargs<sizeof(DraftTopk)>();
     __shared__ float sv[2][kTkT / 64], red[kTkT / 64], wv[kDraftMaxTopk];
     __shared__ int si[2][kTkT / 64], wi[kDraftMaxTopk];
     __shared__ int s_last;

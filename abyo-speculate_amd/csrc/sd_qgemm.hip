@@ -712,6 +712,7 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
 
 template <int RT, int KW>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
+    warm_kernargs<sizeof(GemmParams)>();
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     GemmSeg S[RT];
@@ -912,6 +913,7 @@ __device__ __forceinline__ void qgx_body(const GemmParams &p, const WRow (&row)[
 
 template <int RW, int CT>
 __global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
+    warm_kernargs<sizeof(GemmParams)>();
     extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
