@@ -550,32 +550,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // ---- many queries (tree verify): query tiles across waves, keys shared in LDS ----
-// Grid (kv head, key split, query block).  A workgroup has kTKS key groups of
-// 4 waves; the 4 waves of a group own kTQW query tiles each (the workgroup's
-// 4 * kTQW * 16 queries of one KV head) and walk the group's part of the split
+// Grid (kv head, key split, query block).  The 8 waves of a workgroup own
+// kTQW query tiles each, the 8 * kTQW * 16 queries of one query block of a KV
+// head (all of them up to 256 query rows), and walk the split's keys
 // together: each 32-key block of K and V (contiguous in the blocked cache
-// layout) is copied once into LDS by the group's 256 threads and read there by
-// its 4 waves, so the cache leaves L2 once per query block instead of once per
-// query tile.  Copies run kTStages blocks ahead through registers (as many LDS
-// stages, one barrier per block).  The key groups merge through LDS at the
-// end (fixed order), the splits in the combine kernel.
+// layout) is copied once into LDS by the workgroup's 512 threads and read
+// there by all 8 waves, so the cache leaves L2 once per query block.  Copies
+// run kTStages blocks ahead through registers (as many LDS stages, one barrier
+// per block).  Splits are a few blocks long, so the grid covers the chip; the
+// combine kernel merges them.
+constexpr int kTWaves = 8;
+constexpr int kTThreads = 64 * kTWaves;
 constexpr int kTQW = 2;
-constexpr int kTKS = 2;
 constexpr int kTStages = 3;
-constexpr int kTMaxSplits = 16;
+constexpr int kTMaxSplits = 32;
 
-// a thread's 16-byte pieces of one 32-key block: K (64 * HD bytes) then V
+// a thread's 16-byte pieces of one 32-key block: pieces i * 512 + tid, the
+// block's K (4 * HD pieces) first, then its V
 template <int HD> struct TileCopy {
-    uintx4 r[HD / 32];
+    uintx4 r[HD / 64];
 };
 template <int HD>
 __device__ __forceinline__ void tile_fetch(TileCopy<HD> &c, const KvSrc &src, int kk, int tid) {  // kk < 0: none
     const uint32_t so = kv_so(kk, HD);
-    const uint32_t t16 = (uint32_t)tid * 16u;
 #pragma unroll
-    for (int i = 0; i < HD / 32; i++) {
-        const uint32_t b = (uint32_t)i * 4096u + t16;
-        c.r[i] = i < HD / 64 ? bld16(src.k, b, so) : bld16(src.v, b - 64u * HD, so);
+    for (int i = 0; i < HD / 64; i++) {
+        const int piece = i * kTThreads + tid;
+        c.r[i] = piece < 4 * HD ? bld16(src.k, (uint32_t)piece * 16u, so)
+                                : bld16(src.v, (uint32_t)(piece - 4 * HD) * 16u, so);
     }
 }
 // In LDS each 1 KiB chunk (the 64 16-byte pieces one MFMA operand load reads,
@@ -589,7 +591,7 @@ __device__ __forceinline__ int lds_swz(int piece) {
 template <int HD>
 __device__ __forceinline__ void tile_store(uintx4 *stage, const TileCopy<HD> &c, int tid) {
 #pragma unroll
-    for (int i = 0; i < HD / 32; i++) stage[lds_swz(i * 256 + tid)] = c.r[i];
+    for (int i = 0; i < HD / 64; i++) stage[lds_swz(i * kTThreads + tid)] = c.r[i];
 }
 
 // One 32-key block from LDS for the wave's query tiles (dead tiles skipped)
@@ -622,157 +624,162 @@ __device__ __forceinline__ void tile_step(AttnState<HD, QT> &S, const uintx4 *st
     step_pv<HD, QT>(S, vop, bp, alpha, moved, tl);
 }
 
-template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTKS * kTStages * 8 * HD * 16; }
+template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTStages * 8 * HD * 16; }
+
+// A query tile's raw operands, requested before the first key blocks so that
+// waiting for them does not wait for the blocks (loads complete in order).
+template <int HD> struct QueryRaw {
+    uintx4 q[HD / 32];
+    uint64_t mk0, mk1;
+};
+template <int HD>
+__device__ __forceinline__ void query_fetch(QueryRaw<HD> &r, const AttnParams &p, int h, int q, int g) {
+    const int nq = p.M * p.n_rep;
+    const bool live = q < nq;
+    const int m = live ? q / p.n_rep : 0, rep = live ? q % p.n_rep : 0;
+    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + rep) * p.M + m) * HD;
+#pragma unroll
+    for (int dc = 0; dc < HD / 32; dc++) r.q[dc] = live ? *(const uintx4 *)(qr + dc * 32 + g * 8) : uintx4{0u, 0u, 0u, 0u};
+    r.mk0 = p.mask[(int64_t)m * p.mask_words];
+    r.mk1 = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
+}
+// the query scaled by scale * log2(e) (scores in base-2 softmax units) and an
+// empty softmax state; load_query's arithmetic
+template <int HD, int QT>
+__device__ __forceinline__ void query_init(AttnState<HD, QT> &S, int t, const QueryRaw<HD> &r, float sl2) {
+#pragma unroll
+    for (int dc = 0; dc < HD / 32; dc++) {
+        half8 v = __builtin_bit_cast(half8, r.q[dc]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (_Float16)((float)v[i] * sl2);
+        S.qf[t][dc] = v;
+    }
+    S.mk0[t] = r.mk0;
+    S.mk1[t] = r.mk1;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    S.m[t] = -INFINITY;
+    S.l[t] = 0.f;
+}
 
 template <int HD>
-__global__ __launch_bounds__(256 * kTKS) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {
+__global__ __launch_bounds__(kTThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {
     warm_kernargs<sizeof(AttnParams)>();
-    constexpr int NDT = HD / 16, QT = kTQW, SW = 8 * HD;  // SW: 16-byte pieces of one stage
+    constexpr int QT = kTQW, SW = 8 * HD;  // SW: 16-byte pieces of one stage
     extern __shared__ uintx4 lds[];
     const int h = blockIdx.x, s = blockIdx.y, qb = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kg = wave >> 2, qw = wave & 3, tid = threadIdx.x & 255;
+    const int tid = threadIdx.x;
     const int r16 = lane & 15, g = lane >> 4;
     const int nq = p.M * p.n_rep;
     const int T = p.P + p.M;
-    const int kps = 4 * p.keys_per_wave, kpg = kps / kTKS;  // keys of the split, of a group
-    const int s0 = s * kps;
-    const int k0 = s0 + kg * kpg, lim = min(k0 + kpg, T);   // this group's keys [k0, lim)
-    const int nb = (min(s0 + kpg, T) - s0 + 31) / 32;       // blocks of group 0 (>= group 1's)
+    const int kps = 4 * p.keys_per_wave;  // keys of a split
+    const int k0 = s * kps, lim = min(k0 + kps, T);
+    const int nb = (lim - k0 + 31) / 32;
     const uint32_t stream_bytes = (uint32_t)p.cap * HD * 2u;
     KvSrc src;
     src.k = make_rsrc(p.kc + (int64_t)h * p.cap * HD, stream_bytes);
     src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
     src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
-    uintx4 *stg = lds + kg * kTStages * SW;
     const int lp = lds_swz(r16 * 4 + g);
     auto blk = [&](int j) { return k0 + 32 * j < lim ? k0 + 32 * j : -1; };
 
-    // the first blocks' copies go out before anything else
+    // the queries first, then the first blocks' copies
+    QueryRaw<HD> qr[QT];
+    bool tl[QT];
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        const int tile = (qb * kTWaves + wave) * QT + t;
+        tl[t] = tile * 16 < nq;  // wave-uniform: the tile holds a live query
+        query_fetch<HD>(qr[t], p, h, tile * 16 + r16, g);
+    }
     TileCopy<HD> c0, c1, c2;
     tile_fetch<HD>(c0, src, blk(0), tid);
     tile_fetch<HD>(c1, src, blk(1), tid);
     tile_fetch<HD>(c2, src, blk(2), tid);
 
     AttnState<HD, QT> S;
-    bool tl[QT];
     const float sl2 = p.scale * 1.4426950408889634f;
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
-        const int tile = (qb * 4 + qw) * QT + t;
-        tl[t] = tile * 16 < nq;  // wave-uniform: the tile holds a live query
-        load_query<HD, QT>(S, t, p, h, tile * 16 + r16, g, sl2);
-    }
+    for (int t = 0; t < QT; t++) query_init<HD, QT>(S, t, qr[t], sl2);
 
     // block j lives in stage j % 3; it is written after every wave passed the
     // barrier of block j - 1, i.e. finished block j - 2 and so block j - 3.
-    // Blocks past a group's range load nothing and are fully masked.
     for (int j = 0; j < nb; j += 3) {
-        tile_store<HD>(stg, c0, tid);
+        tile_store<HD>(lds, c0, tid);
         tile_fetch<HD>(c0, src, blk(j + 3), tid);
         __syncthreads();
-        tile_step<HD, QT>(S, stg, lp, tl, k0 + 32 * j, p.P, T, lim, g);
+        tile_step<HD, QT>(S, lds, lp, tl, k0 + 32 * j, p.P, T, lim, g);
         if (j + 1 >= nb) break;
-        tile_store<HD>(stg + SW, c1, tid);
+        tile_store<HD>(lds + SW, c1, tid);
         tile_fetch<HD>(c1, src, blk(j + 4), tid);
         __syncthreads();
-        tile_step<HD, QT>(S, stg + SW, lp, tl, k0 + 32 * (j + 1), p.P, T, lim, g);
+        tile_step<HD, QT>(S, lds + SW, lp, tl, k0 + 32 * (j + 1), p.P, T, lim, g);
         if (j + 2 >= nb) break;
-        tile_store<HD>(stg + 2 * SW, c2, tid);
+        tile_store<HD>(lds + 2 * SW, c2, tid);
         tile_fetch<HD>(c2, src, blk(j + 5), tid);
         __syncthreads();
-        tile_step<HD, QT>(S, stg + 2 * SW, lp, tl, k0 + 32 * (j + 2), p.P, T, lim, g);
+        tile_step<HD, QT>(S, lds + 2 * SW, lp, tl, k0 + 32 * (j + 2), p.P, T, lim, g);
     }
-#pragma unroll
-    for (int t = 0; t < QT; t++) S.l[t] = xsum4(S.l[t]);  // the query's 4 partial sums
-
-    // key group 1 hands its state to group 0 through LDS (the stages are free
-    // once every wave passed this barrier)
-    static_assert(kTKS == 2, "the merge below pairs two key groups");
-    floatx4 *mo = (floatx4 *)lds;                               // [qw][t][dt][lane]
-    float *mml = (float *)(lds + 4 * QT * NDT * 64);            // [qw][t][lane][2]
-    __syncthreads();
-    if (kg == 1) {
-#pragma unroll
-        for (int t = 0; t < QT; t++) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) mo[((qw * QT + t) * NDT + dt) * 64 + lane] = S.o[t][dt];
-            mml[((qw * QT + t) * 64 + lane) * 2] = S.m[t];
-            mml[((qw * QT + t) * 64 + lane) * 2 + 1] = S.l[t];
-        }
-    }
-    __syncthreads();
-    if (kg == 1) return;
 #pragma unroll
     for (int t = 0; t < QT; t++) {
-        const int q = ((qb * 4 + qw) * QT + t) * 16 + r16;
-        if (q >= nq) continue;
-        const float m1 = mml[((qw * QT + t) * 64 + lane) * 2], l1 = mml[((qw * QT + t) * 64 + lane) * 2 + 1];
-        const float mx = fmaxf(S.m[t], m1);
-        const float f0 = S.m[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(S.m[t] - mx);
-        const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
-        floatx4 y[NDT];
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] * f0 + mo[((qw * QT + t) * NDT + dt) * 64 + lane] * f1;
-        attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, mx, S.l[t] * f0 + l1 * f1);
+        const int q = ((qb * kTWaves + wave) * QT + t) * 16 + r16;
+        const float l = xsum4(S.l[t]);  // the query's 4 partial sums
+        if (q < nq) attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, S.o[t], S.m[t], l);
     }
 }
 
 // ---- combine splits -> fp16 fragment-layout input of wo ----------------------
-// grid (n_heads, M), block hd threads; splits are merged in index order:
+// Thread (row, c) of a 128-thread workgroup owns dims [4c, 4c + 4) of one
+// partial row (head, m) and requests every split's (m_s, l_s) and its 4 dims
+// at once (up to NS splits; loads past nsplit read zeros without a memory
+// access), so the merge waits for one memory round trip, and the grid has a
+// workgroup per 4 rows.  Splits are merged in index order:
 // out = sum_s w_s o_s / sum_s w_s, w_s = l_s * exp2(m_s - max m).
-__global__ __launch_bounds__(128) void k_attn_combine(AttnParams p) {
+constexpr int kCombThreads = 128;
+constexpr int kCombMaxSplits = 72;  // >= attn_max_splits for every n_kv
+template <int NS> __global__ __launch_bounds__(kCombThreads) void k_attn_combine(AttnParams p) {
     warm_kernargs<sizeof(AttnParams)>();
-    const int head = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
     const int HD = p.hd, ns = p.nsplit;
-    const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
-    const int64_t pi0 = (int64_t)head * p.M + m;
-    const uint16_t *po = (const uint16_t *)p.part_o;
-    constexpr int kFew = 12;
-    if (ns <= kFew) {
-        // every split's (m, l) and output element requested at once: one
-        // memory round trip instead of two; same arithmetic and order as below
-        float ms[kFew], ls[kFew];
-        uint16_t os[kFew];
+    const int tpr = HD / 4, rows = kCombThreads / tpr;  // threads per row, rows per workgroup
+    const int rl = (int)threadIdx.x / tpr, c = (int)threadIdx.x % tpr;
+    const int64_t nrows = (int64_t)p.n_heads * p.M;
+    const int64_t row = min((int64_t)blockIdx.x * rows + rl, nrows - 1);  // = head * M + m
+    const rsrc_t ro = make_rsrc(p.part_o, (uint32_t)(ns * nrows * HD * 2));
+    const rsrc_t rml = make_rsrc(p.part_ml, (uint32_t)(ns * nrows * 8));
+    const uint32_t vo = (uint32_t)((row * HD + 4 * c) * 2), vml = (uint32_t)(row * 8);
+    uintx2 ov[NS], ml[NS];
 #pragma unroll
-        for (int s = 0; s < kFew; s++) {
-            if (s < ns) {
-                const int64_t pi = pi0 + s * stride;
-                ms[s] = p.part_ml[2 * pi];
-                ls[s] = p.part_ml[2 * pi + 1];
-                os[s] = po[pi * HD + d];
-            }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int s = 0; s < kFew; s++)
-            if (s < ns) mx = fmaxf(mx, ms[s]);
-        float W = 0.f, acc = 0.f;
-#pragma unroll
-        for (int s = 0; s < kFew; s++) {
-            if (s < ns) {
-                const float w = ms[s] == -INFINITY ? 0.f : ls[s] * exp2f(ms[s] - mx);
-                W += w;
-                acc += h2f(os[s]) * w;
-            }
-        }
-        const int64_t k = (int64_t)head * HD + d;
-        p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / W);
-        return;
+    for (int sp = 0; sp < NS; sp++) {
+        const bool on = sp < ns;
+        ov[sp] = bld8(ro, vo, uni(on ? (uint32_t)(sp * nrows * HD * 2) : 0x80000000u));
+        ml[sp] = bld8(rml, vml, uni(on ? (uint32_t)(sp * nrows * 8) : 0x80000000u));
     }
     float mx = -INFINITY;
-    for (int s = 0; s < ns; s++) mx = fmaxf(mx, p.part_ml[2 * (pi0 + s * stride)]);
-    float W = 0.f, acc = 0.f;
-#pragma unroll 4
-    for (int s = 0; s < ns; s++) {
-        const int64_t pi = pi0 + s * stride;
-        const float ms = p.part_ml[2 * pi];
-        const float w = ms == -INFINITY ? 0.f : p.part_ml[2 * pi + 1] * exp2f(ms - mx);
-        W += w;
-        acc += h2f(po[pi * HD + d]) * w;
+#pragma unroll
+    for (int sp = 0; sp < NS; sp++)
+        if (sp < ns) mx = fmaxf(mx, __uint_as_float(ml[sp].x));
+    float W = 0.f, acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < NS; sp++) {
+        if (sp < ns) {
+            const float ms = __uint_as_float(ml[sp].x);
+            const float w = ms == -INFINITY ? 0.f : __uint_as_float(ml[sp].y) * exp2f(ms - mx);
+            W += w;
+            const uint32_t wd[2] = {ov[sp].x, ov[sp].y};
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += h2f((uint16_t)(wd[i >> 1] >> (16 * (i & 1)))) * w;
+        }
     }
-    const int64_t k = (int64_t)head * HD + d;
-    p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc / W);
+    if ((int64_t)blockIdx.x * rows + rl >= nrows) return;
+    const int head = (int)(row / p.M), m = (int)(row % p.M);
+    // dims 4c .. 4c + 3 sit in fragment slots f, f + 2, f + 1, f + 3
+    const int64_t k = (int64_t)head * HD + 4 * c;
+    uint16_t *dst = p.out16 + (int64_t)m * p.out_ld + frag_index(k);
+    *(uintx2 *)dst = uintx2{(uint32_t)f2h(acc[0] / W) | ((uint32_t)f2h(acc[2] / W) << 16),
+                            (uint32_t)f2h(acc[1] / W) | ((uint32_t)f2h(acc[3] / W) << 16)};
 }
 
 // ---- host launchers ----------------------------------------------------------
@@ -789,18 +796,18 @@ static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
 
 // Up to 16 rows (a linear verify or a decode step) the key ranges are a
 // function of P alone, so each row's arithmetic is the same as in a one-row
-// call.  Above, the splits shrink as query tiles grow, towards 2 resident
-// waves per SIMD (512 workgroups of 4 waves).
+// call.  Above, the splits shrink as query blocks grow, towards one 8-wave
+// workgroup per CU (256).
 AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
     const int T = P + M;
     if (M > 16) {
-        // k_attn_t: splits of kps keys (a multiple of 128), towards 256
-        // workgroups over the query blocks
-        const int nqt = (M * n_rep + 15) / 16, nqb = (nqt + 4 * kTQW - 1) / (4 * kTQW);
+        // k_attn_t: splits of kps keys (whole 32-key blocks), towards one
+        // workgroup per CU over the query blocks
+        const int nqt = (M * n_rep + 15) / 16, nqb = (nqt + kTWaves * kTQW - 1) / (kTWaves * kTQW);
         int want = 256 / (n_kv * nqb);
         want = want < 1 ? 1 : want > kTMaxSplits ? kTMaxSplits : want;
         int kps = (P + 1 + want - 1) / want;
-        kps = kps < 128 ? 128 : (kps + 127) / 128 * 128;
+        kps = kps < 32 ? 32 : (kps + 31) / 32 * 32;
         return AttnSplit{kps / 4, (T + kps - 1) / kps};
     }
     const int want = attn_target_splits(n_kv);
@@ -809,11 +816,12 @@ AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
     return AttnSplit{kpw, (T + 4 * kpw - 1) / (4 * kpw)};
 }
 
-// split size >= (P + 1) / want and >= 128 >= M, so
-// nsplit = ceil((P + M) / size) <= want + 1
+// split size >= (P + 1) / want and >= 32, so for M <= 128
+// nsplit = ceil((P + M) / size) <= want + 1 + 128 / 32
 int attn_max_splits(int n_kv) {
     const int t = attn_target_splits(n_kv);
-    return (t > kTMaxSplits ? t : kTMaxSplits) + 3;
+    const int n = (t > kTMaxSplits ? t : kTMaxSplits) + 5;
+    return n < kCombMaxSplits ? n : kCombMaxSplits;
 }
 
 // LDS beyond the 64 KiB default for the M > 16 kernel: a function attribute
@@ -835,7 +843,10 @@ static void allow_attn_t_lds() {
 }
 
 void launch_attention(const AttnParams &p, hipStream_t st) {
-    if (p.keys_per_wave < 32 || p.keys_per_wave % 32) throw BackendError("attention: keys_per_wave");
+    // a split covers 4 * keys_per_wave keys: whole 32-key blocks, and whole
+    // 32-key steps of each of the 4 waves up to 16 rows
+    const int kps_unit = p.M > 16 ? 8 : 32;
+    if (p.keys_per_wave < kps_unit || p.keys_per_wave % kps_unit) throw BackendError("attention: keys_per_wave");
     if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
     if ((int64_t)(p.nsplit - 1) * 4 * p.keys_per_wave >= (int64_t)p.P + p.M) throw BackendError("attention: empty split");
     if (p.cap % 32 || (int64_t)p.P + p.M > p.cap) throw BackendError("attention: cache capacity");
@@ -843,12 +854,11 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.hd != 128 && p.hd != 64) throw BackendError("attention: head_dim must be 64 or 128");
     const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
     if (p.M > 16) {
-        // query blocks of 4 waves x kTQW tiles sharing each key block through LDS
-        const dim3 grid(p.n_kv, p.nsplit, (nqt + 4 * kTQW - 1) / (4 * kTQW));
-        if (p.keys_per_wave * 4 % (32 * kTKS)) throw BackendError("attention: split size");
+        // query blocks of 8 waves x kTQW tiles sharing each key block through LDS
+        const dim3 grid(p.n_kv, p.nsplit, (nqt + kTWaves * kTQW - 1) / (kTWaves * kTQW));
         allow_attn_t_lds();
-        if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(256 * kTKS), attn_t_lds<128>(), st, p);
-        else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(256 * kTKS), attn_t_lds<64>(), st, p);
+        if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(kTThreads), attn_t_lds<128>(), st, p);
+        else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(kTThreads), attn_t_lds<64>(), st, p);
     } else {
         AttnParams a = p;
         a.fused_combine = 0;
@@ -867,7 +877,16 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
         else hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, a);
         if (a.fused_combine) return;
     }
-    if (p.nsplit > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, p.M), dim3(p.hd), 0, st, p);
+    if (p.nsplit > 1) {
+        if (p.nsplit > kCombMaxSplits) throw BackendError("attention: too many splits to combine");
+        const int rows = kCombThreads / (p.hd / 4);
+        const int64_t nrows = (int64_t)p.n_heads * p.M;
+        if ((int64_t)p.nsplit * nrows * p.hd * 2 >= 0x80000000LL) throw BackendError("attention: partials too large");
+        const dim3 grid((unsigned)((nrows + rows - 1) / rows)), block(kCombThreads);
+        if (p.nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p);
+        else if (p.nsplit <= 40) hipLaunchKernelGGL(k_attn_combine<40>, grid, block, 0, st, p);
+        else hipLaunchKernelGGL(k_attn_combine<kCombMaxSplits>, grid, block, 0, st, p);
+    }
 }
 
 }  // namespace sd

@@ -25,7 +25,7 @@ struct RopeKvParams {
 // head layout only (never of M), so a query's arithmetic does not depend on
 // how many other queries share the call.
 struct AttnSplit {
-    int keys_per_wave;  // multiple of 32; a workgroup covers 4 * keys_per_wave keys
+    int keys_per_wave;  // a split covers 4 * keys_per_wave keys (multiple of 32 up to 16 rows, of 8 above)
     int nsplit;         // workgroups along the keys (for T = P + M keys)
 };
 AttnSplit attn_split(int P, int M, int n_kv, int n_rep);
