@@ -383,6 +383,45 @@ template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnPara
     const int head = h * p.n_rep + (live ? q % p.n_rep : 0), m = live ? q / p.n_rep : 0;
     const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
     const int64_t pi0 = (int64_t)head * p.M + m;
+    if (ns <= 8) {
+        // every split's (m, l) and pieces requested at once: one memory round
+        // trip; the same arithmetic and order as below
+        if (!live) return;
+        const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
+        uint64_t mlv[8], ov[8][DPT / 4];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            mlv[j] = j < ns ? ld_dev64(p.part_ml + 2 * (pi0 + j * stride)) : 0ull;
+#pragma unroll
+            for (int k = 0; k < DPT / 4; k++) ov[j][k] = j < ns ? ld_dev64(po + j * stride * HD + 4 * k) : 0ull;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j < ns) mx = fmaxf(mx, __uint_as_float((uint32_t)mlv[j]));
+        float W = 0.f, acc[DPT];
+#pragma unroll
+        for (int i = 0; i < DPT; i++) acc[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j < ns) {
+                const float ms = __uint_as_float((uint32_t)mlv[j]);
+                const float w = ms == -INFINITY ? 0.f : __uint_as_float((uint32_t)(mlv[j] >> 32)) * exp2f(ms - mx);
+                W += w;
+#pragma unroll
+                for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
+            }
+        }
+        // dims 4k .. 4k + 3 of this thread sit in fragment slots f, f + 2, f + 1, f + 3
+#pragma unroll
+        for (int k = 0; k < DPT / 4; k++) {
+            const int64_t e = (int64_t)head * HD + c * DPT + 4 * k;
+            *(uintx2 *)(p.out16 + (int64_t)m * p.out_ld + frag_index(e)) =
+                uintx2{(uint32_t)f2h(acc[4 * k] / W) | ((uint32_t)f2h(acc[4 * k + 2] / W) << 16),
+                       (uint32_t)f2h(acc[4 * k + 1] / W) | ((uint32_t)f2h(acc[4 * k + 3] / W) << 16)};
+        }
+        return;
+    }
     for (int s = c; s < ns; s += 16) {
         const uint64_t v = live ? ld_dev64(p.part_ml + 2 * (pi0 + s * stride)) : 0ull;
         cml[r][s][0] = __uint_as_float((uint32_t)v);

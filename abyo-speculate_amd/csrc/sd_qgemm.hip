@@ -634,10 +634,37 @@ __device__ __forceinline__ void qmm_step1(const typename QFmt<FMT>::D (&w)[RT], 
     }
 }
 
-__device__ __forceinline__ void load_x(uintx4 (&b)[8], rsrc_t xr, uint32_t xvo, int sb) {
+// The activations of superblock sb: XL loads of 16 bytes per lane.  XL = 8:
+// load c is chunk c of token r16.  XL = 4 (up to 8 tokens): lanes r16 < 8 load
+// chunk 2j of token r16 and lanes r16 >= 8 chunk 2j + 1 of token r16 - 8 (the
+// lane's xvo carries the chunk and token), so load j holds chunk 2j for the
+// live tokens and chunk 2j + 1 one row of 8 lanes up (see x_chunks).
+template <int XL>
+__device__ __forceinline__ void load_x(uintx4 (&b)[XL], rsrc_t xr, uint32_t xvo, int sb) {
     const uint32_t so = uni(sb < 0 ? kNoLoad : (uint32_t)sb * 512u);
 #pragma unroll
-    for (int c = 0; c < 8; c++) b[c] = bld16(xr, xvo + 64 * c, so);
+    for (int c = 0; c < XL; c++) b[c] = bld16(xr, xvo + (512 / XL) * c, so);
+}
+// the 8 chunk operands of a superblock: with XL = 4, chunk 2j + 1 of token t
+// comes from lane t + 8 of the same 16-lane row (rows t >= 8 of the MFMA
+// tile hold other data; their products belong to no token and are dropped)
+// DPP row_shl:8: lane i of each 16-lane row takes lane i + 8 (i < 8); the
+// upper 8 lanes keep their own value
+__device__ __forceinline__ uint32_t row_shl8(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x108, 0xF, 0xF, false);
+}
+template <int XL>
+__device__ __forceinline__ void x_chunks(const uintx4 (&b)[XL], uintx4 (&x)[8]) {
+    if constexpr (XL == 8) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) x[c] = b[c];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[2 * j] = b[j];
+            x[2 * j + 1] = uintx4{row_shl8(b[j].x), row_shl8(b[j].y), row_shl8(b[j].z), row_shl8(b[j].w)};
+        }
+    }
 }
 
 // ---- fused RMSNorm, input side ------------------------------------------------
@@ -667,7 +694,7 @@ __device__ __forceinline__ float norm_add(float s, const floatx4 &v) { return s 
 // Superblocks sb = ks, ks + KW, ... in increasing order, x and weights of the
 // next superblock in flight during this one; `after_prologue` runs once the
 // first superblock's loads are in flight.
-template <int FMT, int RT, int KW, typename Hook>
+template <int FMT, int RT, int KW, int XL, typename Hook>
 __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[RT], int ks, floatx4 (&acc)[RT],
                                          float &nsum, const half8 &sel, Hook &&after_prologue) {
     typedef QFmt<FMT> F;
@@ -677,14 +704,15 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
     // token rows past M read the last real token's row: the loads coalesce
     // with that lane's and the padding tokens are never stored
     const rsrc_t xr = make_rsrc(p.xp, (uint32_t)p.M * (uint32_t)p.K * 2u);
-    const uint32_t xvo = ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u;
+    const uint32_t xvo = XL == 8 ? ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u
+                                 : ((uint32_t)min(r16 & 7, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u + (r16 >= 8 ? 64u : 0u);
     if (ks >= nsb) return;
     const int nst = (nsb - ks + KW - 1) / KW;  // superblocks of this wave: ks + i * KW, i < nst
     auto sbi = [&](int i) { return i < nst ? ks + i * KW : -1; };
     typename F::D w0[RT], w1[RT];
-    uintx4 b0[8], b1[8];
+    uintx4 b0[XL], b1[XL], xc[8];
     const NormSrc ns = norm_src(p);
-    load_x(b0, xr, xvo, sbi(0));
+    load_x<XL>(b0, xr, xvo, sbi(0));
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(0), g);
     floatx4 n0 = norm_load(ns, sbi(0)), n1;  // after the weights: waiting for them does not wait for it
@@ -692,25 +720,27 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
     IntCarry<RT> cy;
     cy.live = false;
     for (int i = 0;; i += 2) {
-        load_x(b1, xr, xvo, sbi(i + 1));
+        load_x<XL>(b1, xr, xvo, sbi(i + 1));
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w1[rt], row[rt], nsb, sbi(i + 1), g);
         n1 = norm_load(ns, sbi(i + 1));
-        qmm_step1<FMT, RT>(w0, b0, g, acc, sel, cy);
+        x_chunks<XL>(b0, xc);
+        qmm_step1<FMT, RT>(w0, xc, g, acc, sel, cy);
         nsum = norm_add(nsum, n0);
         if (i + 1 >= nst) break;
-        load_x(b0, xr, xvo, sbi(i + 2));
+        load_x<XL>(b0, xr, xvo, sbi(i + 2));
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) F::load(w0[rt], row[rt], nsb, sbi(i + 2), g);
         n0 = norm_load(ns, sbi(i + 2));
-        qmm_step1<FMT, RT>(w1, b1, g, acc, sel, cy);
+        x_chunks<XL>(b1, xc);
+        qmm_step1<FMT, RT>(w1, xc, g, acc, sel, cy);
         nsum = norm_add(nsum, n1);
         if (i + 2 >= nst) break;
     }
     int_drain<RT>(cy, acc);
 }
 
-template <int RT, int KW>
+template <int RT, int KW, int XL>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
     warm_kernargs<sizeof(GemmParams)>();
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -770,10 +800,10 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
     };
     float nsum = 0.f;
     switch (S[0].fmt) {
-    case Q4_K: qmm_body<Q4_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
-    case Q5_K: qmm_body<Q5_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
-    case Q6_K: qmm_body<Q6_K, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
-    case Q8_0: qmm_body<Q8_0, RT, KW>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q4_K: qmm_body<Q4_K, RT, KW, XL>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q5_K: qmm_body<Q5_K, RT, KW, XL>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q6_K: qmm_body<Q6_K, RT, KW, XL>(p, row, wave, acc, nsum, sel, after_prologue); break;
+    case Q8_0: qmm_body<Q8_0, RT, KW, XL>(p, row, wave, acc, nsum, sel, after_prologue); break;
     default: break;
     }
     // Fixed-order cross-wave reduction (w = 0, 1, ..., KW-1) through LDS, which
@@ -1096,7 +1126,9 @@ static void launch_qgx(const GemmParams &p, hipStream_t st, const LaunchTiming &
 
 template <int RT, int KW>
 static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st, const LaunchTiming &tm) {
-    launch_timed(k_qmm<RT, KW>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
+    // up to 8 tokens the activations of a superblock take half the loads (load_x)
+    if (p.M <= 8) launch_timed(k_qmm<RT, KW, 4>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
+    else launch_timed(k_qmm<RT, KW, 8>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
 }
 
 template <int RT>
