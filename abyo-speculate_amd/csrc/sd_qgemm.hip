@@ -638,7 +638,8 @@ __device__ __forceinline__ void qmm_step1(const typename QFmt<FMT>::D (&w)[RT], 
 // load c is chunk c of token r16.  XL = 4 (up to 8 tokens): lanes r16 < 8 load
 // chunk 2j of token r16 and lanes r16 >= 8 chunk 2j + 1 of token r16 - 8 (the
 // lane's xvo carries the chunk and token), so load j holds chunk 2j for the
-// live tokens and chunk 2j + 1 one row of 8 lanes up (see x_chunks).
+// live tokens and chunk 2j + 1 one row of 8 lanes up (see x_chunks).  XL = 2
+// (up to 4 tokens): lane group q = r16 / 4 loads chunk 4j + q of token r16 % 4.
 template <int XL>
 __device__ __forceinline__ void load_x(uintx4 (&b)[XL], rsrc_t xr, uint32_t xvo, int sb) {
     const uint32_t so = uni(sb < 0 ? kNoLoad : (uint32_t)sb * 512u);
@@ -648,21 +649,32 @@ __device__ __forceinline__ void load_x(uintx4 (&b)[XL], rsrc_t xr, uint32_t xvo,
 // the 8 chunk operands of a superblock: with XL = 4, chunk 2j + 1 of token t
 // comes from lane t + 8 of the same 16-lane row (rows t >= 8 of the MFMA
 // tile hold other data; their products belong to no token and are dropped)
-// DPP row_shl:8: lane i of each 16-lane row takes lane i + 8 (i < 8); the
-// upper 8 lanes keep their own value
-__device__ __forceinline__ uint32_t row_shl8(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x108, 0xF, 0xF, false);
+// DPP row_shl:N: lane i of each 16-lane row takes lane i + N (i < 16 - N);
+// the upper N lanes keep their own value
+template <int N> __device__ __forceinline__ uint32_t row_shl(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x100 + N, 0xF, 0xF, false);
+}
+template <int N> __device__ __forceinline__ uintx4 row_shl4(const uintx4 &v) {
+    return uintx4{row_shl<N>(v.x), row_shl<N>(v.y), row_shl<N>(v.z), row_shl<N>(v.w)};
 }
 template <int XL>
 __device__ __forceinline__ void x_chunks(const uintx4 (&b)[XL], uintx4 (&x)[8]) {
     if constexpr (XL == 8) {
 #pragma unroll
         for (int c = 0; c < 8; c++) x[c] = b[c];
-    } else {
+    } else if constexpr (XL == 4) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             x[2 * j] = b[j];
-            x[2 * j + 1] = uintx4{row_shl8(b[j].x), row_shl8(b[j].y), row_shl8(b[j].z), row_shl8(b[j].w)};
+            x[2 * j + 1] = row_shl4<8>(b[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            x[4 * j] = b[j];
+            x[4 * j + 1] = row_shl4<4>(b[j]);
+            x[4 * j + 2] = row_shl4<8>(b[j]);
+            x[4 * j + 3] = row_shl4<12>(b[j]);
         }
     }
 }
@@ -704,8 +716,9 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
     // token rows past M read the last real token's row: the loads coalesce
     // with that lane's and the padding tokens are never stored
     const rsrc_t xr = make_rsrc(p.xp, (uint32_t)p.M * (uint32_t)p.K * 2u);
-    const uint32_t xvo = XL == 8 ? ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u
-                                 : ((uint32_t)min(r16 & 7, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u + (r16 >= 8 ? 64u : 0u);
+    const uint32_t xvo = XL == 8   ? ((uint32_t)min(r16, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u
+                         : XL == 4 ? ((uint32_t)min(r16 & 7, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u + (r16 >= 8 ? 64u : 0u)
+                                   : ((uint32_t)min(r16 & 3, p.M - 1) * (uint32_t)p.K + 8u * g) * 2u + 64u * (uint32_t)(r16 >> 2);
     if (ks >= nsb) return;
     const int nst = (nsb - ks + KW - 1) / KW;  // superblocks of this wave: ks + i * KW, i < nst
     auto sbi = [&](int i) { return i < nst ? ks + i * KW : -1; };
@@ -1126,8 +1139,10 @@ static void launch_qgx(const GemmParams &p, hipStream_t st, const LaunchTiming &
 
 template <int RT, int KW>
 static void launch_qmm(const GemmParams &p, int nwg, hipStream_t st, const LaunchTiming &tm) {
-    // up to 8 tokens the activations of a superblock take half the loads (load_x)
-    if (p.M <= 8) launch_timed(k_qmm<RT, KW, 4>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
+    // up to 8 (4) tokens the activations of a superblock take half (a quarter)
+    // of the loads (load_x)
+    if (p.M <= 4) launch_timed(k_qmm<RT, KW, 2>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
+    else if (p.M <= 8) launch_timed(k_qmm<RT, KW, 4>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
     else launch_timed(k_qmm<RT, KW, 8>, dim3(nwg), dim3(64 * KW), 0, st, tm, p);
 }
 
