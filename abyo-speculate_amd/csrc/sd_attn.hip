@@ -769,56 +769,71 @@ __global__ __launch_bounds__(kTThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 }
 
 // ---- combine splits -> fp16 fragment-layout input of wo ----------------------
-// Thread (row, c) of a 128-thread workgroup owns dims [4c, 4c + 4) of one
-// partial row (head, m) and requests every split's (m_s, l_s) and its 4 dims
-// at once (up to NS splits; loads past nsplit read zeros without a memory
-// access), so the merge waits for one memory round trip, and the grid has a
-// workgroup per 4 rows.  Splits are merged in index order:
+// Thread (row, c) of a 128-thread workgroup owns dims [8c, 8c + 8) of one
+// partial row (head, m).  The row's threads stage every split's (m_s, l_s)
+// in LDS (thread c loads splits c, c + 16, ...), and each thread requests its
+// dims of every split at once (up to NS splits; loads past nsplit read zeros
+// without a memory access), so the merge waits for one memory round trip.
+// Splits are merged in index order:
 // out = sum_s w_s o_s / sum_s w_s, w_s = l_s * exp2(m_s - max m).
 constexpr int kCombThreads = 128;
-constexpr int kCombMaxSplits = 72;  // >= attn_max_splits for every n_kv
+constexpr int kCombMaxSplits = 80;  // >= attn_max_splits for every n_kv
 template <int NS> __global__ __launch_bounds__(kCombThreads) void k_attn_combine(AttnParams p) {
     warm_kernargs<sizeof(AttnParams)>();
     const int HD = p.hd, ns = p.nsplit;
-    const int tpr = HD / 4, rows = kCombThreads / tpr;  // threads per row, rows per workgroup
+    const int tpr = HD / 8, rows = kCombThreads / tpr;  // threads per row, rows per workgroup
     const int rl = (int)threadIdx.x / tpr, c = (int)threadIdx.x % tpr;
     const int64_t nrows = (int64_t)p.n_heads * p.M;
     const int64_t row = min((int64_t)blockIdx.x * rows + rl, nrows - 1);  // = head * M + m
     const rsrc_t ro = make_rsrc(p.part_o, (uint32_t)(ns * nrows * HD * 2));
     const rsrc_t rml = make_rsrc(p.part_ml, (uint32_t)(ns * nrows * 8));
-    const uint32_t vo = (uint32_t)((row * HD + 4 * c) * 2), vml = (uint32_t)(row * 8);
-    uintx2 ov[NS], ml[NS];
+    const uint32_t vo = (uint32_t)((row * HD + 8 * c) * 2), vml = (uint32_t)(row * 8);
+    constexpr int NML = (NS + 7) / 8;  // (m, l) loads of a thread (tpr >= 8)
+    uintx2 ml[NML];
 #pragma unroll
-    for (int sp = 0; sp < NS; sp++) {
-        const bool on = sp < ns;
-        ov[sp] = bld8(ro, vo, uni(on ? (uint32_t)(sp * nrows * HD * 2) : 0x80000000u));
-        ml[sp] = bld8(rml, vml, uni(on ? (uint32_t)(sp * nrows * 8) : 0x80000000u));
+    for (int i = 0; i < NML; i++) {
+        const int sp = c + tpr * i;
+        ml[i] = bld8(rml, sp < ns ? vml + (uint32_t)(sp * nrows * 8) : 0x80000000u, 0u);
     }
+    uintx4 ov[NS];
+#pragma unroll
+    for (int sp = 0; sp < NS; sp++) ov[sp] = bld16(ro, vo, uni(sp < ns ? (uint32_t)(sp * nrows * HD * 2) : 0x80000000u));
+    __shared__ float cml[kCombThreads / 8][kCombMaxSplits][2];
+#pragma unroll
+    for (int i = 0; i < NML; i++) {
+        const int sp = c + tpr * i;
+        if (sp < ns) {
+            cml[rl][sp][0] = __uint_as_float(ml[i].x);
+            cml[rl][sp][1] = __uint_as_float(ml[i].y);
+        }
+    }
+    __syncthreads();
     float mx = -INFINITY;
+    for (int sp = 0; sp < ns; sp++) mx = fmaxf(mx, cml[rl][sp][0]);
+    float W = 0.f, acc[8];
 #pragma unroll
-    for (int sp = 0; sp < NS; sp++)
-        if (sp < ns) mx = fmaxf(mx, __uint_as_float(ml[sp].x));
-    float W = 0.f, acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = 0.f;
+    for (int i = 0; i < 8; i++) acc[i] = 0.f;
 #pragma unroll
     for (int sp = 0; sp < NS; sp++) {
         if (sp < ns) {
-            const float ms = __uint_as_float(ml[sp].x);
-            const float w = ms == -INFINITY ? 0.f : __uint_as_float(ml[sp].y) * exp2f(ms - mx);
+            const float ms = cml[rl][sp][0];
+            const float w = ms == -INFINITY ? 0.f : cml[rl][sp][1] * exp2f(ms - mx);
             W += w;
-            const uint32_t wd[2] = {ov[sp].x, ov[sp].y};
+            const uint32_t wd[4] = {ov[sp].x, ov[sp].y, ov[sp].z, ov[sp].w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] += h2f((uint16_t)(wd[i >> 1] >> (16 * (i & 1)))) * w;
+            for (int i = 0; i < 8; i++) acc[i] += h2f((uint16_t)(wd[i >> 1] >> (16 * (i & 1)))) * w;
         }
     }
     if ((int64_t)blockIdx.x * rows + rl >= nrows) return;
     const int head = (int)(row / p.M), m = (int)(row % p.M);
-    // dims 4c .. 4c + 3 sit in fragment slots f, f + 2, f + 1, f + 3
-    const int64_t k = (int64_t)head * HD + 4 * c;
-    uint16_t *dst = p.out16 + (int64_t)m * p.out_ld + frag_index(k);
-    *(uintx2 *)dst = uintx2{(uint32_t)f2h(acc[0] / W) | ((uint32_t)f2h(acc[2] / W) << 16),
-                            (uint32_t)f2h(acc[1] / W) | ((uint32_t)f2h(acc[3] / W) << 16)};
+    // dims 4k .. 4k + 3 sit in fragment slots f, f + 2, f + 1, f + 3
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int64_t e = (int64_t)head * HD + 8 * c + 4 * k;
+        *(uintx2 *)(p.out16 + (int64_t)m * p.out_ld + frag_index(e)) =
+            uintx2{(uint32_t)f2h(acc[4 * k] / W) | ((uint32_t)f2h(acc[4 * k + 2] / W) << 16),
+                   (uint32_t)f2h(acc[4 * k + 1] / W) | ((uint32_t)f2h(acc[4 * k + 3] / W) << 16)};
+    }
 }
 
 // ---- host launchers ----------------------------------------------------------
@@ -918,11 +933,14 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
     }
     if (p.nsplit > 1) {
         if (p.nsplit > kCombMaxSplits) throw BackendError("attention: too many splits to combine");
-        const int rows = kCombThreads / (p.hd / 4);
+        const int rows = kCombThreads / (p.hd / 8);
         const int64_t nrows = (int64_t)p.n_heads * p.M;
         if ((int64_t)p.nsplit * nrows * p.hd * 2 >= 0x80000000LL) throw BackendError("attention: partials too large");
         const dim3 grid((unsigned)((nrows + rows - 1) / rows)), block(kCombThreads);
-        if (p.nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p);
+        if (p.nsplit <= 8) hipLaunchKernelGGL(k_attn_combine<8>, grid, block, 0, st, p);
+        else if (p.nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p);
+        else if (p.nsplit <= 24) hipLaunchKernelGGL(k_attn_combine<24>, grid, block, 0, st, p);
+        else if (p.nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, grid, block, 0, st, p);
         else if (p.nsplit <= 40) hipLaunchKernelGGL(k_attn_combine<40>, grid, block, 0, st, p);
         else hipLaunchKernelGGL(k_attn_combine<kCombMaxSplits>, grid, block, 0, st, p);
     }
