@@ -39,58 +39,92 @@ namespace sd {
 #pragma clang fp contract(off)
 
 // ---- RoPE + KV append ------------------------------------------------------
-// projection output (m, col): the matmul's value, or its K-slice partials
-// added in slice order plus the bias
-__device__ __forceinline__ float qkv_at(const RopeKvParams &p, int m, int col) {
+// four consecutive columns of the projection output (col % 4 == 0): the
+// matmul's values, or its K-slice partials added in slice order plus the bias
+__device__ __forceinline__ float4 qkv_at4(const RopeKvParams &p, int m, int col) {
     const int64_t at = (int64_t)m * p.ld_qkv + col;
-    if (p.nks <= 1) return p.qkv[at];
+    if (p.nks <= 1) return *(const float4 *)(p.qkv + at);
     const int64_t stride = (int64_t)p.M * p.ld_qkv;
     // up to 8 slices, all loaded before the first add
-    float a[8];
+    float4 a[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) a[k] = k < p.nks ? p.part[at + k * stride] : 0.f;
-    float v = a[0];
+    for (int k = 0; k < 8; k++) a[k] = k < p.nks ? *(const float4 *)(p.part + at + k * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v = a[0];
 #pragma unroll
     for (int k = 1; k < 8; k++)
-        if (k < p.nks) v += a[k];
+        if (k < p.nks) {
+            v.x += a[k].x;
+            v.y += a[k].y;
+            v.z += a[k].z;
+            v.w += a[k].w;
+        }
     if (!p.bq) return v;
     const int qd = p.n_heads * p.hd, kvd = p.n_kv * p.hd;
-    return v + (col < qd ? p.bq[col] : col < qd + kvd ? p.bk[col - qd] : p.bv[col - qd - kvd]);
+    const float *b = col < qd ? p.bq + col : col < qd + kvd ? p.bk + (col - qd) : p.bv + (col - qd - kvd);
+    const float4 bb = *(const float4 *)b;
+    v.x += bb.x;
+    v.y += bb.y;
+    v.z += bb.z;
+    v.w += bb.w;
+    return v;
+}
+__device__ __forceinline__ void st4h_f(uint16_t *dst, float a, float b, float c, float d) {
+    *(uintx2 *)dst = uintx2{(uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16), (uint32_t)f2h(c) | ((uint32_t)f2h(d) << 16)};
 }
 
-// grid (M, n_heads + n_kv), block hd/2 threads
-__global__ void k_rope_kv(RopeKvParams p) {
+// grid (M, ceil((n_heads + n_kv) * hd / 4 / 64)), block 64: thread (head hh,
+// unit j) owns columns d = 4j .. 4j + 3 of the head (with half rotation the
+// q / k units of the lower half also own d + hd/2 .., the upper half's idle);
+// a KV head's thread does both its k and its v columns.
+__global__ __launch_bounds__(64) void k_rope_kv(RopeKvParams p) {
     warm_kernargs<sizeof(RopeKvParams)>();
-    const int m = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
-    const int half = p.hd / 2;
-    if (i >= half) return;
+    const int m = blockIdx.x, hd = p.hd, half = hd / 2, upr = hd / 4;
+    const int t = (int)blockIdx.y * 64 + (int)threadIdx.x;
+    if (t >= (p.n_heads + p.n_kv) * upr) return;
+    const int hh = t / upr, d = 4 * (t % upr);
     const int pos = p.pos[m];
-    const float c = p.cos_t[(int64_t)pos * half + i], s = p.sin_t[(int64_t)pos * half + i];
-    int a, b;  // element pair
+    const float *ct = p.cos_t + (int64_t)pos * half, *st = p.sin_t + (int64_t)pos * half;
+    const bool q_head = hh < p.n_heads;
+    const int kvh = hh - p.n_heads;
+    const int col = q_head ? hh * hd : p.n_heads * hd + kvh * hd;  // q or k columns of the head
+    const int64_t tk = (int64_t)p.P + m;
+    if (!q_head) {
+        // v: copied (fp16) into the cache
+        const float4 v = qkv_at4(p, m, (p.n_heads + p.n_kv) * hd + kvh * hd + d);
+        uint16_t *vs = p.vc + (int64_t)kvh * p.cap * hd;
+        vs[kv_v_off(tk, d, hd)] = f2h(v.x);
+        vs[kv_v_off(tk, d + 1, hd)] = f2h(v.y);
+        vs[kv_v_off(tk, d + 2, hd)] = f2h(v.z);
+        vs[kv_v_off(tk, d + 3, hd)] = f2h(v.w);
+    }
+    uint16_t *lo, *hi = nullptr;
+    if (q_head) {
+        lo = p.q16 + ((int64_t)hh * p.M + m) * hd + d;
+        hi = lo + half;
+    } else {
+        uint16_t *ks = p.kc + (int64_t)kvh * p.cap * hd;
+        lo = ks + kv_k_off(tk, d, hd);
+        hi = ks + kv_k_off(tk, d + half, hd);
+    }
+    const float4 x = qkv_at4(p, m, col + d);
     if (p.interleaved) {
-        a = 2 * i;
-        b = 2 * i + 1;
-    } else {
-        a = i;
-        b = i + half;
+        // pairs (d, d+1), (d+2, d+3): rotation indices d/2, d/2 + 1
+        const float c0 = ct[d / 2], s0 = st[d / 2], c1 = ct[d / 2 + 1], s1 = st[d / 2 + 1];
+        st4h_f(lo, x.x * c0 - x.y * s0, x.x * s0 + x.y * c0, x.z * c1 - x.w * s1, x.z * s1 + x.w * c1);
+        return;
     }
-    if (hh < p.n_heads) {
-        const int c0 = hh * p.hd;
-        const float x0 = qkv_at(p, m, c0 + a), x1 = qkv_at(p, m, c0 + b);
-        uint16_t *q = p.q16 + ((int64_t)hh * p.M + m) * p.hd;
-        q[a] = f2h(x0 * c - x1 * s);
-        q[b] = f2h(x0 * s + x1 * c);
-    } else {
-        const int h = hh - p.n_heads;
-        const int ck = p.n_heads * p.hd + h * p.hd, cv = (p.n_heads + p.n_kv) * p.hd + h * p.hd;
-        uint16_t *ks = p.kc + (int64_t)h * p.cap * p.hd, *vs = p.vc + (int64_t)h * p.cap * p.hd;
-        const int64_t t = p.P + m;
-        const float k0 = qkv_at(p, m, ck + a), k1 = qkv_at(p, m, ck + b);
-        ks[kv_k_off(t, a, p.hd)] = f2h(k0 * c - k1 * s);
-        ks[kv_k_off(t, b, p.hd)] = f2h(k0 * s + k1 * c);
-        vs[kv_v_off(t, a, p.hd)] = f2h(qkv_at(p, m, cv + a));
-        vs[kv_v_off(t, b, p.hd)] = f2h(qkv_at(p, m, cv + b));
+    if (d >= half) return;  // the unit of d - hd/2 rotates these columns
+    const float4 y = qkv_at4(p, m, col + d + half);
+    const float c[4] = {ct[d], ct[d + 1], ct[d + 2], ct[d + 3]}, sn[4] = {st[d], st[d + 1], st[d + 2], st[d + 3]};
+    const float xa[4] = {x.x, x.y, x.z, x.w}, ya[4] = {y.x, y.y, y.z, y.w};
+    float r0[4], r1[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r0[i] = xa[i] * c[i] - ya[i] * sn[i];
+        r1[i] = xa[i] * sn[i] + ya[i] * c[i];
     }
+    st4h_f(lo, r0[0], r0[1], r0[2], r0[3]);
+    st4h_f(hi, r1[0], r1[1], r1[2], r1[3]);
 }
 
 #pragma clang fp contract(fast)
@@ -843,7 +877,9 @@ template <int NS> __global__ __launch_bounds__(kCombThreads) void k_attn_combine
         if (e_ != hipSuccess) throw BackendError(std::string("attention: ") + hipGetErrorString(e_)); \
     } while (0)
 void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
-    hipLaunchKernelGGL(k_rope_kv, dim3(p.M, p.n_heads + p.n_kv), dim3(p.hd / 2), 0, st, p);
+    if (p.hd % 8 || p.ld_qkv % 4) throw BackendError("rope_kv: head_dim must be a multiple of 8");
+    const int units = (p.n_heads + p.n_kv) * (p.hd / 4);
+    hipLaunchKernelGGL(k_rope_kv, dim3(p.M, (units + 63) / 64), dim3(64), 0, st, p);
 }
 
 static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
