@@ -39,25 +39,45 @@ namespace sd {
 #pragma clang fp contract(off)
 
 // ---- RoPE + KV append ------------------------------------------------------
-// four consecutive columns of the projection output (col % 4 == 0): the
-// matmul's values, or its K-slice partials added in slice order plus the bias
-__device__ __forceinline__ float4 qkv_at4(const RopeKvParams &p, int m, int col) {
-    const int64_t at = (int64_t)m * p.ld_qkv + col;
-    if (p.nks <= 1) return *(const float4 *)(p.qkv + at);
-    const int64_t stride = (int64_t)p.M * p.ld_qkv;
-    // up to 8 slices, all loaded before the first add
+// Four consecutive columns (col % 4 == 0) of the projection output: the
+// matmul's values (nks <= 1) or its K-slice partials, requested through
+// buffer resources without branches so that every load of a thread -- both
+// column groups and the token's norm partials -- is in flight before the
+// first wait.
+struct QkvCols {
     float4 a[8];
+};
+constexpr uint32_t kNoCol = 0x80000000u;  // offset past any resource: reads zeros, no memory access
+__device__ __forceinline__ void qkv_load4(const RopeKvParams &p, int m, int col, QkvCols &c) {
+    const bool split = p.nks > 1;
+    const int64_t stride = (int64_t)p.M * p.ld_qkv;
+    const rsrc_t r = make_rsrc(split ? (const void *)p.part : (const void *)p.qkv,
+                               (uint32_t)((split ? p.nks : 1) * stride * 4));
+    const uint32_t at = (uint32_t)(((int64_t)m * p.ld_qkv + col) * 4);
+    const int n = split ? p.nks : 1;
 #pragma unroll
-    for (int k = 0; k < 8; k++) a[k] = k < p.nks ? *(const float4 *)(p.part + at + k * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 v = a[0];
+    for (int k = 0; k < 8; k++)
+        c.a[k] = __builtin_bit_cast(float4, bld16(r, k < n ? at + (uint32_t)(k * stride * 4) : kNoCol, 0u));
+}
+// slices added in slice order, scaled by the input norm (after K slices),
+// plus the bias
+__device__ __forceinline__ float4 qkv_finish4(const RopeKvParams &p, int col, const QkvCols &c, float inv) {
+    if (p.nks <= 1) return c.a[0];
+    float4 v = c.a[0];
 #pragma unroll
     for (int k = 1; k < 8; k++)
         if (k < p.nks) {
-            v.x += a[k].x;
-            v.y += a[k].y;
-            v.z += a[k].z;
-            v.w += a[k].w;
+            v.x += c.a[k].x;
+            v.y += c.a[k].y;
+            v.z += c.a[k].z;
+            v.w += c.a[k].w;
         }
+    if (p.norm_ssq) {
+        v.x *= inv;
+        v.y *= inv;
+        v.z *= inv;
+        v.w *= inv;
+    }
     if (!p.bq) return v;
     const int qd = p.n_heads * p.hd, kvd = p.n_kv * p.hd;
     const float *b = col < qd ? p.bq + col : col < qd + kvd ? p.bk + (col - qd) : p.bv + (col - qd - kvd);
@@ -82,22 +102,55 @@ __global__ __launch_bounds__(64) void k_rope_kv(RopeKvParams p) {
     const int t = (int)blockIdx.y * 64 + (int)threadIdx.x;
     if (t >= (p.n_heads + p.n_kv) * upr) return;
     const int hh = t / upr, d = 4 * (t % upr);
-    const int pos = p.pos[m];
-    const float *ct = p.cos_t + (int64_t)pos * half, *st = p.sin_t + (int64_t)pos * half;
     const bool q_head = hh < p.n_heads;
     const int kvh = hh - p.n_heads;
     const int col = q_head ? hh * hd : p.n_heads * hd + kvh * hd;  // q or k columns of the head
+    const int vcol = (p.n_heads + p.n_kv) * hd + kvh * hd;          // v columns of a KV head
+    const bool pair_hi = !p.interleaved && d < half;                // also rotates d + hd/2
+    // every load first: the token's norm partials (up to 16), the columns,
+    // then the position and its rotation entries
+    const bool has_norm = p.norm_ssq && p.nks > 1 && p.norm_parts <= 16;
+    // (the resource reaches 4 partials past the last token's: a 16-byte load
+    // never straddles its end; ssq holds hidden >= M * parts + 4 floats)
+    const rsrc_t nr = make_rsrc(p.norm_ssq, has_norm ? (uint32_t)((p.M * p.norm_parts + 4) * 4) : 0u);
+    float sv[16];
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+        // four partials per load; the resource ends at the token's last one
+        const float4 q4 = __builtin_bit_cast(
+            float4, bld16(nr, j < p.norm_parts ? (uint32_t)(m * p.norm_parts + j) * 4u : kNoCol, 0u));
+        sv[j] = q4.x;
+        sv[j + 1] = j + 1 < p.norm_parts ? q4.y : 0.f;
+        sv[j + 2] = j + 2 < p.norm_parts ? q4.z : 0.f;
+        sv[j + 3] = j + 3 < p.norm_parts ? q4.w : 0.f;
+    }
+    QkvCols cx, cy, cv;
+    qkv_load4(p, m, col + d, cx);
+    if (pair_hi) qkv_load4(p, m, col + d + half, cy);
+    if (!q_head) qkv_load4(p, m, vcol + d, cv);
+    const int pos = p.pos[m];
+    const float *ct = p.cos_t + (int64_t)pos * half, *st = p.sin_t + (int64_t)pos * half;
+    float inv = 1.f;
+    if (has_norm) {
+        // norm_inv_rms's order
+        float q[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 16; j++) q[j & 3] += sv[j];
+        inv = 1.0f / sqrtf(((q[0] + q[1]) + (q[2] + q[3])) / (float)p.norm_K + p.norm_eps);
+    } else if (p.norm_ssq && p.nks > 1) {
+        inv = norm_inv_rms(p.norm_ssq + (int64_t)m * p.norm_parts, p.norm_parts, p.norm_K, p.norm_eps);
+    }
     const int64_t tk = (int64_t)p.P + m;
     if (!q_head) {
         // v: copied (fp16) into the cache
-        const float4 v = qkv_at4(p, m, (p.n_heads + p.n_kv) * hd + kvh * hd + d);
+        const float4 v = qkv_finish4(p, vcol + d, cv, inv);
         uint16_t *vs = p.vc + (int64_t)kvh * p.cap * hd;
         vs[kv_v_off(tk, d, hd)] = f2h(v.x);
         vs[kv_v_off(tk, d + 1, hd)] = f2h(v.y);
         vs[kv_v_off(tk, d + 2, hd)] = f2h(v.z);
         vs[kv_v_off(tk, d + 3, hd)] = f2h(v.w);
     }
-    uint16_t *lo, *hi = nullptr;
+    uint16_t *lo, *hi;
     if (q_head) {
         lo = p.q16 + ((int64_t)hh * p.M + m) * hd + d;
         hi = lo + half;
@@ -106,15 +159,15 @@ __global__ __launch_bounds__(64) void k_rope_kv(RopeKvParams p) {
         lo = ks + kv_k_off(tk, d, hd);
         hi = ks + kv_k_off(tk, d + half, hd);
     }
-    const float4 x = qkv_at4(p, m, col + d);
+    const float4 x = qkv_finish4(p, col + d, cx, inv);
     if (p.interleaved) {
         // pairs (d, d+1), (d+2, d+3): rotation indices d/2, d/2 + 1
         const float c0 = ct[d / 2], s0 = st[d / 2], c1 = ct[d / 2 + 1], s1 = st[d / 2 + 1];
         st4h_f(lo, x.x * c0 - x.y * s0, x.x * s0 + x.y * c0, x.z * c1 - x.w * s1, x.z * s1 + x.w * c1);
         return;
     }
-    if (d >= half) return;  // the unit of d - hd/2 rotates these columns
-    const float4 y = qkv_at4(p, m, col + d + half);
+    if (!pair_hi) return;  // the unit of d - hd/2 rotates these columns
+    const float4 y = qkv_finish4(p, col + d + half, cy, inv);
     const float c[4] = {ct[d], ct[d + 1], ct[d + 2], ct[d + 3]}, sn[4] = {st[d], st[d + 1], st[d + 2], st[d + 3]};
     const float xa[4] = {x.x, x.y, x.z, x.w}, ya[4] = {y.x, y.y, y.z, y.w};
     float r0[4], r1[4];

@@ -101,6 +101,15 @@ inline uint64_t tensor_seed(uint64_t model_seed, int layer, int kind) {
     return mix64(model_seed ^ tag);
 }
 
+// 1 / rms of one token from its np partial sums of squares (RMSNorm split
+// around a matmul): four running sums over j = i, i + 4, ... added as
+// ((s0 + s1) + (s2 + s3)), the order in which four lanes combine them
+__device__ inline float norm_inv_rms(const float *ssq_row, int np, int K, float eps) {
+    float q[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < np; j++) q[j & 3] += ssq_row[j];
+    return 1.0f / sqrtf(((q[0] + q[1]) + (q[2] + q[3])) / (float)K + eps);
+}
+
 }  // namespace sd
 
 #define SD_HIP_CHECK(expr)                                                        \

@@ -118,6 +118,58 @@ __global__ __launch_bounds__(256) void k_rmsnorm_any(float *x, const float *w, i
     }
 }
 
+// Residual finalisation spread over each row (17..64 rows): x += the K-slice
+// partials of the residual matmul (slice order, nks <= 8), u = fp16(x * w) in
+// fragment order, and one sum of x^2 per token and block of 4 * NT columns,
+// ssq[m * (K / (4 NT)) + b]; the matmul reading u applies
+// 1 / sqrt(sum / K + eps) (RMSNorm::forward split around it).  The rows of one
+// token spread over K / (4 NT) workgroups instead of one.  grid (M, K / (4 NT)).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_resid_u(float *x, const float *w, int K, const float *part, int nks,
+                                                int64_t pstride, uint16_t *out16, int ld16, float *ssq) {
+    const int m = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int k = (b * NT + t) * 4;
+    float4 *rp = (float4 *)(x + (int64_t)m * K + k);
+    float4 v = *rp;
+    const float4 wv = *(const float4 *)(w + k);
+    if (nks > 1) {
+        float4 a[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            a[ks] = ks < nks ? *(const float4 *)(part + ks * pstride + (int64_t)m * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (ks >= nks) continue;
+            v.x += a[ks].x;
+            v.y += a[ks].y;
+            v.z += a[ks].z;
+            v.w += a[ks].w;
+        }
+        *rp = v;
+    }
+    // elements k .. k+3 sit in fragment slots f, f+2, f+1, f+3: one 8-byte store
+    const uint32_t lo = (uint32_t)f2h(v.x * wv.x) | ((uint32_t)f2h(v.z * wv.z) << 16);
+    const uint32_t hi = (uint32_t)f2h(v.y * wv.y) | ((uint32_t)f2h(v.w * wv.w) << 16);
+    *(uint2 *)(out16 + (int64_t)m * ld16 + frag_index(k)) = make_uint2(lo, hi);
+    float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    ss += __shfl_xor(ss, 8);
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW];
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    if (t == 0) {
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += red[i];  // fixed order
+        ssq[(int64_t)m * gridDim.y + b] = tot;
+    }
+}
+
 // Input of a matmul with the RMSNorm fused into it (M <= 16): u = fp16(x * w)
 // in fragment order and, per 16-element tile, the sum of x^2 (the matmul's
 // epilogue applies 1 / sqrt(sum / K + eps)).  grid M, block 256; K % 16 == 0.
@@ -272,6 +324,17 @@ void launch_norm_u(const float *x, const float *w, int M, int K, uint16_t *out16
                    hipStream_t st) {
     if (K % 16) throw BackendError("norm_u: K must be a multiple of 16");
     hipLaunchKernelGGL(k_norm_u, dim3(M), dim3(256), 0, st, x, w, K, out16, ld16, ssq);
+}
+int resid_u_parts(int K) { return K % 1024 == 0 ? K / 1024 : K % 512 == 0 ? K / 512 : K / 256; }
+void launch_resid_u(float *x, const float *w, int M, int K, const float *part, int nks, uint16_t *out16, int ld16,
+                    float *ssq, hipStream_t st) {
+    if (K % 256 || nks > 8) throw BackendError("resid_u: K must be a multiple of 256, at most 8 slices");
+    const int64_t ps = (int64_t)M * K;
+    const int nb = resid_u_parts(K);
+    if (nb > 64) throw BackendError("resid_u: too many column blocks");
+    if (K % 1024 == 0) hipLaunchKernelGGL(k_resid_u<256>, dim3(M, nb), dim3(256), 0, st, x, w, K, part, nks, ps, out16, ld16, ssq);
+    else if (K % 512 == 0) hipLaunchKernelGGL(k_resid_u<128>, dim3(M, nb), dim3(128), 0, st, x, w, K, part, nks, ps, out16, ld16, ssq);
+    else hipLaunchKernelGGL(k_resid_u<64>, dim3(M, nb), dim3(64), 0, st, x, w, K, part, nks, ps, out16, ld16, ssq);
 }
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st) {
     hipLaunchKernelGGL(k_to_frag16, dim3((K + 255) / 256, M), dim3(256), 0, st, x, K, out16, ld16);

@@ -19,6 +19,12 @@ struct RopeKvParams {
     const float *part;
     int nks;
     const float *bq, *bk, *bv;  // QKV biases (Qwen2) or null
+    // with K slices and norm_ssq set, the input was u = fp16(h * w_norm): the
+    // slices' sum is scaled by norm_inv_rms(norm_ssq + m * norm_parts, ...)
+    // over K columns before the bias
+    const float *norm_ssq;
+    int norm_parts, norm_K;
+    float norm_eps;
 };
 
 // Work split of one attention call, a function of the prefix length P and the

@@ -14,6 +14,12 @@ void launch_embed(int fmt, const uint8_t *table, int K, const int *ids, int M, f
 // residual matmul that produced x) are first added to x in slice order.
 void launch_rmsnorm(float *x, const float *w, int M, int K, float eps, uint16_t *out16, int ld16, float *out32,
                     hipStream_t st, const float *part = nullptr, int nks = 1);
+// 17..64 rows: x += part slices (nks > 1), u = fp16(x * w) in fragment order and
+// one sum of x^2 per token and column block (ssq [M][resid_u_parts(K)]) for a
+// matmul that applies the norm's 1 / rms itself
+int resid_u_parts(int K);
+void launch_resid_u(float *x, const float *w, int M, int K, const float *part, int nks, uint16_t *out16, int ld16,
+                    float *ssq, hipStream_t st);
 void launch_to_frag16(const float *x, int M, int K, uint16_t *out16, int ld16, hipStream_t st);
 // u = fp16(x * w) in fragment order + per-16-element sums of x^2 (ssq [M][K/16])
 // for a matmul with the RMSNorm fused into its epilogue

@@ -585,9 +585,17 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     const bool fused = M <= 16 && H % 256 == 0 && H / 16 <= 256 && (c.head_dim == 64 || c.head_dim == 128);
     const int np = H / 16;
     if (fused) launch_norm_u(h, (const float *)lw[0][K_ATTN_NORM].d, M, H, xp, xp_ld, ssq, st);
+    // 17..64 rows: each RMSNorm is split the same way around its matmul: the
+    // residual finaliser writes u = fp16(h * w) and sums of h^2 per column
+    // block from many workgroups per row, and the matmul (or, after K slices,
+    // the RoPE finaliser) scales by 1/rms
+    const bool spread = !fused && M > 16 && M <= 64;
+    const int sp_parts = resid_u_parts(H);
     for (int l = 0; l < c.n_layers; l++) {
         auto &L = lw[l];
-        if (!fused)
+        if (spread)
+            launch_resid_u(h, (const float *)L[K_ATTN_NORM].d, M, H, qg_part, pend, xp, xp_ld, ssq, st);
+        else if (!fused)
             launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         int nks_qkv;
         {
@@ -608,6 +616,11 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.M = M;
             p.mode = GM_STORE;
             p.allow_split = split_ok;
+            if (spread) {
+                p.norm_ssq = ssq;
+                p.norm_parts = sp_parts;
+                p.norm_eps = c.rms_eps;
+            }
             if (fused) {
                 p.norm_ssq = ssq;
                 p.norm_parts = np;
@@ -652,6 +665,12 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 r.bq = (const float *)L[K_BQ].d;
                 r.bk = (const float *)L[K_BK].d;
                 r.bv = (const float *)L[K_BV].d;
+            }
+            if (spread) {
+                r.norm_ssq = ssq;
+                r.norm_parts = sp_parts;
+                r.norm_K = H;
+                r.norm_eps = c.rms_eps;
             }
             if (!fused) launch_rope_kv(r, st);
             AttnParams a{};
@@ -706,7 +725,9 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             run_gemm(p, PC_WO, wbytes(L[K_ATTN_O]));
             pend = qgemm_slices(p);
         }
-        if (!fused)
+        if (spread)
+            launch_resid_u(h, (const float *)L[K_FFN_NORM].d, M, H, qg_part, pend, xp, xp_ld, ssq, st);
+        else if (!fused)
             launch_rmsnorm(h, (const float *)L[K_FFN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         {
             GemmParams p{};
@@ -721,9 +742,9 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
             p.mode = GM_SWIGLU;
             p.act = act;
             p.act_ld = act_ld;
-            if (fused) {
+            if (fused || spread) {
                 p.norm_ssq = ssq;
-                p.norm_parts = np;
+                p.norm_parts = fused ? np : sp_parts;
                 p.norm_eps = c.rms_eps;
             }
             if (L[K_FFN_GATE].fmt != L[K_FFN_UP].fmt) throw UnsupportedError("ffn_gate and ffn_up must share a format");
@@ -754,11 +775,18 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 SD_HIP_CHECK(hipMemcpyAsync(collect_buf + ci * H, h + (size_t)(M - 1) * H, H * 4,
                                             hipMemcpyDeviceToDevice, st));
     }
-    if (!fused)
+    // the lm_head over all rows reads u and scales; other requests normalise here
+    const bool spread_head = spread && logits_mode == 2;
+    if (spread_head) {
+        launch_resid_u(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, qg_part, pend, xp, xp_ld, ssq, st);
+        if (want_hidden)  // h is complete: the final-norm hidden rows only
+            launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, nullptr, 0, hidden_out, st);
+    } else if (!fused) {
         launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, xp, xp_ld,
                        want_hidden ? hidden_out : nullptr, st, qg_part, pend);
-    else if (want_hidden)  // the final-norm hidden rows only; the lm_head input is already in xp
+    } else if (want_hidden) {  // the final-norm hidden rows only; the lm_head input is already in xp
         launch_rmsnorm(h, (const float *)gw[K_OUTPUT_NORM].d, M, H, c.rms_eps, nullptr, 0, hidden_out, st);
+    }
     logits_rows_last = 0;
     if (logits_mode != 0) {
         const DevTensor &W = c.tied_output ? gw[K_TOK_EMBD] : gw[K_OUTPUT];
@@ -777,6 +805,10 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         if (fused) {
             p.norm_ssq = ssq + (logits_mode == 1 ? (size_t)(M - 1) * np : 0);
             p.norm_parts = np;
+            p.norm_eps = c.rms_eps;
+        } else if (spread_head) {
+            p.norm_ssq = ssq;
+            p.norm_parts = sp_parts;
             p.norm_eps = c.rms_eps;
         }
         if (xp_ld != H) throw UnsupportedError("lm_head needs hidden == q_dim activations stride");

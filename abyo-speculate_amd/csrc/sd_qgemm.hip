@@ -992,6 +992,22 @@ __global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
     for (int rt = 0; rt < RW; rt++) row[rt] = wrow(S[rt], p.K, rloc[rt]);
     const int nsb = p.K >> 8;
     const int sb0 = ks * nsb / nks, sb1 = (ks + 1) * nsb / nks;
+    // Input norm (norm_ssq set, M <= 64, norm_parts <= 64): thread t sums the
+    // partials j = t % 4, t % 4 + 4, ... of token t / 4, requested now and
+    // added after the main loop (norm_inv_rms's order)
+    const bool has_norm = p.norm_ssq != nullptr;
+    float nrm[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) nrm[i] = 0.f;
+    if (has_norm) {
+        const int m = min((int)threadIdx.x >> 2, p.M - 1), j0 = (int)threadIdx.x & 3;
+        const rsrc_t nr = make_rsrc(p.norm_ssq, (uint32_t)(p.M * p.norm_parts * 4));
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int j = j0 + 4 * i;
+            nrm[i] = __uint_as_float(bld4(nr, j < p.norm_parts ? (uint32_t)(m * p.norm_parts + j) * 4u : kNoLoad, 0u));
+        }
+    }
     floatx4 acc[RW][CT];
 #pragma unroll
     for (int rt = 0; rt < RW; rt++)
@@ -1003,6 +1019,18 @@ __global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
     case Q6_K: qgx_body<Q6_K, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
     case Q8_0: qgx_body<Q8_0, RW, CT>(p, row, live, sb0, sb1, acc, xlds); break;
     default: break;
+    }
+    // 1 / rms of every token
+    __shared__ float s_inv[64];
+    if (has_norm) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) t += nrm[i];
+        t += __shfl_xor(t, 1);
+        t += __shfl_xor(t, 2);
+        if ((threadIdx.x & 3) == 0 && (int)(threadIdx.x >> 2) < p.M)
+            s_inv[threadIdx.x >> 2] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
+        __syncthreads();
     }
     const int slot = rb * XG_WAVES + wave;  // argmax partial slot of this wave
     if (!live) {
@@ -1020,6 +1048,11 @@ __global__ __launch_bounds__(256) void k_qgx(GemmParams p, int nks) {
             floatx4 v[RW];
 #pragma unroll
             for (int rt = 0; rt < RW; rt++) v[rt] = acc[rt][ct];
+            if (has_norm) {
+                const float inv = s_inv[min(ct * 16 + r16, 63)];
+#pragma unroll
+                for (int rt = 0; rt < RW; rt++) v[rt] *= inv;
+            }
             EpiPre<RW> e;
             epi_prefetch<RW>(p, S, rloc, ct * 16 + r16, g, e);
             epilogue<RW>(p, S, rloc, v, e, ct * 16 + r16, g, slot);
@@ -1166,9 +1199,13 @@ int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
         for (int i = 1; i < p.nseg; i++)
             if (p.seg[i].tile0 != p.seg[i - 1].tile0 + p.seg[i - 1].rows / 16)
                 throw BackendError("qgemm: segments must be consecutive");
-    // the fused RMSNorm and RoPE epilogues exist in the M <= 16 kernel only
-    if ((p.norm_ssq || p.next_w || p.rope.q16) && p.M > 16) throw BackendError("qgemm: fused epilogues need M <= 16");
-    if (p.norm_ssq && p.norm_parts * 16 != p.K) throw BackendError("qgemm: norm partials must be one per 16 of K");
+    // fused RMSNorm and RoPE: both sides in the M <= 16 kernel's epilogues;
+    // above 16 rows (up to 64) only the input side, in k_qgx (its K slices
+    // are scaled by the kernel that adds them)
+    if ((p.next_w || p.rope.q16) && p.M > 16) throw BackendError("qgemm: fused output epilogues need M <= 16");
+    if (p.norm_ssq && p.M <= 16 && p.norm_parts * 16 != p.K) throw BackendError("qgemm: norm partials must be one per 16 of K");
+    if (p.norm_ssq && p.M > 16 && (p.M > 64 || p.norm_parts < 1 || p.norm_parts > 64))
+        throw BackendError("qgemm: input norm above 16 rows needs M <= 64 and at most 64 partials");
     if (p.next_w && (p.mode != GM_RESID || !p.next_u || !p.next_ssq)) throw BackendError("qgemm: next-norm outputs");
     if (p.rope.q16) {
         const RopeOut &R = p.rope;
