@@ -650,9 +650,10 @@ __device__ __forceinline__ void load_x(uintx4 (&b)[XL], rsrc_t xr, uint32_t xvo,
 // comes from lane t + 8 of the same 16-lane row (rows t >= 8 of the MFMA
 // tile hold other data; their products belong to no token and are dropped)
 // DPP row_shl:N: lane i of each 16-lane row takes lane i + N (i < 16 - N);
-// the upper N lanes keep their own value
+// the upper N lanes, whose token rows are padding wherever a shift is used,
+// read zero (bound_ctrl), so the move needs no copy of the old value
 template <int N> __device__ __forceinline__ uint32_t row_shl(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x100 + N, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x100 + N, 0xF, 0xF, true);
 }
 template <int N> __device__ __forceinline__ uintx4 row_shl4(const uintx4 &v) {
     return uintx4{row_shl<N>(v.x), row_shl<N>(v.y), row_shl<N>(v.z), row_shl<N>(v.w)};
