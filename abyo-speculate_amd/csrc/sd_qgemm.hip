@@ -76,22 +76,19 @@ struct WRow {
 // --------------------------------------------------------------------------
 template <int FMT> struct QFmt;
 
-// get_scale_min_k4 for sub-blocks 2g and 2g+1 without lane-divergent branches.
-// Scale bytes s[0..11] = hdr.y | hdr.z | hdr.w.  For j < 4: sc = s[j] & 63,
-// m = s[j+4] & 63; for j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,
-// m = (s[j+4] >> 4) | (s[j] >> 6) << 4.
+// The lane group's scales and mins from the header's regrouped scale bytes
+// (kq_hdr_pack): w = sc_2g | sc_2g+1 << 6 | m_2g << 12 | m_2g+1 << 18 is byte g
+// of header words 1, 2, 3 (permute selector 12 gives a zero byte).
+__device__ __forceinline__ uint32_t kquant_word(const uintx4 &hdr, int g) {
+    const uint32_t lo = __builtin_amdgcn_perm(hdr.z, hdr.y, 0x0c0c0000u | (uint32_t)(4 + g) << 8 | (uint32_t)g);
+    return __builtin_amdgcn_perm(hdr.w, lo, 0x0c000100u | (uint32_t)(4 + g) << 16);
+}
 __device__ __forceinline__ void kquant_ints(const uintx4 &hdr, int g, int (&sc)[2], int (&mn)[2]) {
-    const int sh = (g & 1) * 16;
-    const uint32_t A = hdr.y >> sh, B = hdr.z >> sh, C = hdr.w >> sh;  // bytes jj, jj+1 in bits 0..15
-    const bool hi = g >= 2;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t a = (A >> (8 * i)) & 0xffu, b = (B >> (8 * i)) & 0xffu, cc = (C >> (8 * i)) & 0xffu;
-        const uint32_t sc_lo = a & 63u, mn_lo = b & 63u;
-        const uint32_t sc_hi = (cc & 15u) | ((a >> 6) << 4), mn_hi = (cc >> 4) | ((b >> 6) << 4);
-        sc[i] = (int)(hi ? sc_hi : sc_lo);
-        mn[i] = (int)(hi ? mn_hi : mn_lo);
-    }
+    const uint32_t w = kquant_word(hdr, g);
+    sc[0] = (int)(w & 63u);
+    sc[1] = (int)((w >> 6) & 63u);
+    mn[0] = (int)((w >> 12) & 63u);
+    mn[1] = (int)(w >> 18);
 }
 
 // Loads address one tile block: the wave-uniform part (tile, superblock) goes
@@ -117,6 +114,8 @@ __device__ __forceinline__ uint32_t tb_off(const WRow &w, int sb, int tbb) {
 // second small product on the MFMA with exact integer m_j.  Weights are thus
 // used exactly instead of rounded to fp16, at two fewer instructions per code
 // pair.
+constexpr uint32_t kOff1024 = 0xE400E400u;  // (-1024, -1024) in fp16
+constexpr uint32_t kOff64 = 0xD400D400u;    // (-64, -64)
 struct KInt {
     uint32_t s0, c0, s1, c1;  // fp16 pairs: sc and -1024 sc (low nibbles), sc and -64 sc (high)
     uint32_t m;               // bf16 m of sub-blocks 2g and 2g + 1
@@ -126,10 +125,16 @@ __device__ __forceinline__ KInt kquant_int(const uintx4 &hdr, int g) {
     int sc[2], mn[2];
     kquant_ints(hdr, g, sc, mn);
     KInt k;
-    k.s0 = h2pair((float)sc[0]);
-    k.c0 = h2pair(-1024.f * (float)sc[0]);
-    k.s1 = h2pair((float)sc[1]);
-    k.c1 = h2pair(-64.f * (float)sc[1]);
+    // (1024 + sc) twice is 0x6400 | sc in both halves; minus 1024 it is sc
+    // exactly, and the offsets -1024 sc, -64 sc are exact fp16 products
+    const half2v s0 = __builtin_bit_cast(half2v, (uint32_t)sc[0] * 0x10001u + 0x64006400u) +
+                      __builtin_bit_cast(half2v, kOff1024);
+    const half2v s1 = __builtin_bit_cast(half2v, (uint32_t)sc[1] * 0x10001u + 0x64006400u) +
+                      __builtin_bit_cast(half2v, kOff1024);
+    k.s0 = __builtin_bit_cast(uint32_t, s0);
+    k.c0 = __builtin_bit_cast(uint32_t, s0 * __builtin_bit_cast(half2v, kOff1024));
+    k.s1 = __builtin_bit_cast(uint32_t, s1);
+    k.c1 = __builtin_bit_cast(uint32_t, s1 * __builtin_bit_cast(half2v, kOff64));
     // bf16 of a small integer: the top half of its f32
     k.m = (__float_as_uint((float)mn[0]) >> 16) | (__float_as_uint((float)mn[1]) & 0xffff0000u);
     k.d = h2f((uint16_t)(hdr.x & 0xffffu));
@@ -152,8 +157,6 @@ __device__ __forceinline__ KS16 kquant_s16(const uintx4 &hdr, int g) {
     k.m1 = h2pair(-(dmin * (float)mn[1]));
     return k;
 }
-constexpr uint32_t kOff1024 = 0xE400E400u;  // (-1024, -1024) in fp16
-constexpr uint32_t kOff64 = 0xD400D400u;    // (-64, -64)
 // codes (off + q) -> round_f16(q * s + nm), q exact
 __device__ __forceinline__ uint32_t qsm(uint32_t p, uint32_t off, uint32_t s, uint32_t nm) {
     const half2v q = __builtin_bit_cast(half2v, p) + __builtin_bit_cast(half2v, off);

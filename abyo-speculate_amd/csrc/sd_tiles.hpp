@@ -50,13 +50,57 @@ __host__ __device__ inline int get_bits(const uint8_t *p, int bit, int nbits) {
     return v;
 }
 
+// ---- K-quant header: scales and mins regrouped per lane group --------------
+// Bytes 0..3 of a row's 16-byte header are GGUF's (d, dmin).  Bytes 4..15 hold
+// the 8 six-bit scales sc_j and mins m_j regrouped: lane group g needs
+// sc_2g, sc_2g+1, m_2g, m_2g+1, the 24-bit word
+//   w_g = sc_2g | sc_2g+1 << 6 | m_2g << 12 | m_2g+1 << 18,
+// and byte k of w_g sits at byte g of header word 1 + k (byte 4 + 4k + g), so
+// a lane gathers it with two byte permutes.  The 96 bits are a permutation of
+// GGUF's 12 scale bytes (get_scale_min_k4's packing), so unpacking is exact.
+__host__ __device__ inline void kq_scale_min(const uint8_t *q, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+// q: GGUF scale bytes (12); h: the header's bytes 4..15
+__host__ __device__ inline void kq_hdr_pack(const uint8_t *q, uint8_t *h) {
+    int sc[8], mn[8];
+    for (int j = 0; j < 8; j++) kq_scale_min(q, j, sc[j], mn[j]);
+    for (int g = 0; g < 4; g++) {
+        const uint32_t w = (uint32_t)sc[2 * g] | (uint32_t)sc[2 * g + 1] << 6 | (uint32_t)mn[2 * g] << 12 |
+                           (uint32_t)mn[2 * g + 1] << 18;
+        for (int k = 0; k < 3; k++) h[4 * k + g] = (uint8_t)(w >> (8 * k));
+    }
+}
+__host__ __device__ inline void kq_hdr_unpack(const uint8_t *h, uint8_t *q) {
+    int sc[8], mn[8];
+    for (int g = 0; g < 4; g++) {
+        const uint32_t w = (uint32_t)h[g] | (uint32_t)h[4 + g] << 8 | (uint32_t)h[8 + g] << 16;
+        sc[2 * g] = (int)(w & 63);
+        sc[2 * g + 1] = (int)((w >> 6) & 63);
+        mn[2 * g] = (int)((w >> 12) & 63);
+        mn[2 * g + 1] = (int)((w >> 18) & 63);
+    }
+    for (int j = 0; j < 4; j++) {
+        q[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        q[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+        q[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+    }
+}
+
 // ---- one row's GGUF superblock <-> its share of a tile block -----------------
 // gg: the row's GGUF bytes of the superblock (fmt_sb_bytes); tb: tile block; r: row in tile.
 // pack writes only bytes owned by row r (its lanes r + 16g), so threads of the
 // 16 rows never touch the same byte.
 __host__ __device__ inline void pack_sb(int fmt, const uint8_t *gg, uint8_t *tb, int r) {
     if (fmt == Q4_K || fmt == Q5_K) {
-        for (int j = 0; j < 16; j++) tb[r * 16 + j] = gg[j];
+        for (int j = 0; j < 4; j++) tb[r * 16 + j] = gg[j];
+        kq_hdr_pack(gg + 4, tb + r * 16 + 4);
         const uint8_t *qs = gg + (fmt == Q4_K ? 16 : 48);
         const int qoff = fmt == Q4_K ? 256 : 768;
         for (int q = 0; q < 128; q++) {
@@ -112,7 +156,8 @@ __host__ __device__ inline void pack_sb(int fmt, const uint8_t *gg, uint8_t *tb,
 
 __host__ __device__ inline void unpack_sb(int fmt, const uint8_t *tb, int r, uint8_t *gg) {
     if (fmt == Q4_K || fmt == Q5_K) {
-        for (int j = 0; j < 16; j++) gg[j] = tb[r * 16 + j];
+        for (int j = 0; j < 4; j++) gg[j] = tb[r * 16 + j];
+        kq_hdr_unpack(tb + r * 16 + 4, gg + 4);
         uint8_t *qs = gg + (fmt == Q4_K ? 16 : 48);
         const int qoff = fmt == Q4_K ? 256 : 768;
         for (int q = 0; q < 128; q++) {
