@@ -571,15 +571,15 @@ __device__ __forceinline__ void int_drain(IntCarry<RT> &cy, floatx4 (&acc)[RT]) 
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     // X_2g, X_2g+1 of the lane's token as bf16 hi + lo: 16 significant bits
     // and the f32 range (a sum of 32 activations can exceed fp16's), times
-    // the integer mins, exact in bf16
+    // the integer mins, exact in bf16; hi and lo take slots 0, 1 and 2, 3 of
+    // one product (the mins repeated), so one MFMA sums all four
     const __bf16 h0 = (__bf16)cy.xs[0], h1 = (__bf16)cy.xs[1];
     const __bf16 l0 = (__bf16)(cy.xs[0] - (float)h0), l1 = (__bf16)(cy.xs[1] - (float)h1);
-    const bf16x8 xh = {h0, h1, 0, 0, 0, 0, 0, 0}, xl = {l0, l1, 0, 0, 0, 0, 0, 0};
+    const bf16x8 xa = {h0, h1, l0, l1, 0, 0, 0, 0};
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        const bf16x8 mb = __builtin_bit_cast(bf16x8, uintx4{cy.m[rt], 0u, 0u, 0u});
-        floatx4 pm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, mb, zero, 0, 0, 0);
-        pm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, mb, pm, 0, 0, 0);
+        const bf16x8 mb = __builtin_bit_cast(bf16x8, uintx4{cy.m[rt], cy.m[rt], 0u, 0u});
+        const floatx4 pm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, mb, zero, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i++)
             acc[rt][i] = __builtin_fmaf(-cy.dmin[rt], pm[i], __builtin_fmaf(cy.d[rt], cy.part[rt][i], acc[rt][i]));
