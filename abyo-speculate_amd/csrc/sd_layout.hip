@@ -6,7 +6,9 @@
 // lane group, lane = r + 16 g) are packed so that each of its loads reads a
 // contiguous range across the wave:
 //
-//   Q4_K (2304 B): hdr[r][16]                     (d, dmin, scales: 256 B)
+//   Q4_K (2304 B): hdr[r][16]                     (d, dmin, then the 6-bit scales
+//                                                 and mins regrouped per lane group:
+//                                                 kq_hdr_pack in sd_tiles.hpp; 256 B)
 //                  qs  part p = 0,1: [lane][16]   (qs bytes 32g + 16p .. +16)
 //   Q5_K (2816 B): hdr[r][16] | qhp[lane][8] | qs part 0,1 as Q4_K
 //                  qhp holds the lane's 64 fifth bits, placed where the matmul
