@@ -89,3 +89,27 @@ def test_repack_rejects_bad_shapes(S):
         S.repack_gguf(Q4_K, g, 8, 512)
     with pytest.raises(S.UnsupportedMethod):
         S.repack_gguf(F32, g, 16, 256)
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, Q5_K])
+def test_kquant_header_regrouped(S, fmt):
+    """A K-quant tile header keeps d, dmin (bytes 0..3) and holds, for lane
+    group g, the word w_g = sc_2g | sc_2g+1 << 6 | m_2g << 12 | m_2g+1 << 18
+    with byte k at header byte 4 + 4k + g; (sc_j, m_j) are the GGUF block's
+    get_scale_min_k4 values (the oracle's, pinned by its known answers)."""
+    import oracle as O
+    rows, K = 32, 512
+    nsb = K // 256
+    g = rand_blocks(fmt, rows, nsb, 100 + fmt)
+    t = S.repack_gguf(fmt, g, rows, K)
+    tbb = {Q4_K: 2304, Q5_K: 2816}[fmt]
+    for row in (0, 5, 16, 31):
+        for sb in range(nsb):
+            blk = g[(row * nsb + sb) * SB_BYTES[fmt]:][:SB_BYTES[fmt]]
+            hdr = t[((row >> 4) * nsb + sb) * tbb + (row & 15) * 16:][:16]
+            assert bytes(hdr[:4]) == bytes(blk[:4])
+            sm = [O.get_scale_min_k4(j, bytes(blk[4:16])) for j in range(8)]
+            for grp in range(4):
+                w = sum(int(hdr[4 + 4 * k + grp]) << (8 * k) for k in range(3))
+                want = (sm[2 * grp][0] | sm[2 * grp + 1][0] << 6 | sm[2 * grp][1] << 12 | sm[2 * grp + 1][1] << 18)
+                assert w == want, (row, sb, grp)
