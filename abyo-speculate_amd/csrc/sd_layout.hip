@@ -49,16 +49,6 @@ __global__ void k_relayout(int fmt, const uint8_t *src, uint8_t *dst, int64_t ro
 // ---- exact f32 dequantisation of one GGUF superblock (no FMA contraction) ------
 __device__ inline float ldh(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
 
-__device__ inline void gsm_k4(int j, const uint8_t *q, int &d, int &m) {
-    if (j < 4) {
-        d = q[j] & 63;
-        m = q[j + 4] & 63;
-    } else {
-        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
-
 // element e (0..255) of a GGUF superblock
 __device__ float deq_gguf(int fmt, const uint8_t *b, int e) {
     if (fmt == Q8_0) {
@@ -68,7 +58,7 @@ __device__ float deq_gguf(int fmt, const uint8_t *b, int e) {
     if (fmt == Q4_K || fmt == Q5_K) {
         const int part = e >> 5, j = e >> 6, hi = part & 1, l = e & 31;
         int s, m;
-        gsm_k4(part, b + 4, s, m);
+        kq_scale_min(b + 4, part, s, m);
         const float d1 = ldh(b) * (float)s, m1 = ldh(b + 2) * (float)m;
         int q;
         if (fmt == Q4_K) {
