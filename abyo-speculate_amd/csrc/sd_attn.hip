@@ -460,6 +460,48 @@ __device__ __forceinline__ void attn_emit(const AttnParams &p, int s, int head, 
 // dims [c HD/16, +HD/16).  The arithmetic, and its order, is k_attn_combine's:
 // out = sum_s w_s o_s / sum_s w_s in split order, w_s = l_s exp2(m_s - max m).
 constexpr int kFusedMaxSplits = 64;
+// The merge when every split's (m, l) and pieces fit in registers at once
+// (ns <= NSM): one memory round trip; the same arithmetic and order as the
+// general path of attn_merge_tile.
+template <int HD, int NSM>
+__device__ __forceinline__ void attn_merge_regs(const AttnParams &p, int head, int m, int c, int ns, int64_t stride,
+                                                int64_t pi0) {
+    constexpr int DPT = HD / 16;
+    const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
+    uint64_t mlv[NSM], ov[NSM][DPT / 4];
+#pragma unroll
+    for (int j = 0; j < NSM; j++) {
+        mlv[j] = j < ns ? ld_dev64(p.part_ml + 2 * (pi0 + j * stride)) : 0ull;
+#pragma unroll
+        for (int k = 0; k < DPT / 4; k++) ov[j][k] = j < ns ? ld_dev64(po + j * stride * HD + 4 * k) : 0ull;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NSM; j++)
+        if (j < ns) mx = fmaxf(mx, __uint_as_float((uint32_t)mlv[j]));
+    float W = 0.f, acc[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NSM; j++) {
+        if (j < ns) {
+            const float ms = __uint_as_float((uint32_t)mlv[j]);
+            const float w = ms == -INFINITY ? 0.f : __uint_as_float((uint32_t)(mlv[j] >> 32)) * exp2f(ms - mx);
+            W += w;
+#pragma unroll
+            for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
+        }
+    }
+    // dims 4k .. 4k + 3 of this thread sit in fragment slots f, f + 2, f + 1, f + 3
+#pragma unroll
+    for (int k = 0; k < DPT / 4; k++) {
+        const int64_t e = (int64_t)head * HD + c * DPT + 4 * k;
+        *(uintx2 *)(p.out16 + (int64_t)m * p.out_ld + frag_index(e)) =
+            uintx2{(uint32_t)f2h(acc[4 * k] / W) | ((uint32_t)f2h(acc[4 * k + 2] / W) << 16),
+                   (uint32_t)f2h(acc[4 * k + 1] / W) | ((uint32_t)f2h(acc[4 * k + 3] / W) << 16)};
+    }
+}
+
 template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnParams &p, int h, int qg) {
     constexpr int DPT = HD / 16;  // dims per thread, 4 or 8: one or two 8-byte loads per split
     __shared__ float cml[16][kFusedMaxSplits][2];
@@ -470,43 +512,10 @@ template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnPara
     const int head = h * p.n_rep + (live ? q % p.n_rep : 0), m = live ? q / p.n_rep : 0;
     const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
     const int64_t pi0 = (int64_t)head * p.M + m;
-    if (ns <= 8) {
-        // every split's (m, l) and pieces requested at once: one memory round
-        // trip; the same arithmetic and order as below
+    if (ns <= 16) {
         if (!live) return;
-        const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
-        uint64_t mlv[8], ov[8][DPT / 4];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            mlv[j] = j < ns ? ld_dev64(p.part_ml + 2 * (pi0 + j * stride)) : 0ull;
-#pragma unroll
-            for (int k = 0; k < DPT / 4; k++) ov[j][k] = j < ns ? ld_dev64(po + j * stride * HD + 4 * k) : 0ull;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j < ns) mx = fmaxf(mx, __uint_as_float((uint32_t)mlv[j]));
-        float W = 0.f, acc[DPT];
-#pragma unroll
-        for (int i = 0; i < DPT; i++) acc[i] = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (j < ns) {
-                const float ms = __uint_as_float((uint32_t)mlv[j]);
-                const float w = ms == -INFINITY ? 0.f : __uint_as_float((uint32_t)(mlv[j] >> 32)) * exp2f(ms - mx);
-                W += w;
-#pragma unroll
-                for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
-            }
-        }
-        // dims 4k .. 4k + 3 of this thread sit in fragment slots f, f + 2, f + 1, f + 3
-#pragma unroll
-        for (int k = 0; k < DPT / 4; k++) {
-            const int64_t e = (int64_t)head * HD + c * DPT + 4 * k;
-            *(uintx2 *)(p.out16 + (int64_t)m * p.out_ld + frag_index(e)) =
-                uintx2{(uint32_t)f2h(acc[4 * k] / W) | ((uint32_t)f2h(acc[4 * k + 2] / W) << 16),
-                       (uint32_t)f2h(acc[4 * k + 1] / W) | ((uint32_t)f2h(acc[4 * k + 3] / W) << 16)};
-        }
+        if (ns <= 8) attn_merge_regs<HD, 8>(p, head, m, c, ns, stride, pi0);
+        else attn_merge_regs<HD, 16>(p, head, m, c, ns, stride, pi0);
         return;
     }
     for (int s = c; s < ns; s += 16) {
