@@ -17,7 +17,7 @@
 //                  elements (s'=0, l) | (s'=1, l) << 4, s' = element half
 //                  hbp[lane][16]                  2-bit high parts (layout_q6_bit)
 //                  sc[r][16] | d[r][2]
-//   Q8_0 (4352 B): qs part p = 0..3: [lane][16]   (blocks 2g, 2g+1: 64 bytes)
+//   Q8_0 (4352 B): qs part p = 0..3: [lane][16]   (blocks 2g, 2g+1: 64 bytes, each q + 128)
 //                  d[r][8 x f16]
 //
 // Lane (r, g) covers elements 64g .. 64g+63 of the superblock: for the K-quants

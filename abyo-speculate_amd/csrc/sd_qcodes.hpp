@@ -132,8 +132,8 @@ struct LaneQ6K {
     }
 };
 
-// Q8_0: the lane's 64 bytes are blocks 2g (parts 0, 1) and 2g+1 (parts 2, 3);
-// codes 1024 + (q + 128)
+// Q8_0: the lane's 64 bytes are blocks 2g (parts 0, 1) and 2g+1 (parts 2, 3),
+// stored as q + 128 (the relayout flips each byte's top bit); codes 1024 + (q + 128)
 struct LaneQ80 {
     uintx4 a0, a1, b0, b1;
     uint32_t d;
@@ -141,7 +141,7 @@ struct LaneQ80 {
     __host__ __device__ static int off_part(int lane, int p) { return 1024 * p + lane * 16; }
     __host__ __device__ static int off_d(int lane) { return 4096 + (lane & 15) * 16 + 4 * (lane >> 4); }
     __host__ __device__ void codes(int g, int c, uint32_t p[4]) const {
-        const uint32_t qa = wsel(a0, a1, c) ^ 0x80808080u, qb = wsel(b0, b1, c) ^ 0x80808080u;
+        const uint32_t qa = wsel(a0, a1, c), qb = wsel(b0, b1, c);
         const uint32_t M = 0x64646464u;
         p[0] = perm(qa, M, 0x00060004u);  // {qa.b0, 0x64, qa.b2, 0x64}
         p[1] = perm(qa, M, 0x00070005u);  // {qa.b1, 0x64, qa.b3, 0x64}

@@ -148,7 +148,7 @@ __host__ __device__ inline void pack_sb(int fmt, const uint8_t *gg, uint8_t *tb,
             const int g = b >> 1, lane = r + 16 * g;
             for (int i = 0; i < 32; i++) {
                 const int o = 32 * (b & 1) + i;  // byte within the lane's 64
-                tb[(o >> 4) * 1024 + lane * 16 + (o & 15)] = blk[2 + i];
+                tb[(o >> 4) * 1024 + lane * 16 + (o & 15)] = (uint8_t)(blk[2 + i] ^ 0x80);  // q + 128
             }
         }
     }
@@ -203,7 +203,7 @@ __host__ __device__ inline void unpack_sb(int fmt, const uint8_t *tb, int r, uin
             const int g = b >> 1, lane = r + 16 * g;
             for (int i = 0; i < 32; i++) {
                 const int o = 32 * (b & 1) + i;
-                blk[2 + i] = tb[(o >> 4) * 1024 + lane * 16 + (o & 15)];
+                blk[2 + i] = (uint8_t)(tb[(o >> 4) * 1024 + lane * 16 + (o & 15)] ^ 0x80);
             }
         }
     }
