@@ -1128,8 +1128,10 @@ void Decoder::tree_logits(const uint32_t *tokens, const uint32_t *parents, size_
         SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.logits, n * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
     truncate(prefix);
-    forward_advance(&last, 1, false);  // GEMV-path root row (quantized_llama.rs:306-322)
-    if (out_logits)
+    forward_advance(&last, 1, false);  // restores the cache and the cached next-token row
+    // Llama replaces row 0 by the one-token pass's row (quantized_llama.rs:306-322); Qwen2 discards that
+    // row and keeps the tree pass's row 0 (quantized_qwen2.rs:227-234).
+    if (out_logits && m.cfg.arch == 0)
         SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
 }

@@ -536,17 +536,32 @@ class HipQuantDecoder:
         _check(_lib.sd_last_hidden_states_multi(self._h, _ptr(a), a.size, _ptr(fin), _ptr(mids)))
         return fin, [mids[i] for i in range(a.size)]
 
-    def apply_lm_head(self, hidden: np.ndarray) -> np.ndarray:
-        h = np.ascontiguousarray(np.atleast_2d(hidden), np.float32)
-        out = np.empty((h.shape[0], self.vocab), np.float32)
-        _check(_lib.sd_apply_lm_head(self._h, _ptr(h), h.shape[0], _ptr(out)))
-        return out
+    def apply_lm_head(self, hidden) -> np.ndarray:
+        """TreeDecoder::apply_lm_head (quantized_llama_local.rs:316-318): the
+        lm_head QMatMul over the last dim, [..., hidden] -> [..., vocab] f32,
+        leading dims kept. F16 / F64 input is promoted to f32 first, as the
+        quantised path does with a draft's F16 rows (eagle.rs:536-547)."""
+        h = np.asarray(hidden)
+        if h.ndim == 0 or h.shape[-1] != self.hidden:
+            raise BackendError(f"apply_lm_head: last dim of shape {h.shape} must be hidden ({self.hidden})")
+        lead = h.shape[:-1]
+        flat = np.ascontiguousarray(h.reshape(-1, self.hidden), np.float32)
+        out = np.empty((flat.shape[0], self.vocab), np.float32)
+        if flat.shape[0]:
+            _check(_lib.sd_apply_lm_head(self._h, _ptr(flat), flat.shape[0], _ptr(out)))
+        return out.reshape(lead + (self.vocab,))
 
-    def embed_tokens(self, ids: Sequence[int]) -> np.ndarray:
-        a = _u32(ids)
-        out = np.empty((a.size, self.hidden), np.float32)
-        _check(_lib.sd_embed_tokens(self._h, _ptr(a), a.size, _ptr(out)))
-        return out
+    def embed_tokens(self, ids) -> np.ndarray:
+        """TreeDecoder::embed_tokens (quantized_llama_local.rs:328-330): the
+        token table's rows, ids.shape ++ [hidden] f32 (a (1, 1) id tensor gives
+        the [1, 1, hidden] input of the EAGLE-3 midlayer, eagle3.rs:641-650)."""
+        a = np.asarray(ids)
+        shape = a.shape
+        flat = _u32(a.reshape(-1))
+        out = np.empty((flat.size, self.hidden), np.float32)
+        if flat.size:
+            _check(_lib.sd_embed_tokens(self._h, _ptr(flat), flat.size, _ptr(out)))
+        return out.reshape(shape + (self.hidden,))
 
     def num_hidden_layers(self) -> int:
         return int(_lib.sd_num_hidden_layers(self._h))

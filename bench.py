@@ -27,11 +27,13 @@ decoder's stream gives each dequant-matmul launch's duration, from which the
 roofline figure is computed (algorithmic bytes = weight blocks + activations
 in + out, per launch).
 
-The CPU baseline times the oracle's C dequant-matmul (f32 dequantisation,
-f64 accumulation, OpenMP over output rows) on a bounded sample of the same
-step -- one Q6_K-mix layer, one Q4_K layer and the lm_head at M=5, repeated
-for about 12 s -- and scales the mean to a whole verify step (16 layers of
-each kind + lm_head).
+The CPU baseline times the C restatement of the CPU algorithm candle runs for
+a quantised matmul (oracle/cpu_q8k.c: every activation row quantised to Q8_K,
+integer Q4_K x Q8_K / Q6_K x Q8_K block dot products scaled in f32, AVX2,
+OpenMP over output rows), composed into whole layers, on a bounded sample of
+the same step -- one Q6_K-mix layer, one Q4_K layer and the lm_head at M=5,
+repeated for about 12 s -- and scales the mean to a whole verify step (16
+layers of each kind + lm_head).
 
 roofline.traffic is read from profiles/k1_hbm_traffic_llama8b_q4km.json: the
 HBM bytes per launch that rocprofv3's FETCH_SIZE and WRITE_SIZE counters gave
@@ -339,9 +341,15 @@ def main():
         tg = gemm_rows(tprof, ("qkv", "wo", "gate_up", "down", "lm_head"))
         tb = sum(e[1] for e in tg)
         tt = sum(e[2] for e in tg) * 1e-3
-        log(f"tree verify: {t_tree * 1e6:.1f} us/step, K1 {tb / tt / 1e9:.0f} GB/s")
+        # the step's algorithmic bytes as for the M=5 leg: every K1 launch's weight blocks, activations
+        # and outputs, plus the K/V rows each layer's attention reads once
+        tstep_bytes = (tb + sum(e[1] for e in tprof if e[0] == "attn")) / args.steps
+        log(f"tree verify: {t_tree * 1e6:.1f} us/step ({tstep_bytes / t_tree / 1e9:.0f} GB/s over the step), "
+            f"K1 {tb / tt / 1e9:.0f} GB/s")
         result["tree60"] = {"us": round(t_tree * 1e6, 1), "nodes": int(len(toks)), "kv_positions": args.tree_prefix,
                             "tokens_per_s": round((plen / args.steps) / t_tree, 1),
+                            "step_hbm_gbps": round(tstep_bytes / t_tree / 1e9, 1),
+                            "step_algorithmic_bytes": int(tstep_bytes),
                             "k1_gbps": round(tb / tt / 1e9, 1),
                             "k1_frac": round(tb / tt / 1e9 / PEAK_HBM_GBPS, 4),
                             "k1_kernel": "k_qgx (K1 for M>16)",

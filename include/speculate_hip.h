@@ -148,8 +148,10 @@ size_t sd_eos_token_ids(const sd_model *m, uint32_t *out, size_t cap);
  * out_hidden [n][hidden] (final-norm hidden); cache left at prefix + n. */
 sd_status sd_tree_logits_keep_kv(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,
                                  float *out_logits, float *out_hidden);
-/* TreeDecoder::tree_logits (quantized_llama.rs:262-325): strict form, row 0 from an
- * M=1 pass of the root, cache restored. */
+/* TreeDecoder::tree_logits: the tree pass, then the cache restored by an M=1 pass of the
+ * root (which refreshes the cached next-token row). Llama handles (quantized_llama.rs:262-325)
+ * return that M=1 row as row 0; Qwen2 handles (quantized_qwen2.rs:184-237) keep the tree
+ * pass's row 0 and discard the M=1 row, as the reference does. */
 sd_status sd_tree_logits(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits);
 /* TreeDecoder::commit_tree_path (quantized_llama.rs:409-440): keep [0..P) ++ [P + accepted[j]]. */
 sd_status sd_commit_tree_path(sd_model *m, const uint32_t *tokens, const uint32_t *parents, size_t n,

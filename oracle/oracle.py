@@ -970,6 +970,13 @@ class OracleDecoder:
         return logits, hidden
 
     def tree_logits(self, tree: DraftTree) -> np.ndarray:
+        """Strict tree verify: tree pass, cache restored to P, then a one-token
+        pass of the root (which also refreshes last_logits).
+
+        Llama (quantized_llama.rs:262-325): row 0 is replaced by the restoring
+        pass's row. Qwen2 (quantized_qwen2.rs:184-237): the restoring pass's
+        row is discarded and row 0 stays the tree pass's row.
+        """
         if not self.history:
             raise SamplingError("tree_logits with empty history")
         last = self.history[-1]
@@ -978,7 +985,8 @@ class OracleDecoder:
         self.m.truncate_kv_cache_to(prefix)
         self.cache_len = prefix
         restore = self._forward_advance([last])
-        logits[0] = restore[-1]
+        if self.m.cfg.arch == "llama":
+            logits[0] = restore[-1]
         return logits
 
     def commit_tree_path(self, tree: DraftTree, accepted: Sequence[int]):

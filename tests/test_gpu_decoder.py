@@ -168,6 +168,30 @@ def test_strict_root_row(hip):
     argmax_agreement(strict, ostrict)
 
 
+def test_strict_tree_logits_qwen2_keeps_tree_row(hip):
+    """Qwen2QuantDecoder::tree_logits (quantized_qwen2.rs:184-237): the restoring
+    one-token pass runs (and refreshes next_logits) but its row is discarded, so
+    every row, row 0 included, is the tree pass's row -- bit for bit the
+    fast path's rows -- and within the contract of the oracle's Qwen2 rule."""
+    over = dict(arch="qwen2", n_kv_heads=2, mix="q5k_q80", n_layers=2, rms_eps=1e-6, rope_theta=1e6)
+    od, hd, prefix = make_pair(hip, prefix_len=70, **over)
+    chain = greedy_chain(od, 3)
+    tree = O.build_cartesian_tree(prefix[-1], _tree_with_chain(chain, 32000))
+    strict = hd.tree_logits(tree)
+    assert hd.cache_len() == len(prefix) and hd.history() == prefix
+    one = hd.next_logits()  # the restoring pass's row
+    fast, _ = hd.tree_logits_keep_kv(tree)
+    assert np.array_equal(strict.view(np.uint32), fast.view(np.uint32))
+    hd.rollback_to(len(prefix) - 1)
+    hd.observe([prefix[-1]])
+    assert np.array_equal(one.view(np.uint32), hd.next_logits().view(np.uint32))
+    ostrict = od.tree_logits(tree)
+    assert od.cache_len == len(prefix)
+    for i in range(len(tree)):
+        assert rel_err(strict[i], ostrict[i]) < TOL, i
+    argmax_agreement(strict, ostrict)
+
+
 def test_error_semantics_keep_state(hip):
     od, hd, prefix = make_pair(hip, prefix_len=16)
     fresh = hip.HipQuantDecoder(hd.cfg)
@@ -235,6 +259,61 @@ def test_apply_lm_head_leaves_verify_state(hip):
     for i in (0, 16, 36):
         assert np.array_equal(hd.apply_lm_head(h[i:i + 1])[0].view(np.uint32), out[i].view(np.uint32))
     assert hd.history() == prefix + drafts
+
+
+def test_tree_decoder_tensor_contract(hip):
+    """Ranks and dtypes of every Decoder / TreeDecoder output are the
+    reference's, replayed through the shape handling of its callers:
+    hidden rows are rank-1 [hidden] f32 (quantized_llama.rs:190,211,245-247,391);
+    run_eagle unsqueezes one to [1, 1, hidden], hands the draft's F16 output to
+    apply_lm_head and reads logits.i((0, seq - 1, ..)) (eagle.rs:515-547);
+    run_eagle3 lifts the three layer rows to [1, 1, hidden] and concatenates
+    them, and embed_tokens of a (1, 1) id tensor is the [1, 1, hidden] input of
+    the midlayer's dims3() (eagle3.rs:598-650); apply_lm_head keeps leading
+    dims (QMatMul over the last dim, quantized_llama_local.rs:316-318)."""
+    od, hd, prefix = make_pair(hip, prefix_len=40)
+    H, V = od.m.cfg.hidden, od.m.cfg.vocab
+    f32 = np.dtype(np.float32)
+    nl = hd.next_logits()
+    assert nl.shape == (V,) and nl.dtype == f32
+    rows = hd.batched_logits([5, 6])
+    assert rows.shape == (3, V) and rows.dtype == f32
+    hd.rollback_to(len(prefix))
+    # run_eagle: observe_returning_last_hidden -> [hidden] -> [1, 1, hidden]
+    th = hd.observe_returning_last_hidden([7])
+    assert th.shape == (H,) and th.dtype == f32
+    draft_hidden = th[None, None].astype(np.float16)  # a draft's F16 [1, seq, hidden] output
+    logits = hd.apply_lm_head(draft_hidden)
+    assert logits.shape == (1, 1, V) and logits.dtype == f32
+    last = logits[0, draft_hidden.shape[1] - 1]
+    assert last.shape == (V,)
+    assert np.array_equal(last.view(np.uint32), hd.apply_lm_head(draft_hidden[0, 0].astype(np.float32)).view(np.uint32))
+    # the tree's per-node hidden rows; the bonus node's row becomes the next target_hidden (eagle.rs:727)
+    tree = O.build_cartesian_tree(7, [[1, 2], [3]])
+    lg, hs = hd.tree_logits_keep_kv(tree)
+    assert lg.shape == (len(tree), V) and hs.shape == (len(tree), H) and hs.dtype == f32
+    assert hs[len(tree) - 1].shape == (H,) and hs[len(tree) - 1][None, None].shape == (1, 1, H)
+    hd.rollback_to(len(prefix) + 1)
+    strict = hd.tree_logits(tree)
+    assert strict.shape == (len(tree), V)
+    ls = hd.last_hidden_state()
+    assert ls.shape == (H,) and ls.dtype == f32
+    # run_eagle3: last_hidden_states_multi -> three [hidden] rows -> [1, 1, 3 hidden]
+    fin, mids = hd.last_hidden_states_multi([0, 1, 2])
+    assert fin.shape == (H,) and len(mids) == 3 and all(m.shape == (H,) and m.dtype == f32 for m in mids)
+    hidden_in = np.concatenate([m.astype(np.float16)[None, None] for m in mids], axis=-1)
+    assert hidden_in.shape == (1, 1, 3 * H)
+    emb = hd.embed_tokens(np.array([[prefix[-1]]], np.uint32))
+    assert emb.shape == (1, 1, H) and emb.dtype == f32
+    assert np.array_equal(emb[0, 0], od.m.embed([prefix[-1]])[0])
+    assert hd.embed_tokens([3, 4]).shape == (2, H) and hd.embed_tokens(np.zeros((2, 3), np.int64)).shape == (2, 3, H)
+    # leading dims kept, rows unchanged by the reshape
+    x = np.random.default_rng(9).standard_normal((2, 3, H)).astype(np.float32)
+    out = hd.apply_lm_head(x)
+    assert out.shape == (2, 3, V)
+    assert np.array_equal(out.reshape(6, V).view(np.uint32), hd.apply_lm_head(x.reshape(6, H)).view(np.uint32))
+    with pytest.raises(hip.BackendError):
+        hd.apply_lm_head(np.zeros((1, H + 1), np.float32))
 
 
 def test_greedy_tree_commit_with_eos(hip):

@@ -120,7 +120,7 @@ def test_round_matches_device_steps_and_oracle(hip, depth, top_k):
     x, tok, dev_logits, dev_out = h, prefix[-1], [], []
     for s in range(depth):
         out = d.forward(x, tok, P + s)
-        lg = hd.apply_lm_head(out)[0]
+        lg = hd.apply_lm_head(out)
         dev_logits.append(lg)
         dev_out.append(out)
         want = E3.top_k_indices(lg, ks[s])

@@ -18,10 +18,18 @@ the reference's own tests fix -- never by retyping the oracle's formula:
 * the layer structure (quantized_llama_local.rs:363-409): with wo and
   ffn_down zero, every layer is the identity on the residual stream, so the
   final hidden is RMSNorm(embedding) exactly.
+* the MLP roles (quantized_llama_local.rs:45-51): a one-feature known answer
+  in which silu(gate) * up and silu(up) * gate differ; the roles exchanged
+  (a planted mistake) fail it.
+* the Qwen2 QKV bias (quantized_qwen2_local.rs:69-109), added before RoPE:
+  with zero q/k weights the cached key and the attention weight at position 1
+  are the rotated bias's closed forms; the bias added after the rotation (a
+  planted mistake) fails it.
 * the decoder (quantized_llama.rs; tests/with_qwen2_05b.rs:95-184,
   tests/tree_logits_consistency.rs:74-122): batched rows equal sequential
   observe rows, a linear tree equals the batched pass, tree row 0 equals
-  next_logits, strict tree_logits restores the cache.
+  next_logits, strict tree_logits restores the cache; on Qwen2
+  (quantized_qwen2.rs:184-237) strict row 0 stays the tree pass's row.
 """
 import math
 
@@ -228,6 +236,123 @@ def test_zero_residual_branches_make_layers_identity(arch):
     np.testing.assert_allclose(hid, O.rms_norm(emb, om.w[(-1, O.K_OUTPUT_NORM)][0], cfg.rms_eps), rtol=1e-7)
 
 
+def _q8_0_exact(w):
+    """Q8_0 blocks (f16 d, 32 int8) whose weights are the integers of w exactly (d = 1)."""
+    w = np.asarray(w)
+    rows, K = w.shape
+    assert K % 32 == 0 and np.all(np.abs(w) <= 127) and np.all(w == np.round(w))
+    blk = np.zeros((rows, K // 32, 34), np.uint8)
+    blk[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[:, :, 2:] = w.reshape(rows, K // 32, 32).astype(np.int8).view(np.uint8)
+    return O.Q8_0, blk.reshape(-1)
+
+
+def _f32_tensor(v):
+    return O.F32, np.ascontiguousarray(v, np.float32).view(np.uint8)
+
+
+def _exact_model(cfg, emb, mats):
+    """One layer from integer Q8_0 weights: embedding `emb`, the matrices and
+    biases in `mats` (keyed by tensor kind), every other matrix and bias zero,
+    every norm weight 1."""
+    t = {}
+    keys = [(-1, O.K_TOK_EMBD), (-1, O.K_OUTPUT_NORM), (-1, O.K_OUTPUT)] + [(0, k) for k in cfg.layer_kinds()]
+    for (li, kind) in keys:
+        rows, K = cfg.shape(kind)
+        if kind in (O.K_OUTPUT_NORM, O.K_ATTN_NORM, O.K_FFN_NORM):
+            t[(li, kind)] = _f32_tensor(np.ones(K))
+        elif kind in (O.K_BQ, O.K_BK, O.K_BV):
+            t[(li, kind)] = _f32_tensor(mats.get(kind, np.zeros(K)))
+        elif kind == O.K_TOK_EMBD:
+            t[(li, kind)] = _q8_0_exact(emb)
+        else:
+            t[(li, kind)] = _q8_0_exact(mats.get(kind, np.zeros((rows, K))))
+    return O.OracleModel(cfg, t)
+
+
+def _kat_cfg(arch):
+    return oracle_cfg(arch=arch, n_layers=1, hidden=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn=256, vocab=64,
+                      ctx_len=16, mix="q8_0")
+
+
+def _swiglu_kat(swap_roles):
+    """quantized_llama_local.rs:45-51 (quantized_qwen2_local.rs:39-45): the MLP is
+    ffn_down(silu(ffn_gate(x)) * ffn_up(x)). Attention is off (wo = 0), the
+    embedding row is all ones, so the normalised input is r = 1/sqrt(1 + eps)
+    in every column; feature 0 has gate weight 2 and up weight -1 on column 0,
+    and ffn_down copies feature 0 into column 0 of the residual:
+    x[0] = 1 + silu(2r) * (-r), against 1 + silu(-r) * 2r with the roles
+    exchanged."""
+    cfg = _kat_cfg("llama")
+    H, F = cfg.hidden, cfg.ffn
+    gate, up, down = np.zeros((F, H)), np.zeros((F, H)), np.zeros((H, F))
+    gate[0, 0], up[0, 0], down[0, 0] = 2, -1, 1
+    if swap_roles:  # the planted mistake: the two matrices' roles exchanged
+        gate, up = up, gate
+    om = _exact_model(cfg, np.ones((cfg.vocab, H)), {O.K_FFN_GATE: gate, O.K_FFN_UP: up, O.K_FFN_DOWN: down})
+    _, (x1,) = om.forward([5], [0], O.causal_mask(0, 1), collect_layers=[0])
+    r = 1.0 / math.sqrt(1.0 + cfg.rms_eps)
+    g, u = 2.0 * r, -r
+    assert abs(float(x1[0, 0]) - (1.0 + g / (1.0 + math.exp(-g)) * u)) < 2e-6
+    assert np.all(x1[0, 1:] == 1.0)
+
+
+def test_swiglu_gate_and_up_roles():
+    _swiglu_kat(swap_roles=False)
+
+
+def test_swiglu_planted_role_swap_fails():
+    with pytest.raises(AssertionError):
+        _swiglu_kat(swap_roles=True)
+
+
+def _qwen2_bias_kat():
+    """quantized_qwen2_local.rs:69-109: q = rope(x Wq + bq), k = rope(x Wk + bk),
+    v = x Wv + bv -- the bias is added before RoPE. With Wq = Wk = 0 the
+    rotated biases are the whole of q and k: bq = bk = 5 e_0 per head, so at
+    position 1 (half rotation, theta_0 = 1) k1 = q1 = 5 (cos 1 e_0 + sin 1 e_32)
+    while k0 = 5 e_0. Token 1 (all +1) at position 0 and token 2 (all -1) at
+    position 1; Wv = Wo = I, so the residual after the layer is the embedding
+    plus the attention output: row 0 = 1 + v0, row 1 = -1 + w v1 + (1 - w) v0,
+    w = logistic((q1.k1 - q1.k0) / 8), v_t = fp16(xn_t + bv)."""
+    cfg = _kat_cfg("qwen2")
+    H, hd = cfg.hidden, cfg.head_dim
+    emb = np.zeros((cfg.vocab, H))
+    emb[1], emb[2] = 1, -1
+    bq = np.zeros(H)
+    bq[0::hd] = 5.0
+    bv = 0.25 * (np.arange(H) % 5) - 0.5
+    eye = np.eye(H)
+    om = _exact_model(cfg, emb, {O.K_ATTN_V: eye, O.K_ATTN_O: eye, O.K_BQ: bq, O.K_BK: bq, O.K_BV: bv})
+    _, (x1,) = om.forward([1, 2], [0, 1], O.causal_mask(0, 2), collect_layers=[0])
+    r = 1.0 / math.sqrt(1.0 + cfg.rms_eps)
+    f16 = lambda a: np.asarray(a, np.float16).astype(np.float64)
+    # the cached key at position 1: 5 (cos 1, sin 1) on the pair (0, 32) of every head
+    k1 = np.zeros(hd)
+    k1[0], k1[hd // 2] = 5.0 * math.cos(1.0), 5.0 * math.sin(1.0)
+    for h in range(cfg.n_kv_heads):
+        np.testing.assert_allclose(om.k_cache[0][h, 1], f16(k1), rtol=0, atol=1e-6)
+        np.testing.assert_allclose(om.k_cache[0][h, 0], f16(5.0 * np.eye(hd)[0]), rtol=0, atol=1e-6)
+    v0, v1 = f16(r + bv), f16(-r + bv)
+    s1, s0 = float(k1 @ f16(k1)), float(k1 @ f16(5.0 * np.eye(hd)[0]))
+    w = 1.0 / (1.0 + math.exp(-(s1 - s0) / math.sqrt(hd)))
+    assert 0.75 < w < 0.85  # 0.5 if the bias were added after the rotation
+    np.testing.assert_allclose(x1[0], 1.0 + v0, rtol=0, atol=2e-6)
+    np.testing.assert_allclose(x1[1], -1.0 + w * v1 + (1.0 - w) * v0, rtol=0, atol=2e-5)
+
+
+def test_qwen2_bias_before_rope():
+    _qwen2_bias_kat()
+
+
+def test_qwen2_planted_bias_after_rope_fails(monkeypatch):
+    """With Wq = Wk = 0, adding the bias after the rotation gives q = bq and
+    k = bk at every position, i.e. the forward with the rotation removed."""
+    monkeypatch.setattr(O, "rope_half", lambda x, c, s: x)
+    with pytest.raises(AssertionError):
+        _qwen2_bias_kat()
+
+
 def test_causal_mask_matches_causal_bias():
     """causal_bias (quantized_llama_local.rs:332-350): prefix columns visible,
     -inf strictly above the diagonal of the new block."""
@@ -301,6 +426,27 @@ def test_tree_root_row_and_strict_restore(small):
     assert a.cache_len == len(prefix) and a.history == prefix
     assert np.array_equal(strict[0], a.next_logits())
     np.testing.assert_allclose(strict[1:], rows[1:], rtol=1e-6, atol=1e-6 * np.abs(rows).max())
+
+
+def test_qwen2_strict_tree_logits_keeps_the_tree_row(small):
+    """Qwen2QuantDecoder::tree_logits (quantized_qwen2.rs:184-237) runs the same
+    restoring one-token pass as Llama's but discards its row: row 0 stays the
+    tree pass's row, while the restoring pass refreshes next_logits."""
+    import dataclasses
+    cfg = dataclasses.replace(small, arch="qwen2")
+    rng = np.random.default_rng(8)
+    prefix = [int(v) for v in rng.integers(0, cfg.vocab, 7)]
+    a = _dec(cfg)
+    a.observe(prefix)
+    tree = O.build_cartesian_tree(prefix[-1], [[1, 2], [3, 4]])
+    strict = a.tree_logits(tree)
+    assert a.cache_len == len(prefix) and a.history == prefix
+    one = a.next_logits()  # the restoring pass's row, cached
+    rows, _ = a.tree_logits_keep_kv(tree)
+    assert np.array_equal(strict, rows)
+    a.rollback_to(len(prefix) - 1)
+    a.observe([prefix[-1]])
+    assert np.array_equal(one, a.next_logits())
 
 
 def test_commit_tree_path_equals_observing_the_path(small):
