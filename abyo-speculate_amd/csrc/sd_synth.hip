@@ -12,6 +12,7 @@
 // behind every QMatMul (:47-49, 73-90, 135, 317).
 #include "sd_common.hpp"
 #include "sd_kernels.hpp"
+#include "sd_tiles.hpp"
 
 namespace sd {
 
@@ -194,15 +195,6 @@ __global__ void k_fill_kv(uint16_t *kv, int L, int n_kv, int64_t cap, int hd, in
 }
 
 // ---- exact f32 dequantisation: one thread per 32 outputs ----------------
-__device__ inline void gsm_k4(int j, const uint8_t *q, int &d, int &m) {
-    if (j < 4) {
-        d = q[j] & 63;
-        m = q[j + 4] & 63;
-    } else {
-        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
 __device__ inline float ldh(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
 
 __global__ void k_dequant(int fmt, const uint8_t *w, int64_t n_groups, float *y) {
@@ -223,7 +215,7 @@ __global__ void k_dequant(int fmt, const uint8_t *w, int64_t n_groups, float *y)
         const uint8_t *b = w + sb * bb;
         const float d = ldh(b), mn = ldh(b + 2);
         int s, m;
-        gsm_k4(part, b + 4, s, m);
+        kq_scale_min(b + 4, part, s, m);  // GGUF's 6-bit scale / min packing
         const float d1 = d * (float)s, m1 = mn * (float)m;
         const int j = part >> 1, hi = part & 1;
         if (fmt == Q4_K) {

@@ -307,3 +307,40 @@ def test_round_top_k_ties_across_slices(hip):
         assert ids[s] == [int(d2t[i]) for i in dids[s]]
     d.close()
     hd.close()
+
+
+@pytest.mark.parametrize("draft_vocab", [1025, 4097])
+def test_round_top_k_short_last_slice(hip, draft_vocab):
+    """A draft vocabulary of 1024 n + 1 leaves a last 1024-entry top-k slice
+    with one logit, fewer than k = 8 eligible entries: its unfilled candidate
+    places drop out of the merge, so the round's top-8 equals top_k_indices
+    (medusa.rs:477-487) of the device's own step logits and the log-probs are
+    l - logsumexp(l); that slice's single entry still takes part (planted as
+    the largest logit, it ranks first)."""
+    od, hd, prefix = _target(hip, prefix_len=20)
+    d, c = _draft(hip, draft_vocab=draft_vocab)
+    d2t = d.get_tensor(hip.D3_D2T)
+    layers, depth = [1, 2, 3], 3
+    fin, mids = hd.last_hidden_states_multi(layers)
+    h0 = np.concatenate(mids)
+    for planted in (False, True):
+        ids, lps, dids = d.round(hd, layers, depth, 8)
+        h, tok = h0, prefix[-1]
+        d.reset()
+        for s in range(depth):
+            out, lg = d.forward_hidden(h, hd.embed_tokens([tok])[0], len(prefix) + s)
+            want = E.top_k_indices(lg, 8)
+            assert dids[s] == want, (draft_vocab, planted, s, dids[s], want)
+            assert ids[s] == [int(d2t[i]) for i in want]
+            _check_log_probs(lps[s], lg, want, s)
+            if planted and s == 0:
+                assert want[0] == draft_vocab - 1, want
+            h, tok = out, ids[s][0]
+        if not planted:
+            # the last row := twice the first step's winning row: its logit doubles
+            lm = d.get_tensor(hip.D3_LM_HEAD).reshape(draft_vocab, c["hidden"]).copy()
+            w0 = dids[0][0]
+            lm[draft_vocab - 1] = (lm[w0].astype(np.float32) * 2).astype(np.float16)
+            d.set_tensor(hip.D3_LM_HEAD, lm)
+    d.close()
+    hd.close()

@@ -2,8 +2,9 @@
 through the C ABI, on device buffers the test allocates itself with the HIP
 runtime the library is linked against: bit-identical to sd_model_qmatmul on
 two calls in a row (the second with fewer rows, so the shared scratch holds a
-longer previous input), on both the M <= 16 and the M > 16 kernels, and a
-clear error for inputs beyond the scratch."""
+longer previous input), on both the M <= 16 and the M > 16 kernels, on the
+handle's stream and on a stream the caller creates, and a clear error for
+inputs beyond the scratch."""
 import ctypes
 
 import numpy as np
@@ -22,7 +23,11 @@ def _hip_runtime():
     rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
     rt.hipFree.argtypes = [ctypes.c_void_p]
     rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    for f in (rt.hipMalloc, rt.hipFree, rt.hipMemcpy, rt.hipDeviceSynchronize):
+    rt.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    rt.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    rt.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    for f in (rt.hipMalloc, rt.hipFree, rt.hipMemcpy, rt.hipDeviceSynchronize, rt.hipStreamCreate,
+              rt.hipStreamSynchronize, rt.hipStreamDestroy):
         f.restype = ctypes.c_int
     return rt
 
@@ -47,12 +52,12 @@ class DevBuf:
         self.rt.hipFree(self.p)
 
 
-def _noalloc(hip, dec, layer, kind, xbuf, rows, ybuf):
+def _noalloc(hip, dec, layer, kind, xbuf, rows, ybuf, stream=None):
     lib = hip.load_library()
     lib.sd_model_qmatmul_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                              ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
     lib.sd_model_qmatmul_noalloc.restype = ctypes.c_int32
-    return lib.sd_model_qmatmul_noalloc(dec._h, layer, kind, xbuf.p, rows, ybuf.p, None)
+    return lib.sd_model_qmatmul_noalloc(dec._h, layer, kind, xbuf.p, rows, ybuf.p, stream)
 
 
 @pytest.mark.parametrize("mix,kind,rows", [("q4_k", 9, (12, 5)), ("q4_k_m", 9, (64, 17)), ("q5k_q80", 3, (40, 3)),
@@ -77,6 +82,39 @@ def test_noalloc_matches_qmatmul(hip, mix, kind, rows):
                 ref = dec.qmatmul(layer, kind, x)
                 assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (mix, kind, M)
         finally:
+            xb.free()
+            yb.free()
+    finally:
+        dec.close()
+
+
+def test_noalloc_on_a_caller_stream(hip):
+    """The stream argument: the call is enqueued on the caller's own stream
+    (created here with hipStreamCreate), which the caller synchronises."""
+    ocfg = oracle_cfg(mix="q4_k_m", n_layers=2, vocab=2048)
+    dec = hip.HipQuantDecoder(hip_cfg(hip, ocfg))
+    try:
+        dec.synthesize(MIX_IDS["q4_k_m"], ocfg.seed, ocfg.weight_std)
+        dec.synchronize()
+        rt = _hip_runtime()
+        layer, kind = 1, 7
+        N, K = ocfg.shape(kind)
+        xb, yb = DevBuf(rt, 128 * K * 4), DevBuf(rt, 128 * N * 4)
+        stream = ctypes.c_void_p()
+        assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+        rng = np.random.default_rng(77)
+        try:
+            for M in (40, 9, 2):
+                x = rng.standard_normal((M, K)).astype(np.float32)
+                xb.put(x)
+                assert _noalloc(hip, dec, layer, kind, xb, M, yb, stream) == 0, hip.load_library().sd_last_error()
+                assert rt.hipStreamSynchronize(stream) == 0
+                got = yb.get((M, N))
+                ref = dec.qmatmul(layer, kind, x)
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), M
+        finally:
+            rt.hipStreamSynchronize(stream)
+            rt.hipStreamDestroy(stream)
             xb.free()
             yb.free()
     finally:
