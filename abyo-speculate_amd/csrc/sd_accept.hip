@@ -30,11 +30,13 @@
 // its precondition on the siblings holds; deterministic top-k siblings meet
 // neither.
 //
-// The rows' softmax statistics and distributions are computed across the
-// GPU; the walk, one workgroup, then reads the distributions.  Sums here are
-// parallel (fixed-order trees over slices, tiles and lanes), so they can
-// differ from the reference's sequential f32 sums in the last bits; a
-// decision can only differ when u lies within a few ulps of a threshold.
+// The rows' softmax statistics and distributions, and every V-wide pass the
+// walk can make (per node, the normaliser of each possible rejection and the
+// final draw), are computed across the GPU; the walk, one workgroup, then
+// takes the decisions from those sums and searches one tile for the draw.
+// Sums here are parallel (fixed-order trees over slices, tiles and lanes), so
+// they can differ from the reference's sequential f32 sums in the last bits;
+// a decision can only differ when u lies within a few ulps of a threshold.
 #include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels_accept.hpp"
@@ -192,45 +194,11 @@ __global__ __launch_bounds__(kRsT) void k_row_stats(const float *logits, int64_t
     }
 }
 
-// ---- the rows as distributions ----------------------------------------------
-// grid (rows, slices), block kRsT: prob[r][x] = softmax_with_temperature's
-// value (tokens.rs:15-55), 0 where the t2d map masks x; at T = 0 the one-hot
-// of the first max.
-__global__ __launch_bounds__(kRsT) void k_row_prob(const float *logits, int64_t ld, int V, float inv_t, int greedy,
-                                                  const int *t2d_inv, const float *row_m, const float *row_s,
-                                                  const int *row_am, float *prob) {
-    const int r = blockIdx.x, sl = blockIdx.y;
-    const float *row = logits + (int64_t)r * ld;
-    float *out = prob + (int64_t)r * V;
-    const float m = row_m[r], S = row_s[r];
-    const int am = row_am[r];
-    const int x1 = min(V, (sl + 1) * kSlice);
-    constexpr int kPer = kSlice / kRsT;
-    float lv[kPer];
-    bool live[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-        const int x = sl * kSlice + threadIdx.x + kRsT * i;
-        live[i] = x < x1 && !(t2d_inv && t2d_inv[x] < 0);
-        lv[i] = live[i] && !greedy ? row[x] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-        const int x = sl * kSlice + threadIdx.x + kRsT * i;
-        if (x >= x1) break;
-        float p;
-        if (!live[i]) p = 0.f;
-        else if (greedy) p = x == am ? 1.f : 0.f;
-        else p = expf((lv[i] - m) * inv_t) / S;
-        out[x] = p;
-    }
-}
-
 // ---- the walk ----------------------------------------------------------------
 constexpr int WT = 1024;       // threads of the walk kernel (16 waves)
 constexpr int kTile = 256;     // entries per tile: lane l of a wave holds x = 256 tile + l + 64 j, j < 4
 constexpr int kMaxTiles = 1024;  // vocabularies up to 262144
-constexpr int MAX_REJ = 16;
+constexpr int MAX_REJ = kAcceptMaxChildren;
 
 constexpr int kMaxNodes = 256;
 struct WalkShared {
@@ -243,14 +211,28 @@ struct WalkShared {
     float Z[MAX_REJ];  // normalisers of the successive adjusted distributions at the current node
     float R[MAX_REJ];  // without replacement: the mass of q left before rejection r (R[0] = 1)
     int rej[MAX_REJ];  // without replacement: the rejected tokens at the current node
+    // the current node's precomputed values: per k, the pass total (the
+    // normaliser of rejection k, or the final draw's sum at k = its children)
+    // and the test of child k (p, q and the raw draft probability q0)
+    float nz[MAX_REJ + 1], np[MAX_REJ], nq[MAX_REJ], nq0[MAX_REJ];
     int node, krej, used, plen, fin, status, go;
     float u;
+};
+
+// The rejection state at the current node: the normalisers Z of the adjusted
+// distributions so far and, without replacement, the rejected tokens and the
+// mass R of q left before each rejection (R[0] = 1).  Held by the walk
+// (WalkShared) and by the precomputation of a node's passes (RejState).
+struct RejState {
+    float Z[MAX_REJ], R[MAX_REJ];
+    int rej[MAX_REJ];
 };
 
 // the draft probability of x (q0 = q(x)) that rejection r at the current
 // node tests against: q itself for i.i.d. siblings; without replacement, 0 on
 // the tokens rejected before r and q(x) / R_r elsewhere (0 once no mass is left)
-__device__ __forceinline__ float walk_q(const AcceptParams &a, const WalkShared &W, float q0, int r, int x) {
+template <typename St>
+__device__ __forceinline__ float walk_q(const AcceptParams &a, const St &W, float q0, int r, int x) {
     if (!a.wor) return q0;
     for (int i = 0; i < r; i++)
         if (W.rej[i] == x) return 0.f;
@@ -259,15 +241,15 @@ __device__ __forceinline__ float walk_q(const AcceptParams &a, const WalkShared 
 
 // probability of x after `krej` rejections at a node whose distribution is p0
 // (its prob row's entry) and whose draft row holds q0 = q(x)
-__device__ __forceinline__ float walk_val(const AcceptParams &a, const WalkShared &W, int krej, float p0, float q0,
-                                          int x) {
+template <typename St>
+__device__ __forceinline__ float walk_val(const AcceptParams &a, const St &W, int krej, float p0, float q0, int x) {
     float p = p0;
     for (int r = 0; r < krej; r++) p = fmaxf(p - walk_q(a, W, q0, r, x), 0.f) / W.Z[r];
     return p;
 }
 // the normaliser term of the adjusted distribution after rejection krej
-__device__ __forceinline__ float walk_adj(const AcceptParams &a, const WalkShared &W, int krej, float p0, float q0,
-                                          int x) {
+template <typename St>
+__device__ __forceinline__ float walk_adj(const AcceptParams &a, const St &W, int krej, float p0, float q0, int x) {
     return fmaxf(walk_val(a, W, krej, p0, q0, x) - walk_q(a, W, q0, krej, x), 0.f);
 }
 __device__ __forceinline__ float walk_p(const AcceptParams &a, const WalkShared &W, int node, int krej, int x) {
@@ -292,92 +274,13 @@ __device__ __forceinline__ float wave_scan(float v) {
     return v;
 }
 
-// Sum over x < V of the walk's values at `node` in a fixed order: tiles of
-// 256 entries (wave w takes tiles w, w + 16, ...; a lane its 4 entries in
-// order, then the wave's lanes), then the tiles.  ZPASS: the adjusted
-// distribution's unnormalised terms (walk_adj), else the current
-// distribution (walk_val).  QM: how q(x) is read -- 0 not at all, 1 from a
-// target-vocabulary row, 2 through the t2d map.  Each wave requests kBatch
-// tiles' entries (clamped into the row, so that every load is issued
-// unconditionally) before it computes any of them.  Leaves the tile sums in
-// W.tsum for walk_search.
+// Tiles of 256 entries (lane l of a wave holds x = 256 tile + l + 64 j,
+// j < 4); kBatch tiles' entries are requested by a wave before it computes
+// any (clamped into the row, so that every load is issued unconditionally).
 constexpr int kBatch = 6;
-template <bool ZPASS, int QM>
-__device__ __forceinline__ void walk_tiles(WalkShared &W, const AcceptParams &a, int node, int krej) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int V = a.V, ntiles = (V + kTile - 1) / kTile;
-    const float *prow = a.prob + (int64_t)node * V;
-    const int qr = W.qrow[node];
-    const float *qrow = QM ? a.q + (int64_t)(qr < 0 ? 0 : qr) * a.q_ld : nullptr;
-    for (int tb = wave; tb < ntiles; tb += (WT / 64) * kBatch) {
-        float p0[kBatch][4], q0[kBatch][4];
-        int d[kBatch][4];
-#pragma unroll
-        for (int b = 0; b < kBatch; b++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int x = min((tb + (WT / 64) * b) * kTile + lane + 64 * j, V - 1);
-                p0[b][j] = prow[x];
-                if constexpr (QM == 1) q0[b][j] = qrow[x];
-                if constexpr (QM == 2) d[b][j] = a.q_map[x];
-            }
-        if constexpr (QM == 2) {
-#pragma unroll
-            for (int b = 0; b < kBatch; b++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float v = qrow[d[b][j] < 0 ? 0 : d[b][j]];
-                    q0[b][j] = d[b][j] < 0 ? 0.f : v;
-                }
-        }
-        if constexpr (QM == 0) {
-#pragma unroll
-            for (int b = 0; b < kBatch; b++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) q0[b][j] = 0.f;
-        }
-#pragma unroll
-        for (int b = 0; b < kBatch; b++) {
-            const int tl = tb + (WT / 64) * b;
-            if (tl >= ntiles) break;
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int x = tl * kTile + lane + 64 * j;
-                const float v = ZPASS ? walk_adj(a, W, krej, p0[b][j], q0[b][j], x)
-                                      : walk_val(a, W, krej, p0[b][j], q0[b][j], x);
-                s += x < V ? v : 0.f;
-            }
-            s = wave_sum(s);
-            if (lane == 0) W.tsum[tl] = s;
-        }
-    }
-}
-__device__ __forceinline__ float walk_pass(WalkShared &W, const AcceptParams &a, int node, int krej, bool zpass) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int ntiles = (a.V + kTile - 1) / kTile;
-    const int qm = !(zpass || krej > 0) ? 0 : a.q_map ? 2 : 1;
-    if (zpass) {
-        if (qm == 2) walk_tiles<true, 2>(W, a, node, krej);
-        else walk_tiles<true, 1>(W, a, node, krej);
-    } else {
-        if (qm == 0) walk_tiles<false, 0>(W, a, node, krej);
-        else if (qm == 2) walk_tiles<false, 2>(W, a, node, krej);
-        else walk_tiles<false, 1>(W, a, node, krej);
-    }
-    __syncthreads();
-    if (wave == 0) {
-        float s = 0.f;
-        for (int tl = lane; tl < ntiles; tl += 64) s += W.tsum[tl];
-        s = wave_sum(s);
-        if (lane == 0) W.total = s;
-    }
-    __syncthreads();
-    return W.total;
-}
 
-// sample_from_distribution's search (tokens.rs:99-120) after a walk_pass of
-// the same f, by wave 0: the first x with f(x) > 0 whose running sum exceeds
+// sample_from_distribution's search (tokens.rs:99-120) over the tile sums of
+// the same f in W.tsum, by wave 0: the first x with f(x) > 0 whose running sum exceeds
 // target, the running sum taken over the tiles' sums and then entry by entry
 // inside a tile; -1 when none does (the reference's drift case).
 template <typename F> __device__ __forceinline__ int walk_search(const WalkShared &W, int V, float target, F f) {
@@ -422,58 +325,176 @@ template <typename F> __device__ __forceinline__ int walk_search(const WalkShare
     return -1;
 }
 
-// ---- a chain's passes, precomputed across the GPU ---------------------------------
-// grid (n, tile groups), block kLtT: wave w of group y sums tiles
-// (y * 4 + w) * kBatch + b, b < kBatch, of row r exactly as walk_tiles does
-// (a lane's 4 entries in order, then wave_sum).  Phase 0: for a node with a
-// child, max(0, p - q) (the normaliser pass of its first rejection), for the
-// leaf p itself (its final draw); phase 1, after phase 0: max(0, p - q) / Z
-// with Z totalled as walk_pass totals (the draw after the rejection).
+// ---- every pass of the walk, precomputed across the GPU ---------------------------
+// Children are tested in BFS order, so the r-th rejection at node n is always
+// that of n's r-th child, and the distribution after k rejections (k <= c_n,
+// the number of children) depends on the node and k alone.  Launch k
+// (k = 0 .. max c_n, over the nodes with c_n >= k) computes, for a node with
+// k < c_n, the tile sums of the adjusted distribution's terms after k
+// rejections (walk_adj: the normaliser pass of rejection k), and for a node
+// with k == c_n the tile sums of its distribution after all c_n rejections
+// (walk_val: the final draw; for a leaf, p itself) -- the walk's only
+// possible passes, in its arithmetic and order: a lane's 4 entries of a tile
+// in order, then wave_sum.  The Z of rejections i < k are launch i's tile
+// sums totalled as walk_load_tiles totals them.  Workgroup 0 of a node also
+// evaluates the test of child k exactly as the walk would (walk_p, walk_q).
+// Launch 0 also writes the rows as distributions (softmax_with_temperature,
+// tokens.rs:15-55; 0 where the t2d map masks x; at T = 0 the one-hot of the
+// first max) from the logits and the row statistics.
+// grid (participating nodes, tile groups), block kLtT.
+// softmax_with_temperature's value at x of row r from its logit (the row's
+// statistics from k_row_stats): 0 where the t2d map masks x, the one-hot of
+// the first max at T = 0
+__device__ __forceinline__ float row_prob_at(const AcceptParams &a, int r, int x, float logit, bool masked) {
+    if (masked) return 0.f;
+    if (a.greedy) return x == a.row_am[r] ? 1.f : 0.f;
+    return expf((logit - a.row_m[r]) * a.inv_t) / a.row_s[r];
+}
+
 constexpr int kLtT = 256;
-template <int PHASE> __global__ __launch_bounds__(kLtT) void k_linear_tiles(AcceptParams a, float *lin) {
+template <bool FIRST>
+__global__ __launch_bounds__(kLtT) void k_tree_tiles(AcceptParams a, int k, const int *recs) {
     warm_kernargs<sizeof(AcceptParams)>();
-    const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the node's record (kTreeRec ints): node, children, draft row of its
+    // children, and child k's token, its draft-row index (-1: none) and
+    // whether the t2d map masks it
+    const int *rec = recs + (int64_t)blockIdx.x * kTreeRec;
+    const int r = rec[0], c = rec[1], qr = rec[2], tk = rec[3], dk = rec[4], mk_t = rec[5];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int V = a.V, n = a.n, ntiles = (V + kTile - 1) / kTile;
-    const bool leaf = r == n - 1;
-    if (PHASE == 1 && leaf) return;
-    const float *prow = a.prob + (int64_t)r * V;
-    const float *qrow = a.q + (int64_t)(leaf ? 0 : a.q_row_of[r]) * a.q_ld;
-    float Z = 1.f;
-    if (PHASE == 1) {
-        const float *zt = lin + (int64_t)r * ntiles;
-        float s = 0.f;
-        for (int tl = lane; tl < ntiles; tl += 64) s += zt[tl];
-        Z = wave_sum(s);
-    }
-    float *out = PHASE == 1 ? lin + (int64_t)(n + r) * ntiles : leaf ? lin + 2LL * n * ntiles : lin + (int64_t)r * ntiles;
+    const bool zpass = k < c;
+    const bool need_q = zpass || k > 0;
+    float *prow = a.prob + (int64_t)r * V;
+    const float *qrow = need_q ? a.q + (int64_t)(qr < 0 ? 0 : qr) * a.q_ld : nullptr;
     const int tb = ((int)blockIdx.y * (kLtT / 64) + wave) * kBatch;
-    float p0[kBatch][4], q0[kBatch][4];
+    // Every load that depends on nothing loaded here is issued first, in this
+    // order: the rejection state (tile sums of rejection i = wave, the
+    // rejected children's tokens and draft probabilities), the inputs of child
+    // k's test, the entries (p or the logits, the mask, the map or q); then the
+    // gathers through the map.
+    const bool zi = wave < k;
+    float zv[kMaxTiles / 64];
+    {
+        const float *zt = a.tiles + ((int64_t)(zi ? wave : 0) * n + r) * ntiles;
+#pragma unroll
+        for (int m2 = 0; m2 < kMaxTiles / 64; m2++) zv[m2] = zi ? zt[min(lane + 64 * m2, ntiles - 1)] : 0.f;
+    }
+    int s_tok = 0;
+    float s_q0 = 0.f;
+    if (wave == 0 && lane < k) {
+        s_tok = a.kids[r * kAcceptMaxChildren + lane];
+        s_q0 = a.test[((int64_t)lane * n + r) * 3 + 2];  // launch lane's test of child lane
+    }
+    const bool tester = blockIdx.y == 0 && threadIdx.x == 0 && zpass;
+    float t_raw = 0.f, t_q0 = 0.f;
+    if (tester) {
+        t_raw = FIRST ? a.logits[(int64_t)r * a.logits_ld + tk] : prow[tk];
+        t_q0 = dk < 0 ? 0.f : a.q[(int64_t)qr * a.q_ld + dk];
+    }
+    float p0[kBatch][4], q0[kBatch][4], mk[kBatch][4];
+    int d[kBatch][4];
 #pragma unroll
     for (int b = 0; b < kBatch; b++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int x = min((tb + b) * kTile + lane + 64 * j, V - 1);
-            p0[b][j] = prow[x];
-            q0[b][j] = leaf ? 0.f : qrow[x];
+            if constexpr (FIRST) {
+                p0[b][j] = a.logits[(int64_t)r * a.logits_ld + x];
+                mk[b][j] = a.t2d_inv ? (float)a.t2d_inv[x] : 0.f;  // < 0: masked
+            } else {
+                p0[b][j] = prow[x];
+            }
+            q0[b][j] = 0.f;
+            if (need_q) {
+                if (a.q_map) d[b][j] = a.q_map[x];
+                else q0[b][j] = qrow[x];
+            }
         }
+    if (need_q && a.q_map) {
+#pragma unroll
+        for (int b = 0; b < kBatch; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float v = qrow[d[b][j] < 0 ? 0 : d[b][j]];
+                q0[b][j] = d[b][j] < 0 ? 0.f : v;
+            }
+    }
+    // the rejection state, one shared copy: Z of rejection i = wave totalled
+    // as walk_load_tiles totals a pass (rejections past the wave count, which
+    // needs more than 4 children, in further rounds), R[0] = 1 and
+    // R[i + 1] = R[i] - q0(child i) as the walk updates it
+    __shared__ RejState S;
+    __shared__ float s_q[MAX_REJ];
+    auto zsum = [&](const float (&v)[kMaxTiles / 64]) {
+        float sz = 0.f;
+#pragma unroll
+        for (int m2 = 0; m2 < kMaxTiles / 64; m2++)
+            if (lane + 64 * m2 < ntiles) sz += v[m2];
+        return wave_sum(sz);
+    };
+    if (zi) {
+        const float z = zsum(zv);
+        if (lane == 0) S.Z[wave] = z;
+    }
+    for (int i = wave + kLtT / 64; i < k; i += kLtT / 64) {
+        const float *zt = a.tiles + ((int64_t)i * n + r) * ntiles;
+#pragma unroll
+        for (int m2 = 0; m2 < kMaxTiles / 64; m2++) zv[m2] = zt[min(lane + 64 * m2, ntiles - 1)];
+        const float z = zsum(zv);
+        if (lane == 0) S.Z[i] = z;
+    }
+    if (wave == 0 && lane < k) {
+        S.rej[lane] = s_tok;
+        s_q[lane] = s_q0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float Rr = 1.f;
+        for (int i = 0; i <= k && i < MAX_REJ; i++) {
+            S.R[i] = Rr;
+            if (i < k) Rr = Rr - s_q[i];
+        }
+    }
+    __syncthreads();
+    if constexpr (FIRST) {
+        // softmax_with_temperature's values, written for the later launches and the walk
+#pragma unroll
+        for (int b = 0; b < kBatch; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int x = (tb + b) * kTile + lane + 64 * j;
+                const float pv = row_prob_at(a, r, x, p0[b][j], mk[b][j] < 0.f);
+                p0[b][j] = pv;
+                if (x < V) prow[x] = pv;
+            }
+    }
+    // the test of child k: walk_p and walk_q at its token, as the walk evaluates them
+    if (tester) {
+        float *te = a.test + ((int64_t)k * n + r) * 3;
+        const float pt = FIRST ? row_prob_at(a, r, tk, t_raw, mk_t != 0) : t_raw;
+        te[0] = walk_val(a, S, k, pt, k > 0 ? t_q0 : 0.f, tk);
+        te[1] = walk_q(a, S, t_q0, k, tk);
+        te[2] = t_q0;
+    }
+    float *out = a.tiles + ((int64_t)k * n + r) * ntiles;
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
         const int tl = tb + b;
         if (tl >= ntiles) break;
-        float s = 0.f;
+        float sum = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int x = tl * kTile + lane + 64 * j;
-            const float v = leaf ? p0[b][j] : PHASE == 0 ? fmaxf(p0[b][j] - q0[b][j], 0.f)
-                                                         : fmaxf(p0[b][j] - q0[b][j], 0.f) / Z;
-            s += x < V ? v : 0.f;
+            const float v = zpass ? walk_adj(a, S, k, p0[b][j], q0[b][j], x) : walk_val(a, S, k, p0[b][j], q0[b][j], x);
+            sum += x < V ? v : 0.f;
         }
-        s = wave_sum(s);
-        if (lane == 0) out[tl] = s;
+        sum = wave_sum(sum);
+        if (lane == 0) out[tl] = sum;
     }
 }
 
-// wave 0: a row of precomputed tile sums into W.tsum and its total (walk_pass's order)
+// a row of precomputed tile sums into W.tsum and its total: wave 0 adds tiles
+// lane, lane + 64, ... per lane, then the lanes (wave_sum)
 __device__ __forceinline__ float walk_load_tiles(WalkShared &W, const float *src, int ntiles) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int tl = threadIdx.x; tl < ntiles; tl += WT) W.tsum[tl] = src[tl];
@@ -488,12 +509,16 @@ __device__ __forceinline__ float walk_load_tiles(WalkShared &W, const float *src
     return W.total;
 }
 
-// grid 1, block 1024
+// grid 1, block 1024.  The decisions read the precomputed values of the
+// current node (staged into LDS when the walk arrives there), so thread 0
+// tests a node's children without a memory round trip per child; the final
+// draw loads the chosen pass's tile sums and searches one tile.
 __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     warm_kernargs<sizeof(AcceptParams)>();
     __shared__ WalkShared W;
     const int t = threadIdx.x;
-    for (int i = t; i < a.n; i += WT) {
+    const int n = a.n;
+    for (int i = t; i < n; i += WT) {
         W.par[i] = a.parents[i];
         W.tok[i] = a.tokens[i];
         W.qrow[i] = a.q_row_of[i];
@@ -509,98 +534,98 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
         W.krej = 0;
         a.out_path[0] = 0;
     }
-    __syncthreads();
+    bool draw = false;
     while (true) {
-        // every thread has read the previous turn's W.go / W.node / W.krej
-        // before thread 0 rewrites them
+        // stage the current node's pass totals and child tests
+        __syncthreads();
+        {
+            const int node = W.node, c = a.nchild[node];
+            const int wave = t >> 6, lane = t & 63, ntl = (a.V + kTile - 1) / kTile;
+            if (t < c) {
+                const float *te = a.test + ((int64_t)t * n + node) * 3;
+                W.np[t] = te[0];
+                W.nq[t] = te[1];
+                W.nq0[t] = te[2];
+            }
+            // wave w totals pass k = w's tile sums (k <= c) as walk_load_tiles does
+            for (int kk = wave; kk <= c; kk += WT / 64) {
+                const float *zt = a.tiles + ((int64_t)kk * n + node) * ntl;
+                float zv[kMaxTiles / 64];
+#pragma unroll
+                for (int m2 = 0; m2 < kMaxTiles / 64; m2++) zv[m2] = zt[min(lane + 64 * m2, ntl - 1)];
+                float sz = 0.f;
+#pragma unroll
+                for (int m2 = 0; m2 < kMaxTiles / 64; m2++)
+                    if (lane + 64 * m2 < ntl) sz += zv[m2];
+                sz = wave_sum(sz);
+                if (lane == 0) W.nz[kk] = sz;
+            }
+        }
         __syncthreads();
         // ---- thread 0: test the children of the current node in BFS order ----
         if (t == 0) {
-            W.go = 0;  // 0: descend done / 1: sample at node / 2: normaliser pass needed / 3: stop
+            W.go = 3;  // 0: descend / 1: final draw at the node / 3: stop
             const int node = W.node;
             const float S = W.rs[node];
             if (!a.greedy && (!(S > 0.f) || !isfinite(S))) {
                 W.status = ACC_ERR_SOFTMAX;
-                W.go = 3;
-            } else if (a.max_commit > 0 && W.plen - 1 >= a.max_commit && W.krej == 0) {
-                W.go = 3;  // budget reached after an accepted draft: no final token
+            } else if (a.max_commit > 0 && W.plen - 1 >= a.max_commit) {
+                // budget reached after an accepted draft: no final token
             } else {
-                int c = node + 1;
-                int seen = 0;  // children already tested at this node (= krej)
-                int accepted = -1;
-                for (; c < a.n; c++) {
-                    if (W.par[c] != node) continue;
-                    if (seen++ < W.krej) continue;
+                W.R[0] = 1.f;
+                int accepted = -1, krej = 0;
+                for (int ch = node + 1; ch < n; ch++) {
+                    if (W.par[ch] != node) continue;
                     const float u = W.uni[W.used++];
-                    const int tok = W.tok[c];
-                    const float p = walk_p(a, W, node, W.krej, tok);
-                    if (W.krej == 0) W.R[0] = 1.f;
-                    const float q = walk_q(a, W, accept_q(a, W.qrow[node], tok), W.krej, tok);
+                    const float p = W.np[krej], q = W.nq[krej];
                     // modified_rejection_step (vanilla.rs:59-73)
-                    const bool acc = q <= 0.f || u <= fminf(p / q, 1.f);
-                    if (acc) {
-                        accepted = c;
+                    if (q <= 0.f || u <= fminf(p / q, 1.f)) {
+                        accepted = ch;
                         break;
                     }
-                    W.go = 2;  // rejected: the adjusted distribution's normaliser is needed
-                    if (W.krej < MAX_REJ) {
-                        W.rej[W.krej] = tok;
-                        if (W.krej + 1 < MAX_REJ) W.R[W.krej + 1] = W.R[W.krej] - accept_q(a, W.qrow[node], tok);
+                    // rejected: the adjusted distribution's normaliser (vanilla.rs:83-106)
+                    const float Z = W.nz[krej];
+                    if (!(Z > 0.f) || !isfinite(Z)) {
+                        W.status = ACC_ERR_ADJUSTED;
+                        break;
                     }
-                    break;
+                    W.Z[krej] = Z;
+                    W.rej[krej] = W.tok[ch];
+                    if (krej + 1 < MAX_REJ) W.R[krej + 1] = W.R[krej] - W.nq0[krej];
+                    krej++;
                 }
-                if (accepted >= 0) {
-                    a.out_path[W.plen++] = accepted;
-                    W.node = accepted;
-                    W.krej = 0;
-                    W.go = 0;
-                } else if (W.go != 2) {
-                    W.go = 1;  // no child left to test (or a leaf): final draw
-                    W.u = W.uni[W.used++];
+                W.krej = krej;
+                if (W.status == ACC_OK) {
+                    if (accepted >= 0) {
+                        a.out_path[W.plen++] = accepted;
+                        W.node = accepted;
+                        W.go = 0;
+                    } else {
+                        W.go = 1;  // no child left to test (or a leaf): final draw
+                        W.u = W.uni[W.used++];
+                    }
                 }
             }
         }
         __syncthreads();
         const int go = W.go;
         if (go == 0) continue;
-        if (go == 3) break;
+        draw = go == 1;
+        break;
+    }
+    if (draw) {
+        // sample_from_distribution (tokens.rs:99-120) over the distribution
+        // after all of the node's children were rejected (a leaf's p itself)
         const int node = W.node, krej = W.krej;
-        if (go == 2) {
-            // adjusted_distribution (vanilla.rs:83-106) of the current distribution
-            if (krej >= MAX_REJ) {
-                if (t == 0) W.status = ACC_ERR_ARG;
-                break;
-            }
-            const int ntl = (a.V + kTile - 1) / kTile;
-            const float Z = a.lin && krej == 0 ? walk_load_tiles(W, a.lin + (int64_t)node * ntl, ntl)
-                                               : walk_pass(W, a, node, krej, true);
-            if (t == 0) {
-                if (!(Z > 0.f) || !isfinite(Z)) {
-                    W.status = ACC_ERR_ADJUSTED;
-                } else {
-                    W.Z[krej] = Z;
-                    W.krej = krej + 1;
-                }
-            }
-            __syncthreads();
-            if (W.status != ACC_OK) break;
-            continue;
-        }
-        // go == 1: sample_from_distribution (tokens.rs:99-120) over the current distribution
-        auto f = [&](int x) { return walk_p(a, W, node, krej, x); };
         const int ntl = (a.V + kTile - 1) / kTile;
-        const float sum = a.lin && krej == 1 ? walk_load_tiles(W, a.lin + (int64_t)(a.n + node) * ntl, ntl)
-                          : a.lin && krej == 0 && node == a.n - 1 ? walk_load_tiles(W, a.lin + 2LL * a.n * ntl, ntl)
-                                                                  : walk_pass(W, a, node, krej, false);
+        const float sum = walk_load_tiles(W, a.tiles + ((int64_t)krej * n + node) * ntl, ntl);
         if (!(sum > 0.f) || !isfinite(sum)) {
             if (t == 0) W.status = ACC_ERR_SOFTMAX;
-            break;
-        }
-        if (t < 64) {
+        } else if (t < 64) {
+            auto f = [&](int x) { return walk_p(a, W, node, krej, x); };
             const int x = walk_search(W, a.V, W.u * sum, f);
             if (t == 0) W.fin = x < 0 ? a.V - 1 : x;
         }
-        break;
     }
     __syncthreads();
     if (t == 0) {
@@ -611,29 +636,36 @@ __global__ __launch_bounds__(WT) void k_accept_walk(AcceptParams a) {
     }
 }
 
-void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, int greedy, const int *t2d_inv,
-                      uint64_t *part, int *cnt, float *row_m, float *row_s, int *row_am, float *prob, hipStream_t st) {
+void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, const int *t2d_inv, uint64_t *part,
+                      int *cnt, float *row_m, float *row_s, int *row_am, hipStream_t st) {
     if (V < 1 || V > kRowStatsMaxSlices * kSlice) throw BackendError("acceptance: vocabulary too large");
     const dim3 grid(rows, (V + kSlice - 1) / kSlice);
     hipLaunchKernelGGL(k_row_stats, grid, dim3(kRsT), 0, st, logits, ld, V, inv_t, t2d_inv, part, cnt, row_m, row_s,
                        row_am);
-    hipLaunchKernelGGL(k_row_prob, grid, dim3(kRsT), 0, st, logits, ld, V, inv_t, greedy, t2d_inv, row_m, row_s,
-                       row_am, prob);
 }
 
-size_t linear_tiles_floats(int n, int V) { return (size_t)(2 * n + 1) * ((V + kTile - 1) / kTile); }
+size_t tree_tiles_floats(int n, int V, int kmax) {
+    // tile sums, child tests
+    return (size_t)(kmax + 1) * n * ((V + kTile - 1) / kTile) + (size_t)3 * (kmax + 1) * n;
+}
 
-void launch_linear_tiles(const AcceptParams &a, float *lin, hipStream_t st) {
+void launch_tree_tiles(const AcceptParams &a, int kmax, const int *const *recs, const int *counts, hipStream_t st) {
     if (a.V > kMaxTiles * kTile) throw BackendError("acceptance: vocabulary too large");
-    if (a.n < 1 || a.n > kMaxNodes || a.q_map) throw BackendError("acceptance: linear tiles need a chain in the target vocabulary");
+    if (a.n < 1 || a.n > kMaxNodes) throw BackendError("acceptance: too many tree nodes");
+    if (kmax < 0 || kmax > MAX_REJ) throw BackendError("acceptance: too many children for the precomputed passes");
+    if (!a.tiles || !a.test || !a.nchild || !a.kids || !a.logits || !a.prob) throw BackendError("acceptance: pass buffers");
+    if (counts[0] != a.n) throw BackendError("acceptance: the first pass covers every node");
     const int ntiles = (a.V + kTile - 1) / kTile, per = (kLtT / 64) * kBatch;
-    const dim3 grid(a.n, (ntiles + per - 1) / per);
-    hipLaunchKernelGGL(k_linear_tiles<0>, grid, dim3(kLtT), 0, st, a, lin);
-    hipLaunchKernelGGL(k_linear_tiles<1>, grid, dim3(kLtT), 0, st, a, lin);
+    const unsigned groups = (unsigned)((ntiles + per - 1) / per);
+    hipLaunchKernelGGL(k_tree_tiles<true>, dim3(a.n, groups), dim3(kLtT), 0, st, a, 0, recs[0]);
+    for (int k = 1; k <= kmax; k++)
+        if (counts[k] > 0)
+            hipLaunchKernelGGL(k_tree_tiles<false>, dim3(counts[k], groups), dim3(kLtT), 0, st, a, k, recs[k]);
 }
 
 void launch_accept_walk(const AcceptParams &a, hipStream_t st) {
     if (a.V > kMaxTiles * kTile) throw BackendError("acceptance: vocabulary too large");
+    if (!a.tiles || !a.test || !a.nchild) throw BackendError("acceptance: the walk reads the passes of launch_tree_tiles");
     if (a.n < 1 || a.n > kMaxNodes) throw BackendError("acceptance: too many tree nodes");
     hipLaunchKernelGGL(k_accept_walk, dim3(1), dim3(WT), 0, st, a);
 }

@@ -7,8 +7,19 @@ namespace sd {
 
 enum AcceptStatus : int { ACC_OK = 0, ACC_ERR_SOFTMAX = 1, ACC_ERR_ADJUSTED = 2, ACC_ERR_ARG = 3 };
 
+// children per tree node the walk supports (one normaliser per rejection)
+constexpr int kAcceptMaxChildren = 16;
+// ints of one node's record in a precomputed pass: node, children, draft row
+// of its children, child k's token, its draft-row index (-1: none), whether
+// the t2d map masks it, padding
+constexpr int kTreeRec = 8;
+// ints per tree node of a walk's inputs: parents, tokens, draft row, uniform,
+// children count, the children's tokens, and the node's records of each
+// precomputed pass
+constexpr int kAccTreeInts = 5 + kAcceptMaxChildren + kTreeRec * (kAcceptMaxChildren + 1);
+
 struct AcceptParams {
-    const float *prob;     // [n][V] the verify rows as distributions (k_row_prob), row i = tree node i
+    float *prob;           // [n][V] the verify rows as distributions (written by the first pass), row i = tree node i
     int V;                 // target vocabulary
     int n;                 // tree nodes (a chain for the linear walk)
     const int *parents;    // [n], parents[0] unused
@@ -28,12 +39,21 @@ struct AcceptParams {
                            // token's q is zeroed and q renormalised before the next sibling
     int *out_path;         // [n] accepted node indices, root first
     int *out_info;         // [4]: path length, final token (-1 none), uniforms used, status
-    // A chain (node i's child is i + 1) with draft rows in the target
-    // vocabulary may carry every pass its walk can make, precomputed across
-    // the GPU by launch_linear_tiles: per node the tile sums of max(0, p - q)
-    // and of max(0, p - q) / Z, and the leaf's tile sums of p.  Null: the walk
-    // makes its passes itself.
-    const float *lin;
+    // The logits rows of the verify pass (row i = tree node i), from which the
+    // first precomputed pass writes prob.
+    const float *logits;
+    int64_t logits_ld;
+    // The tree's shape for the precomputed passes: children per node, and
+    // per node its children's tokens in BFS order ([n][kAcceptMaxChildren]).
+    const int *nchild, *kids;
+    // Every pass the walk can make, precomputed across the GPU by
+    // launch_tree_tiles, per node and k = 0 .. c (its children): the tile
+    // sums (tiles + (k * n + node) * tile count) of the adjusted
+    // distribution's terms after k rejections (k < c: the normaliser of
+    // rejection k is their total) or of the distribution after all c
+    // rejections (k = c: the final draw); for k < c the test of child k,
+    // (p, q, q0) at test + (k * n + node) * 3.
+    float *tiles, *test;
 };
 
 // q(x) of draft row qr
@@ -45,16 +65,19 @@ __device__ __forceinline__ float accept_q(const AcceptParams &a, int qr, int x) 
     return a.q[(int64_t)qr * a.q_ld + x];
 }
 
-// Softmax statistics (max, sum, first-max argmax) of `rows` logits rows and
-// the rows as distributions into prob [rows][V].  part: kRowStatsMaxSlices x 2
-// words per row; cnt: one zeroed int per row (left zeroed).
+// Softmax statistics (max, sum, first-max argmax) of `rows` logits rows.
+// part: kRowStatsMaxSlices x 2 words per row; cnt: one zeroed int per row
+// (left zeroed).
 constexpr int kRowStatsMaxSlices = 32;
-void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, int greedy, const int *t2d_inv,
-                      uint64_t *part, int *cnt, float *row_m, float *row_s, int *row_am, float *prob, hipStream_t st);
+void launch_row_stats(const float *logits, int64_t ld, int V, int rows, float inv_t, const int *t2d_inv, uint64_t *part,
+                      int *cnt, float *row_m, float *row_s, int *row_am, hipStream_t st);
 void launch_accept_walk(const AcceptParams &a, hipStream_t st);
-// the precomputed passes of a chain's walk into lin [(2 n + 1) x tiles]
-// (AcceptParams::lin; a.prob, a.q, a.q_row_of, a.V, a.n as for the walk)
-size_t linear_tiles_floats(int n, int V);
-void launch_linear_tiles(const AcceptParams &a, float *lin, hipStream_t st);
+// The walk's passes, precomputed into a.tiles / a.test (kmax: the most
+// children of a node, <= kAcceptMaxChildren), and the rows as distributions
+// into a.prob; tree_tiles_floats is the floats of tiles and tests together.
+// recs[k] (device) holds the kTreeRec-int records of the counts[k] nodes
+// with at least k children (recs[0]: all of them).  Then launch_accept_walk.
+size_t tree_tiles_floats(int n, int V, int kmax);
+void launch_tree_tiles(const AcceptParams &a, int kmax, const int *const *recs, const int *counts, hipStream_t st);
 
 }  // namespace sd

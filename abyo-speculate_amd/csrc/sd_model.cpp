@@ -145,7 +145,9 @@ void Model::alloc_buffers() {
     acc_m = dalloc<float>(Mx);
     acc_s = dalloc<float>(Mx);
     acc_am = dalloc<int>(Mx);
-    acc_tree = dalloc<int>((size_t)4 * Mx);  // parents | tokens | q_row_of | uniforms of one walk
+    // parents | tokens | q_row_of | uniforms | children per node | the children's tokens [n][16] | the
+    // nodes of each precomputed pass (<= 17 n) of one walk
+    acc_tree = dalloc<int>((size_t)kAccTreeInts * Mx);
     acc_out = dalloc<int>((size_t)Mx + 4);
     acc_part = dalloc<uint64_t>((size_t)Mx * 2 * kRowStatsMaxSlices);
     acc_cnt = dalloc<int>(Mx);
@@ -155,7 +157,8 @@ void Model::alloc_buffers() {
     aux_ids = dalloc<int>(kAuxRows);
     h_stage_bytes = (size_t)Mx * (3 * sizeof(int) + 2 * sizeof(uint64_t)) + 256;
     SD_HIP_CHECK(hipHostMalloc((void **)&h_stage, h_stage_bytes, hipHostMallocDefault));
-    SD_HIP_CHECK(hipHostMalloc((void **)&acc_stage, ((size_t)5 * Mx + 8) * sizeof(int), hipHostMallocDefault));
+    SD_HIP_CHECK(hipHostMalloc((void **)&acc_stage, ((size_t)(kAccTreeInts + 1) * Mx + 8) * sizeof(int),
+                               hipHostMallocDefault));
     SD_HIP_CHECK(hipEventCreateWithFlags(&stage_ev, hipEventDisableTiming));
 }
 
@@ -1399,7 +1402,7 @@ static void check_device_rows(const Model &m, const float *q, size_t n) {
 void Decoder::accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, bool q_on_device,
                           size_t q_rows_n, size_t q_vocab, const int *q_row_of, const float *uniforms,
                           float temperature, int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin,
-                          size_t &used, bool linear) {
+                          size_t &used) {
     Model &m = *model;
     const ModelCfg &c = m.cfg;
     if (m.logits_rows_last < n) throw BackendError("acceptance: fewer logits rows than tree nodes");
@@ -1419,22 +1422,60 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
         SD_HIP_CHECK(hipMalloc((void **)&m.acc_prob, pn * sizeof(float) + 256));
         m.acc_prob_cap = pn;
     }
-    // parents | tokens | q_row_of | uniforms through the pinned acceptance
-    // stage in one copy (the previous walk synchronised before returning, so
-    // the stage is free), the draft rows in another unless on the device
+    // parents | tokens | q_row_of | uniforms | children per node | children's
+    // tokens in BFS order through the pinned acceptance stage in one copy (the
+    // previous walk synchronised before returning, so the stage is free), the
+    // draft rows in another unless on the device
     int *in = m.acc_stage;
     std::memcpy(in, parents, n * sizeof(int));
     std::memcpy(in + n, tokens, n * sizeof(int));
     std::memcpy(in + 2 * n, q_row_of, n * sizeof(int));
     std::memcpy(in + 3 * n, uniforms, n * sizeof(float));
-    SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, in, (size_t)4 * n * sizeof(int), hipMemcpyHostToDevice, m.st));
+    int *nchild = in + 4 * n, *kids = in + 5 * n;
+    std::fill(nchild, nchild + n, 0);
+    std::fill(kids, kids + (size_t)n * kAcceptMaxChildren, 0);
+    for (int i = 1; i < n; i++) {
+        const int p = parents[i];
+        if (nchild[p] >= kAcceptMaxChildren) throw UnsupportedError("rejection walk: at most 16 children per node");
+        kids[(size_t)p * kAcceptMaxChildren + nchild[p]++] = tokens[i];
+    }
+    const int kmax = *std::max_element(nchild, nchild + n);
+    // the nodes each precomputed pass k covers (those with at least k
+    // children) as records: node, children, draft row, child k's token, its
+    // index into the draft row (through the t2d map for draft-vocabulary
+    // rows; -1: none) and whether the t2d mask removes it from the target row
+    const bool qmap = q_vocab != (size_t)c.vocab;
+    int *lists = kids + (size_t)n * kAcceptMaxChildren;
+    int counts[kAcceptMaxChildren + 1];
+    const int *dlists[kAcceptMaxChildren + 1];
+    size_t off = 0;
+    for (int k = 0; k <= kmax; k++) {
+        counts[k] = 0;
+        dlists[k] = m.acc_tree + (lists - in) + off;
+        for (int i = 0; i < n; i++) {
+            if (nchild[i] < k) continue;
+            int *rc = lists + off + (size_t)kTreeRec * counts[k]++;
+            const int tk = k < nchild[i] ? kids[(size_t)i * kAcceptMaxChildren + k] : 0;
+            const int dk = k < nchild[i] ? (qmap ? t2d_host[tk] : tk) : -1;
+            rc[0] = i;
+            rc[1] = nchild[i];
+            rc[2] = q_row_of[i];
+            rc[3] = tk;
+            rc[4] = dk;
+            rc[5] = use_t2d && t2d_host[tk] < 0 ? 1 : 0;
+            rc[6] = rc[7] = 0;
+        }
+        off += (size_t)kTreeRec * counts[k];
+    }
+    SD_HIP_CHECK(hipMemcpyAsync(m.acc_tree, in, ((size_t)(lists - in) + off) * sizeof(int), hipMemcpyHostToDevice,
+                                m.st));
     if (qn && !q_on_device)
         SD_HIP_CHECK(hipMemcpyAsync(m.acc_q, q_rows, qn * sizeof(float), hipMemcpyHostToDevice, m.st));
     const bool greedy = temperature == 0.f;
     const float inv_t = greedy ? 1.f : 1.0f / temperature;
     const int *mask = use_t2d ? m.t2d_inv : nullptr;
-    launch_row_stats(m.logits, c.vocab, c.vocab, n, inv_t, greedy ? 1 : 0, mask, m.acc_part, m.acc_cnt, m.acc_m,
-                     m.acc_s, m.acc_am, m.acc_prob, m.st);
+    launch_row_stats(m.logits, c.vocab, c.vocab, n, inv_t, mask, m.acc_part, m.acc_cnt, m.acc_m, m.acc_s, m.acc_am,
+                     m.st);
     AcceptParams a{};
     a.prob = m.acc_prob;
     a.V = c.vocab;
@@ -1456,21 +1497,26 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     a.wor = wor;
     a.out_path = m.acc_out + 4;
     a.out_info = m.acc_out;
-    if (linear && !a.q_map && !wor) {
-        // a chain: every pass the walk can make, computed across the GPU first
-        const size_t ln = linear_tiles_floats(n, c.vocab);
-        if (ln > m.acc_lin_cap) {
-            if (m.acc_lin) SD_HIP_CHECK(hipFree(m.acc_lin));
-            m.acc_lin = nullptr;
-            m.acc_lin_cap = 0;
-            SD_HIP_CHECK(hipMalloc((void **)&m.acc_lin, ln * sizeof(float) + 256));
-            m.acc_lin_cap = ln;
-        }
-        launch_linear_tiles(a, m.acc_lin, m.st);
-        a.lin = m.acc_lin;
+    // every pass the walk can make (per node, one per possible rejection and
+    // the final draw), computed across the GPU first; the walk reads them
+    a.nchild = m.acc_tree + 4 * n;
+    a.kids = m.acc_tree + 5 * n;
+    const int ntl = (c.vocab + 255) / 256;
+    const size_t ln = tree_tiles_floats(n, c.vocab, kmax);
+    if (ln > m.acc_lin_cap) {
+        if (m.acc_lin) SD_HIP_CHECK(hipFree(m.acc_lin));
+        m.acc_lin = nullptr;
+        m.acc_lin_cap = 0;
+        SD_HIP_CHECK(hipMalloc((void **)&m.acc_lin, ln * sizeof(float) + 256));
+        m.acc_lin_cap = ln;
     }
+    a.tiles = m.acc_lin;
+    a.test = a.tiles + (size_t)(kmax + 1) * n * ntl;
+    a.logits = m.logits;
+    a.logits_ld = c.vocab;
+    launch_tree_tiles(a, kmax, dlists, counts, m.st);
     launch_accept_walk(a, m.st);
-    int *out = m.acc_stage + 4 * c.max_batch;
+    int *out = m.acc_stage + (size_t)kAccTreeInts * c.max_batch;
     SD_HIP_CHECK(hipMemcpyAsync(out, m.acc_out, ((size_t)n + 4) * sizeof(int), hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
     const int status = out[3];
@@ -1517,7 +1563,7 @@ void Decoder::verify_rejection_linear(const uint32_t *drafts, size_t k, const fl
     int fin;
     size_t used;
     accept_walk(parents.data(), tokens.data(), n, q_rows, q_on_device, k, m.cfg.vocab, qrow.data(), uniforms,
-                temperature, 0, 0, max_commit, path, fin, used, true);
+                temperature, 0, 0, max_commit, path, fin, used);
     size_t nc = 0;
     for (size_t i = 1; i < path.size(); i++) commits[nc++] = (uint32_t)tokens[path[i]];
     if (fin >= 0) commits[nc++] = (uint32_t)fin;
@@ -1545,7 +1591,8 @@ void Decoder::verify_rejection_tree(const uint32_t *tokens, const uint32_t *pare
     std::vector<int> nchild(n, 0);
     for (size_t i = 1; i < n; i++) {
         has_child[t.parents[i]] = true;
-        if (++nchild[t.parents[i]] > 16) throw UnsupportedError("rejection walk: at most 16 children per node");
+        if (++nchild[t.parents[i]] > kAcceptMaxChildren)
+            throw UnsupportedError("rejection walk: at most 16 children per node");
     }
     for (size_t i = 0; i < n; i++) {
         if (has_child[i] && (q_row_of[i] < 0 || (size_t)q_row_of[i] >= q_rows_n))

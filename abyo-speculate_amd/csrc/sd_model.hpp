@@ -160,7 +160,7 @@ class Model {
     size_t acc_q_cap = 0;  // floats
     uint64_t *acc_part = nullptr;  // row statistics' per-slice partials
     int *acc_cnt = nullptr;        // their per-row arrival counts (zero between launches)
-    float *acc_lin = nullptr;      // a chain walk's precomputed passes (launch_linear_tiles)
+    float *acc_lin = nullptr;      // the walk's precomputed passes (launch_tree_tiles)
     size_t acc_lin_cap = 0;        // floats
     float *acc_prob = nullptr;     // the verify rows as distributions
     size_t acc_prob_cap = 0;       // floats
@@ -181,7 +181,7 @@ class Model {
     int *aux_ids = nullptr;
     // pinned staging for small H2D transfers
     int *h_stage = nullptr;
-    int *acc_stage = nullptr;  // pinned: a walk's inputs [4 max_batch] and outputs [max_batch + 4]
+    int *acc_stage = nullptr;  // pinned: a walk's inputs [kAccTreeInts max_batch] and outputs [max_batch + 4]
     size_t h_stage_bytes = 0;
     hipEvent_t stage_ev = nullptr;  // recorded after the last copy out of h_stage
     void stage_wait();               // host waits until h_stage may be rewritten
@@ -261,8 +261,7 @@ class Decoder {
     // the acceptance walk over logits rows [0, n) of the last pass
     void accept_walk(const int *parents, const int *tokens, int n, const float *q_rows, bool q_on_device,
                      size_t q_rows_n, size_t q_vocab, const int *q_row_of, const float *uniforms, float temperature,
-                     int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used,
-                     bool linear = false);
+                     int use_t2d, int wor, size_t max_commit, std::vector<int> &path, int &fin, size_t &used);
     void truncate(size_t len);
     void tree_forward(const uint32_t *tokens, const uint32_t *parents, size_t n, bool want_hidden, int &prefix);
 };
