@@ -243,26 +243,41 @@ __device__ __forceinline__ float xsum4(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Query fragment of lane (r16 = query row, g): 8 dims of dc-chunk, scaled by
-// scale * log2(e) so that scores come out in base-2 softmax units.
-template <int HD, int QT>
-__device__ __forceinline__ void load_query(AttnState<HD, QT> &S, int t, const AttnParams &p, int h, int q, int g,
-                                           float sl2) {
-    constexpr int NDC = HD / 32;
+// A query tile's raw operands for lane (r16 = query row, g): 8 dims of each
+// 32-dim chunk and the row's tree-mask words.  Lanes past the last query read
+// the last query's row, so every load is in bounds and unconditional and the
+// compiler issues them back to back before the first wait; query_init zeroes
+// those lanes' fragments.
+template <int HD> struct QueryRaw {
+    uintx4 q[HD / 32];
+    uint64_t mk0, mk1;
+    bool live;
+};
+template <int HD>
+__device__ __forceinline__ void query_fetch(QueryRaw<HD> &r, const AttnParams &p, int h, int q, int g) {
     const int nq = p.M * p.n_rep;
-    const bool live = q < nq;
-    const int m = live ? q / p.n_rep : 0, r = live ? q % p.n_rep : 0;
-    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + r) * p.M + m) * HD;
+    r.live = q < nq;
+    const int qc = r.live ? q : nq - 1;
+    const int m = qc / p.n_rep, rep = qc % p.n_rep;
+    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + rep) * p.M + m) * HD;
 #pragma unroll
-    for (int dc = 0; dc < NDC; dc++) {
-        half8 v = half8{};
-        if (live) v = __builtin_bit_cast(half8, *(const uintx4 *)(qr + dc * 32 + g * 8));
+    for (int dc = 0; dc < HD / 32; dc++) r.q[dc] = *(const uintx4 *)(qr + dc * 32 + g * 8);
+    r.mk0 = p.mask[(int64_t)m * p.mask_words];
+    r.mk1 = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
+}
+// the query scaled by scale * log2(e) (scores in base-2 softmax units) and an
+// empty softmax state
+template <int HD, int QT>
+__device__ __forceinline__ void query_init(AttnState<HD, QT> &S, int t, const QueryRaw<HD> &r, float sl2) {
+#pragma unroll
+    for (int dc = 0; dc < HD / 32; dc++) {
+        half8 v = r.live ? __builtin_bit_cast(half8, r.q[dc]) : half8{};
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (_Float16)((float)v[i] * sl2);
         S.qf[t][dc] = v;
     }
-    S.mk0[t] = p.mask[(int64_t)m * p.mask_words];
-    S.mk1[t] = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
+    S.mk0[t] = r.mk0;
+    S.mk1[t] = r.mk1;
 #pragma unroll
     for (int dt = 0; dt < HD / 16; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     S.m[t] = -INFINITY;
@@ -573,8 +588,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
     src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
 
-    // two register buffers: the next 32 keys load while the current ones compute
-    // (K at the start of a step, V once the step's scores are done)
+    // the queries first (just written by the Q/K/V launch), then the first
+    // 32 keys; two register buffers: the next 32 keys load while the current
+    // ones compute (K at the start of a step, V once the step's scores are done)
+    QueryRaw<HD> qr[QT];
+#pragma unroll
+    for (int t = 0; t < QT; t++) query_fetch<HD>(qr[t], p, h, (qg * QT + t) * 16 + r16, g);
     KvStep<HD> b0, b1;
     int kk = k0;
     kv_load_k<HD>(b0, src, kk < k1 ? kk : -1);
@@ -583,7 +602,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     AttnState<HD, QT> S;
     const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
 #pragma unroll
-    for (int t = 0; t < QT; t++) load_query<HD, QT>(S, t, p, h, (qg * QT + t) * 16 + r16, g, sl2);
+    for (int t = 0; t < QT; t++) query_init<HD, QT>(S, t, qr[t], sl2);
 
     while (kk < k1) {
         kv_load_k<HD>(b1, src, kk + 32 < k1 ? kk + 32 : -1);
@@ -760,42 +779,6 @@ __device__ __forceinline__ void tile_step(AttnState<HD, QT> &S, const uintx4 *st
 }
 
 template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTStages * 8 * HD * 16; }
-
-// A query tile's raw operands, requested before the first key blocks so that
-// waiting for them does not wait for the blocks (loads complete in order).
-template <int HD> struct QueryRaw {
-    uintx4 q[HD / 32];
-    uint64_t mk0, mk1;
-};
-template <int HD>
-__device__ __forceinline__ void query_fetch(QueryRaw<HD> &r, const AttnParams &p, int h, int q, int g) {
-    const int nq = p.M * p.n_rep;
-    const bool live = q < nq;
-    const int m = live ? q / p.n_rep : 0, rep = live ? q % p.n_rep : 0;
-    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + rep) * p.M + m) * HD;
-#pragma unroll
-    for (int dc = 0; dc < HD / 32; dc++) r.q[dc] = live ? *(const uintx4 *)(qr + dc * 32 + g * 8) : uintx4{0u, 0u, 0u, 0u};
-    r.mk0 = p.mask[(int64_t)m * p.mask_words];
-    r.mk1 = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
-}
-// the query scaled by scale * log2(e) (scores in base-2 softmax units) and an
-// empty softmax state; load_query's arithmetic
-template <int HD, int QT>
-__device__ __forceinline__ void query_init(AttnState<HD, QT> &S, int t, const QueryRaw<HD> &r, float sl2) {
-#pragma unroll
-    for (int dc = 0; dc < HD / 32; dc++) {
-        half8 v = __builtin_bit_cast(half8, r.q[dc]);
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (_Float16)((float)v[i] * sl2);
-        S.qf[t][dc] = v;
-    }
-    S.mk0[t] = r.mk0;
-    S.mk1[t] = r.mk1;
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    S.m[t] = -INFINITY;
-    S.l[t] = 0.f;
-}
 
 template <int HD>
 __global__ __launch_bounds__(kTThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {

@@ -40,14 +40,29 @@ __device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t vo, uint32_t so) {
 // kernel that reads a large parameter struct field by field, with branches
 // between the reads, waits one memory round trip (~0.5 us) per cache line it
 // first touches.  Touching every 64-byte line of the first BYTES bytes at once
-// fills them in a single round trip; later reads of any field then hit.
+// fills them in a single round trip; later reads of any field then hit.  The
+// eight loads (the last line repeated for blocks under 512 bytes) sit in one
+// asm statement with their wait, so the compiler cannot split them into
+// batches with a wait between each.
 template <int BYTES> __device__ __forceinline__ void warm_kernargs() {
-    typedef const uint32_t __attribute__((address_space(4))) cu32;
-    const cu32 *ka = (const cu32 *)__builtin_amdgcn_kernarg_segment_ptr();
-    uint32_t acc = 0;
-#pragma unroll
-    for (int i = 0; i < (BYTES + 63) / 64; i++) acc ^= ka[16 * i];
-    asm volatile("" ::"s"(acc));  // waits for every line once, here
+    constexpr int L = (BYTES + 63) / 64 - 1;  // last line
+    static_assert(L >= 0 && L < 8, "argument blocks of at most 512 bytes");
+    const auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t v0, v1, v2, v3, v4, v5, v6, v7;
+    asm volatile(
+        "s_load_dword %0, %8, %9\n\t"
+        "s_load_dword %1, %8, %10\n\t"
+        "s_load_dword %2, %8, %11\n\t"
+        "s_load_dword %3, %8, %12\n\t"
+        "s_load_dword %4, %8, %13\n\t"
+        "s_load_dword %5, %8, %14\n\t"
+        "s_load_dword %6, %8, %15\n\t"
+        "s_load_dword %7, %8, %16\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(v0), "=&s"(v1), "=&s"(v2), "=&s"(v3), "=&s"(v4), "=&s"(v5), "=&s"(v6), "=&s"(v7)
+        : "s"(ka), "i"(0), "i"((L < 1 ? L : 1) * 64), "i"((L < 2 ? L : 2) * 64), "i"((L < 3 ? L : 3) * 64),
+          "i"((L < 4 ? L : 4) * 64), "i"((L < 5 ? L : 5) * 64), "i"((L < 6 ? L : 6) * 64), "i"(L * 64)
+        : "memory");
 }
 
 }  // namespace sd
