@@ -19,7 +19,9 @@ from typing import List, Optional, Sequence, Tuple
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libspeculate_hip.so")
+# SPECULATE_HIP_LIB selects another build of the same library (the CPU tests
+# load the AddressSanitizer build of the host code through it)
+LIB_PATH = os.environ.get("SPECULATE_HIP_LIB") or os.path.join(HERE, "libspeculate_hip.so")
 
 # sd_status
 SD_OK, SD_ERR_SAMPLING, SD_ERR_ROLLBACK, SD_ERR_BACKEND, SD_ERR_ARG, SD_ERR_UNSUPPORTED = range(6)
