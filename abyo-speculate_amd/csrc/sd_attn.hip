@@ -704,34 +704,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // ---- many queries (tree verify): query tiles across waves, keys shared in LDS ----
-// Grid (kv head, key split, query block).  The 8 waves of a workgroup own
-// kTQW query tiles each, the 8 * kTQW * 16 queries of one query block of a KV
-// head (all of them up to 256 query rows), and walk the split's keys
+// Grid (kv head, key split, query block).  The kTWaves waves of a workgroup
+// own kTQW query tiles each, the kTWaves * kTQW * 16 queries of one query block
+// of a KV head (all of them up to 256 query rows), and walk the split's keys
 // together: each 32-key block of K and V (contiguous in the blocked cache
-// layout) is copied once into LDS by the workgroup's 512 threads and read
-// there by all 8 waves, so the cache leaves L2 once per query block.  Copies
-// run kTStages blocks ahead through registers (as many LDS stages, one barrier
-// per block).  Splits are a few blocks long, so the grid covers the chip; the
-// combine kernel merges them.
-constexpr int kTWaves = 8;
+// layout) is copied once into LDS by the workgroup's threads and read there by
+// all its waves, so the cache leaves L2 once per query block.  Copies run
+// kTStages blocks ahead through registers (as many LDS stages, one barrier per
+// block).  Splits are a few blocks long, so the grid covers the chip; the
+// combine kernel merges them.  Sixteen waves of one tile each (four per SIMD)
+// hide the softmax's and the MFMAs' latencies better than eight of two.
+constexpr int kTWaves = 16;
 constexpr int kTThreads = 64 * kTWaves;
-constexpr int kTQW = 2;
+constexpr int kTQW = 1;
 constexpr int kTStages = 3;
 constexpr int kTMaxSplits = 32;
 
-// a thread's 16-byte pieces of one 32-key block: pieces i * 512 + tid, the
-// block's K (4 * HD pieces) first, then its V
+// a thread's 16-byte pieces of one 32-key block: pieces i * kTThreads + tid,
+// the block's K (4 * HD pieces) first, then its V; which stream a piece comes
+// from is the same for a whole wave (4 * HD is a multiple of 64)
+template <int HD> constexpr int tile_pieces() { return (8 * HD + kTThreads - 1) / kTThreads; }
 template <int HD> struct TileCopy {
-    uintx4 r[HD / 64];
+    uintx4 r[tile_pieces<HD>()];
 };
 template <int HD>
 __device__ __forceinline__ void tile_fetch(TileCopy<HD> &c, const KvSrc &src, int kk, int tid) {  // kk < 0: none
     const uint32_t so = kv_so(kk, HD);
+    const int wave_piece = __builtin_amdgcn_readfirstlane(tid & ~63);
 #pragma unroll
-    for (int i = 0; i < HD / 64; i++) {
-        const int piece = i * kTThreads + tid;
-        c.r[i] = piece < 4 * HD ? bld16(src.k, (uint32_t)piece * 16u, so)
-                                : bld16(src.v, (uint32_t)(piece - 4 * HD) * 16u, so);
+    for (int i = 0; i < tile_pieces<HD>(); i++) {
+        const int piece = i * kTThreads + tid, wp = i * kTThreads + wave_piece;  // wp: wave-uniform
+        const bool is_k = wp < 4 * HD;
+        const rsrc_t r = is_k ? src.k : src.v;
+        const uint32_t vo = wp >= 8 * HD ? kNoKv : (uint32_t)(is_k ? piece : piece - 4 * HD) * 16u;
+        c.r[i] = bld16(r, vo, so);
     }
 }
 // In LDS each 1 KiB chunk (the 64 16-byte pieces one MFMA operand load reads,
@@ -745,7 +751,8 @@ __device__ __forceinline__ int lds_swz(int piece) {
 template <int HD>
 __device__ __forceinline__ void tile_store(uintx4 *stage, const TileCopy<HD> &c, int tid) {
 #pragma unroll
-    for (int i = 0; i < HD / 64; i++) stage[lds_swz(i * kTThreads + tid)] = c.r[i];
+    for (int i = 0; i < tile_pieces<HD>(); i++)
+        if (i * kTThreads + tid < 8 * HD) stage[lds_swz(i * kTThreads + tid)] = c.r[i];
 }
 
 // One 32-key block from LDS for the wave's query tiles (dead tiles skipped)
@@ -781,7 +788,7 @@ __device__ __forceinline__ void tile_step(AttnState<HD, QT> &S, const uintx4 *st
 template <int HD> constexpr size_t attn_t_lds() { return (size_t)kTStages * 8 * HD * 16; }
 
 template <int HD>
-__global__ __launch_bounds__(kTThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_t(AttnParams p) {
+__global__ __launch_bounds__(kTThreads) void k_attn_t(AttnParams p) {
     warm_kernargs<sizeof(AttnParams)>();
     constexpr int QT = kTQW, SW = 8 * HD;  // SW: 16-byte pieces of one stage
     extern __shared__ uintx4 lds[];
@@ -989,7 +996,7 @@ void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.hd != 128 && p.hd != 64) throw BackendError("attention: head_dim must be 64 or 128");
     const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
     if (p.M > 16) {
-        // query blocks of 8 waves x kTQW tiles sharing each key block through LDS
+        // query blocks of kTWaves waves x kTQW tiles sharing each key block through LDS
         const dim3 grid(p.n_kv, p.nsplit, (nqt + kTWaves * kTQW - 1) / (kTWaves * kTQW));
         allow_attn_t_lds();
         if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(kTThreads), attn_t_lds<128>(), st, p);
