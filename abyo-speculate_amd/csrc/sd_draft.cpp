@@ -137,9 +137,12 @@ Draft3::Draft3(const Draft3Cfg &c) : cfg(c) {
     tok = dmalloc<int32_t>(1);
     tk_part = dmalloc<uint64_t>((size_t)64 * (1 + kDraftMaxTopk));
     tk_cnt = dmalloc<int>(1);
-    o_ids = dmalloc<int32_t>((size_t)kDraftMaxSteps * kDraftMaxTopk);
-    o_dids = dmalloc<int32_t>((size_t)kDraftMaxSteps * kDraftMaxTopk);
-    o_lp = dmalloc<float>((size_t)kDraftMaxSteps * kDraftMaxTopk);
+    // the round's outputs, ids | draft ids | log-probs, in one block that a
+    // single copy brings back into pinned memory
+    o_ids = dmalloc<int32_t>(3 * kDraftOut);
+    o_dids = o_ids + kDraftOut;
+    o_lp = (float *)(o_ids + 2 * kDraftOut);
+    SD_D3_CHECK(hipHostMalloc((void **)&pin, (3 * kDraftOut + 4) * sizeof(int32_t), hipHostMallocDefault));
     SD_D3_CHECK(hipDeviceSynchronize());
 }
 
@@ -149,8 +152,9 @@ Draft3::~Draft3() {
     for (void *p : {(void *)w, (void *)d2t, (void *)cos16, (void *)sin16, (void *)kc, (void *)vc, (void *)x3,
                     (void *)hid[0], (void *)hid[1], (void *)proj, (void *)comb, (void *)qkv, (void *)att,
                     (void *)after, (void *)xn, (void *)act, (void *)xf, (void *)emb, (void *)hin32, (void *)logits,
-                    (void *)tok, (void *)tk_part, (void *)tk_cnt, (void *)o_ids, (void *)o_dids, (void *)o_lp})
+                    (void *)tok, (void *)tk_part, (void *)tk_cnt, (void *)o_ids})
         if (p) hipFree(p);
+    if (pin) hipHostFree(pin);
     if (own) hipStreamDestroy(own);
 }
 
@@ -371,8 +375,8 @@ void Draft3::round(Model &target, Decoder &dec, const uint32_t layers[3], int de
     //    the device (TreeDecoder::last_hidden_states_multi), as f16 [low, mid, high]
     const float *h3 = dec.collect_hidden_device(layers, 3);
     launch_to_f16(h3, 3 * (int64_t)cfg.hidden, x3, st);
-    const int32_t root = (int32_t)dec.history.back();
-    SD_D3_CHECK(hipMemcpyAsync(tok, &root, 4, hipMemcpyHostToDevice, st));
+    pin[3 * kDraftOut] = (int32_t)dec.history.back();
+    SD_D3_CHECK(hipMemcpyAsync(tok, pin + 3 * kDraftOut, 4, hipMemcpyHostToDevice, st));
     // 2. depth steps: the embedding of the current token, the midlayer, norm +
     //    lm_head, top-k; the top-1 target id is the next step's token
     reset();
@@ -382,10 +386,11 @@ void Draft3::round(Model &target, Decoder &dec, const uint32_t layers[3], int de
                     o_lp + s * kDraftMaxTopk);
     }
     const size_t n = (size_t)depth * kDraftMaxTopk;
-    SD_D3_CHECK(hipMemcpyAsync(ids, o_ids, n * 4, hipMemcpyDeviceToHost, st));
-    SD_D3_CHECK(hipMemcpyAsync(draft_ids, o_dids, n * 4, hipMemcpyDeviceToHost, st));
-    SD_D3_CHECK(hipMemcpyAsync(log_probs, o_lp, n * 4, hipMemcpyDeviceToHost, st));
+    SD_D3_CHECK(hipMemcpyAsync(pin, o_ids, 3 * kDraftOut * 4, hipMemcpyDeviceToHost, st));
     SD_D3_CHECK(hipStreamSynchronize(st));
+    std::memcpy(ids, pin, n * 4);
+    std::memcpy(draft_ids, pin + kDraftOut, n * 4);
+    std::memcpy(log_probs, pin + 2 * kDraftOut, n * 4);
 }
 
 // ===== EAGLE-2 (EagleDraftCandle, crates/speculate/src/methods/eagle.rs) =====
@@ -439,9 +444,12 @@ Draft2::Draft2(const Draft2Cfg &c) : cfg(c) {
     out32 = dmalloc<float>(H);
     logits = dmalloc<float>(c.vocab);
     tok = dmalloc<int32_t>(1);
-    o_ids = dmalloc<int32_t>((size_t)kDraftMaxSteps * kDraftMaxTopk);
-    o_dids = dmalloc<int32_t>((size_t)kDraftMaxSteps * kDraftMaxTopk);
-    o_lp = dmalloc<float>((size_t)kDraftMaxSteps * kDraftMaxTopk);
+    // the round's outputs, ids | draft ids | log-probs, in one block that a
+    // single copy brings back into pinned memory
+    o_ids = dmalloc<int32_t>(3 * kDraftOut);
+    o_dids = o_ids + kDraftOut;
+    o_lp = (float *)(o_ids + 2 * kDraftOut);
+    SD_D3_CHECK(hipHostMalloc((void **)&pin, (3 * kDraftOut + 4) * sizeof(int32_t), hipHostMallocDefault));
     tk_part = dmalloc<uint64_t>((size_t)256 * (1 + kDraftMaxTopk));
     tk_cnt = dmalloc<int>(1);
     SD_D3_CHECK(hipDeviceSynchronize());
@@ -452,9 +460,9 @@ Draft2::~Draft2() {
     if (own) hipStreamSynchronize(own);
     for (void *p : {(void *)w, (void *)cos16, (void *)sin16, (void *)kc, (void *)vc, (void *)comb, (void *)xs,
                     (void *)qkv, (void *)att, (void *)after, (void *)xn, (void *)act, (void *)xp, (void *)hin32,
-                    (void *)out32, (void *)logits, (void *)tok, (void *)o_ids, (void *)o_dids, (void *)o_lp,
-                    (void *)tk_part, (void *)tk_cnt})
+                    (void *)out32, (void *)logits, (void *)tok, (void *)o_ids, (void *)tk_part, (void *)tk_cnt})
         if (p) hipFree(p);
+    if (pin) hipHostFree(pin);
     if (own) hipStreamDestroy(own);
 }
 
@@ -597,9 +605,9 @@ void Draft2::round(Model &target, Decoder &dec, const float *target_hidden, int 
     SD_D3_CHECK(hipSetDevice(cfg.device));
     hipStream_t st = target.st;
     const int H = cfg.hidden;
-    const int32_t root = (int32_t)dec.history.back();
+    pin[3 * kDraftOut] = (int32_t)dec.history.back();
     SD_D3_CHECK(hipMemcpyAsync(hin32, target_hidden, (size_t)H * 4, hipMemcpyHostToDevice, st));
-    SD_D3_CHECK(hipMemcpyAsync(tok, &root, 4, hipMemcpyHostToDevice, st));
+    SD_D3_CHECK(hipMemcpyAsync(tok, pin + 3 * kDraftOut, 4, hipMemcpyHostToDevice, st));
     launch_to_f16(hin32, H, comb, st);
     reset();
     for (int s = 0; s < depth; s++) {
@@ -622,9 +630,10 @@ void Draft2::round(Model &target, Decoder &dec, const float *target_hidden, int 
         launch_draft_topk(t, st);
     }
     const size_t n = (size_t)depth * kDraftMaxTopk;
-    SD_D3_CHECK(hipMemcpyAsync(ids, o_ids, n * 4, hipMemcpyDeviceToHost, st));
-    SD_D3_CHECK(hipMemcpyAsync(log_probs, o_lp, n * 4, hipMemcpyDeviceToHost, st));
+    SD_D3_CHECK(hipMemcpyAsync(pin, o_ids, 3 * kDraftOut * 4, hipMemcpyDeviceToHost, st));
     SD_D3_CHECK(hipStreamSynchronize(st));
+    std::memcpy(ids, pin, n * 4);
+    std::memcpy(log_probs, pin + 2 * kDraftOut, n * 4);
 }
 
 }  // namespace sd

@@ -19,6 +19,7 @@ class Decoder;
 constexpr int kDraftMaxK = 32768;    // inputs of one matrix-vector product
 constexpr int kDraftMaxSteps = 16;   // draft steps of one round (the draft's own KV cache)
 constexpr int kDraftMaxTopk = 8;     // candidates per step
+constexpr size_t kDraftOut = (size_t)kDraftMaxSteps * kDraftMaxTopk;  // entries of one round's output array
 
 enum DraftGemvMode : int { DG_STORE = 0, DG_ADD = 1, DG_SWIGLU = 2, DG_LOGITS = 3 };
 
@@ -129,8 +130,9 @@ class Draft3 {
     int32_t *tok = nullptr;                         // the current step's token id
     uint64_t *tk_part = nullptr;                    // top-k slice partials
     int *tk_cnt = nullptr;                          // top-k arrival count
-    int32_t *o_ids = nullptr, *o_dids = nullptr;    // [kDraftMaxSteps][kDraftMaxTopk]
+    int32_t *o_ids = nullptr, *o_dids = nullptr;    // [kDraftMaxSteps][kDraftMaxTopk], in one block with o_lp
     float *o_lp = nullptr;
+    int32_t *pin = nullptr;                         // pinned: the three output arrays, then the root token
     int cur = 0;  // which hid[] holds the current step's input
     int steps = 0;
     hipStream_t own = nullptr;
@@ -191,8 +193,9 @@ class Draft2 {
     uint16_t *comb = nullptr, *xs = nullptr, *qkv = nullptr, *att = nullptr, *after = nullptr, *xn = nullptr,
              *act = nullptr, *xp = nullptr;
     float *hin32 = nullptr, *out32 = nullptr, *logits = nullptr;
-    int32_t *tok = nullptr, *o_ids = nullptr, *o_dids = nullptr;
+    int32_t *tok = nullptr, *o_ids = nullptr, *o_dids = nullptr;  // o_ids | o_dids | o_lp: one block
     float *o_lp = nullptr;
+    int32_t *pin = nullptr;  // pinned: the three output arrays, then the root token
     uint64_t *tk_part = nullptr;
     int *tk_cnt = nullptr;
     int steps = 0;

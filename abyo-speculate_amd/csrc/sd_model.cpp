@@ -1267,8 +1267,13 @@ const float *Decoder::collect_hidden_device(const uint32_t *layers, size_t nl) {
 void Decoder::argmax_rows(int32_t *out, size_t n) {
     Model &m = *model;
     if (n > (size_t)m.logits_rows_last) throw ArgError("fewer rows in the last verify pass");
-    SD_HIP_CHECK(hipMemcpyAsync(out, m.argmax, n * 4, hipMemcpyDeviceToHost, m.st));
+    // through the pinned output region of the acceptance staging block (a
+    // direct copy; a pageable destination goes through the runtime's own
+    // staging buffer first)
+    int *pin = m.acc_stage + (size_t)kAccTreeInts * m.cfg.max_batch;
+    SD_HIP_CHECK(hipMemcpyAsync(pin, m.argmax, n * 4, hipMemcpyDeviceToHost, m.st));
     SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    std::memcpy(out, pin, n * 4);
 }
 
 // batched_logits + greedy acceptance with the logits kept in HBM:
@@ -1306,8 +1311,10 @@ void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents
     if (strict) {
         next_logits(nullptr);
         launch_argmax_rows(m.last_row, m.cfg.vocab, m.cfg.vocab, 1, m.argmax, m.st);
-        SD_HIP_CHECK(hipMemcpyAsync(&root_am, m.argmax, 4, hipMemcpyDeviceToHost, m.st));
+        int *pin = m.acc_stage + (size_t)kAccTreeInts * m.cfg.max_batch;  // pinned (see argmax_rows)
+        SD_HIP_CHECK(hipMemcpyAsync(pin, m.argmax, 4, hipMemcpyDeviceToHost, m.st));
         SD_HIP_CHECK(hipStreamSynchronize(m.st));
+        root_am = pin[0];
     }
     tree_logits_keep_kv(tokens, parents, n, nullptr, nullptr);
     std::vector<int32_t> am(n);
