@@ -18,6 +18,11 @@ INCLUDE = os.environ.get("SD_INCLUDE_DIR", os.path.join(os.path.dirname(HERE), "
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
+          # multiply-adds (and products rounded to fp16) fuse only where one
+          # source expression forms them, so every kernel that inlines the
+          # same device code rounds the same way (the default, fast, lets the
+          # backend fuse across statements depending on the surrounding code)
+          "-ffp-contract=on",
           # no packed-FP32 instructions anywhere (hipcc's host pass warns that it
           # does not know the feature; that warning is expected)
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -55,12 +55,6 @@ namespace sd {
 // Also the first-max argmax (greedy one-hot).
 constexpr int kRsT = 256, kSlice = 8192;
 
-__device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
-    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev64(const void *p) {
-    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint64_t pack2(float a, uint32_t b) { return (uint64_t)__float_as_uint(a) | ((uint64_t)b << 32); }
 
 // (m1, s1) + (m2, s2) of the online softmax sum

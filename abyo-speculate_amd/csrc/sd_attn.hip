@@ -273,7 +273,7 @@ __device__ __forceinline__ void query_init(AttnState<HD, QT> &S, int t, const Qu
     for (int dc = 0; dc < HD / 32; dc++) {
         half8 v = r.live ? __builtin_bit_cast(half8, r.q[dc]) : half8{};
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (_Float16)((float)v[i] * sl2);
+        for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(_Float16, f2h((float)v[i] * sl2));
         S.qf[t][dc] = v;
     }
     S.mk0[t] = r.mk0;
@@ -419,16 +419,6 @@ __device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, K
     kv_load_v<HD>(nb, src, kk + 32 < k1 ? kk + 32 : -1);
     zero_stale_v<HD / 16>(b.v, kk, T, g);
     step_pv<HD, QT>(S, b.v, bp, alpha, moved, tl);
-}
-
-// Device-scope (sc1) 8-byte accesses, for data that workgroups of one launch
-// hand to each other: a store is visible, and a load fresh, across the XCDs'
-// separate L2 caches without writing back or invalidating those caches.
-__device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
-    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev64(const void *p) {
-    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Result of one query (lane (r16, g) holds d = dt*16 + 4g + i): with one

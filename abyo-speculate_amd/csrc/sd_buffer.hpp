@@ -36,6 +36,20 @@ __device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t vo, uint32_t so) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
 }
 
+// Device-scope (sc1) 8-byte accesses, for data that workgroups of one launch
+// hand to each other.  Each XCD has its own L2: a plain store may stay there
+// until the kernel ends and a plain load may hit a line another XCD has since
+// rewritten, while an sc1 store is written through to memory and an sc1 load
+// reads past the XCD's L2, without writing back or invalidating whole caches.
+// (Plain stores handed over inside one launch were measured to deliver stale
+// data to other XCDs.)  Device-scope atomics are coherent across the XCDs.
+__device__ __forceinline__ void st_dev64(void *p, uint64_t v) {
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const void *p) {
+    return __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // A kernel's argument block reaches its waves through the scalar cache.  A
 // kernel that reads a large parameter struct field by field, with branches
 // between the reads, waits one memory round trip (~0.5 us) per cache line it

@@ -81,7 +81,15 @@ __host__ __device__ inline int64_t kv_off(int which, int64_t pos, int d, int hd)
 
 // ---- fp16 bit helpers --------------------------------------------------
 __device__ inline float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ inline uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// f32 -> fp16 (round to nearest even) of the f32 value as the source computed
+// it.  The empty asm keeps the compiler from fusing a producing multiply or
+// multiply-add into the conversion (v_fma_mix*_f16: one rounding instead of
+// two), which it does in some kernels and not in others; the same source then
+// rounds the same way in every kernel that inlines it.
+__device__ inline uint16_t f2h(float f) {
+    asm("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 // ---- seeded synthetic values (same arithmetic as the CPU generator) -----
 __host__ __device__ inline uint64_t mix64(uint64_t z) {

@@ -107,7 +107,12 @@ def test_eagle2_reference_config_chain(hip):
                 print(f"eagle2 pos {pos0 + s}: {e:.2e}", flush=True)
                 assert e < TOL, (pos0, s, e)
                 assert np.array_equal(out_d, out_d.astype(np.float16).astype(np.float32))
-                h_dev, h_or = out_d, out_o
+                # the next step's input is the oracle's output on both sides (each
+                # keeps its own KV rows): with random weights the draft amplifies a
+                # difference fed back through its hidden input from step to step, so
+                # a chain of each side's own outputs would test that amplification
+                # rather than one forward at these shapes
+                h_dev = h_or = out_o
     finally:
         d.close()
 
