@@ -12,24 +12,21 @@
 // query token i iff bit t of mask[i] is set (ancestor-or-self for trees,
 // t <= i for a causal chain).
 //
-// Attention is split flash-decoding with the KV streamed straight from HBM
-// into MFMA operand registers (no LDS staging): the blocked cache layout makes
-// every operand a 16-byte load per lane, 1 KiB contiguous per wave.  Scores
-// are computed transposed, S^T = K Q^T (16 keys x 16 queries per MFMA tile),
-// so a lane's accumulator already holds the P^T operand of O^T = V^T P^T.
-//
-// Grid (kv head, key split, query tile).  A workgroup's 4 waves take 4
-// consecutive key ranges of keys_per_wave keys and one query tile (16 of the
-// n_rep query heads of the KV head times the M tokens); their partial softmax
-// states are merged in LDS in a fixed order, and the splits by the last
-// workgroup of the tile to finish (up to 16 tokens; a counter per tile, device-
-// scope partials) or by a combine kernel (more tokens), with the same
-// arithmetic; nothing to merge when one split covers all keys.  Up to 16 tokens,
-// keys_per_wave and the split boundaries depend on P only, so a query's
-// result does not depend on how many other queries share the call.
+// Split flash-decoding (sd_attn_dev.hpp).  Up to 16 tokens: grid (kv head,
+// key split, query tile); a workgroup's 8 waves take the split's 32-key steps
+// in turn for one query tile (16 of the n_rep query heads of the KV head times
+// the M tokens); their partial softmax states are merged in LDS in a fixed
+// order, and the splits by the last workgroup of the tile to finish (a counter
+// per tile, device-scope partials) or by a combine kernel, with the same
+// arithmetic; nothing to merge when one split covers all keys.  The same
+// workgroups also run inside the fused Q/K/V launch (sd_qgemm.hip).
+// keys_per_wave and the split boundaries depend on P only, so a query's result
+// does not depend on how many other queries share the call.
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
+#include "sd_attn_dev.hpp"
 #include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels_attn.hpp"
@@ -182,515 +179,12 @@ __global__ __launch_bounds__(64) void k_rope_kv(RopeKvParams p) {
 
 #pragma clang fp contract(fast)
 
-// ---- flash-decode over one key split -------------------------------------------
-template <int HD> struct KvStep {
-    uintx4 k[2][HD / 32];  // S^T A operands: two 16-key tiles x HD/32 d-chunks
-    uintx4 v[HD / 16];     // O^T A operands: HD/16 d-tiles x 32 key slots
-};
-
-// One KV head's K and V streams as buffer resources and the lane's fixed byte
-// offset inside a 32-key block, (r16 * 32 + g * 8) * 2 in both layouts; the
-// block's offset kk * HD * 2 is wave-uniform and goes in a scalar register.
-struct KvSrc {
-    rsrc_t k, v;
-    uint32_t lane;
-};
-// A load that must not happen gets an offset past the resource (a stream is
-// < 2 GiB), which reads zeros without touching memory; loads are then issued
-// unconditionally and the compiler's wait counts stay exact across the loop.
-constexpr uint32_t kNoKv = 0x80000000u;
-__device__ __forceinline__ uint32_t kv_so(int kk, int HD) { return uni(kk < 0 ? kNoKv : (uint32_t)kk * HD * 2u); }
-
-// 32 keys [kk, kk+32) of one stream (kk < 0: none): 16-byte pieces, 1 KiB per wave each
+// M <= 16 (decode, linear verify): see attn_wg.  Grid (kv head, key split,
+// query tile).
 template <int HD>
-__device__ __forceinline__ void kv_load_k(KvStep<HD> &b, const KvSrc &s, int kk) {
-    const uint32_t so = kv_so(kk, HD);
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int dc = 0; dc < HD / 32; dc++) b.k[kt][dc] = bld16(s.k, s.lane + kt * 32 * HD + dc * 1024, so);
-}
-template <int HD>
-__device__ __forceinline__ void kv_load_v(KvStep<HD> &b, const KvSrc &s, int kk) {
-    const uint32_t so = kv_so(kk, HD);
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) b.v[dt] = bld16(s.v, s.lane + dt * 1024, so);
-}
-
-template <int HD, int QT> struct AttnState {
-    half8 qf[QT][HD / 32];
-    floatx4 o[QT][HD / 16];
-    float m[QT], l[QT];
-    uint64_t mk0[QT], mk1[QT];
-};
-
-// key of P^T / V^T slot j (0..7) of lane group g within a 32-key step
-__device__ __forceinline__ int slot_key(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
-
-// The 4 lanes of one query (lane groups g = 0..3 of a 16x16 MFMA layout)
-// combined with lane ^ 16 and lane ^ 32: two VALU swaps instead of LDS
-// permutes.  Every lane ends with the same value (the operations commute).
-__device__ __forceinline__ float xmax4(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float xsum4(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// A query tile's raw operands for lane (r16 = query row, g): 8 dims of each
-// 32-dim chunk and the row's tree-mask words.  Lanes past the last query read
-// the last query's row, so every load is in bounds and unconditional and the
-// compiler issues them back to back before the first wait; query_init zeroes
-// those lanes' fragments.
-template <int HD> struct QueryRaw {
-    uintx4 q[HD / 32];
-    uint64_t mk0, mk1;
-    bool live;
-};
-template <int HD>
-__device__ __forceinline__ void query_fetch(QueryRaw<HD> &r, const AttnParams &p, int h, int q, int g) {
-    const int nq = p.M * p.n_rep;
-    r.live = q < nq;
-    const int qc = r.live ? q : nq - 1;
-    const int m = qc / p.n_rep, rep = qc % p.n_rep;
-    const uint16_t *qr = p.q16 + ((int64_t)(h * p.n_rep + rep) * p.M + m) * HD;
-#pragma unroll
-    for (int dc = 0; dc < HD / 32; dc++) r.q[dc] = *(const uintx4 *)(qr + dc * 32 + g * 8);
-    r.mk0 = p.mask[(int64_t)m * p.mask_words];
-    r.mk1 = p.mask_words > 1 ? p.mask[(int64_t)m * p.mask_words + 1] : 0ull;
-}
-// the query scaled by scale * log2(e) (scores in base-2 softmax units) and an
-// empty softmax state
-template <int HD, int QT>
-__device__ __forceinline__ void query_init(AttnState<HD, QT> &S, int t, const QueryRaw<HD> &r, float sl2) {
-#pragma unroll
-    for (int dc = 0; dc < HD / 32; dc++) {
-        half8 v = r.live ? __builtin_bit_cast(half8, r.q[dc]) : half8{};
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(_Float16, f2h((float)v[i] * sl2));
-        S.qf[t][dc] = v;
-    }
-    S.mk0[t] = r.mk0;
-    S.mk1[t] = r.mk1;
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) S.o[t][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    S.m[t] = -INFINITY;
-    S.l[t] = 0.f;
-}
-
-// Softmax of one 32-key step for query tile t: st holds the lane's 8 scores
-// (keys kk + 16 kt + 4g + i) in base-2 units; returns the P^T fragment.
-//
-// The running max m of a query (the same in its 4 lanes) moves only when a
-// score exceeds it by more than 8: probabilities exp2(s - m) then stay below
-// 256, which fp16 and f32 hold with full relative precision.  Each lane keeps
-// its own partial sum l of the probabilities it produced; the 4 partials of a
-// query are added once, at the end.  So the common step has no cross-lane
-// traffic at all: the max is only gathered (and the accumulators rescaled by
-// alpha) when some lane of the wave sees a score above its m + 8.
-// Keys at or past lim (<= T) belong to another range and are masked.
-template <int HD, int QT>
-__device__ __forceinline__ half8 step_softmax(AttnState<HD, QT> &S, int t, floatx4 (&st)[2], int kk, int P, int T,
-                                              int lim, int g, float &alpha, bool &moved) {
-    const bool full = kk + 32 <= P && kk + 32 <= lim;  // every key of the step is visible to every query
-    float lmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v = st[kt][i];
-            if (!full) {
-                const int key = kk + kt * 16 + 4 * g + i;
-                bool vis = key < P && key < lim;
-                if (!vis && key < lim) {
-                    const int tt = key - P;
-                    vis = (((tt < 64 ? S.mk0[t] : S.mk1[t]) >> (tt & 63)) & 1ull) != 0;
-                }
-                v = vis ? v : -INFINITY;
-            }
-            st[kt][i] = v;
-            lmax = fmaxf(lmax, v);
-        }
-    alpha = 1.f;
-    // -inf + 8 == -inf: the first finite score always moves the max
-    if (__builtin_amdgcn_ballot_w64(lmax > S.m[t] + 8.f) != 0) {
-        const float cm = xmax4(lmax);
-        if (cm > S.m[t] + 8.f) {  // the same decision in the query's 4 lanes
-            alpha = __builtin_amdgcn_exp2f(S.m[t] - cm);
-            S.m[t] = cm;
-            moved = true;
-        }
-    }
-    const float muse = S.m[t] == -INFINITY ? 0.f : S.m[t];
-    float ps = 0.f;
-    uint32_t pk[4];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-        float e[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            e[i] = __builtin_amdgcn_exp2f(st[kt][i] - muse);
-            ps += e[i];
-        }
-        pk[2 * kt] = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
-        pk[2 * kt + 1] = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
-    }
-    S.l[t] = S.l[t] * alpha + ps;
-    const uintx4 bu = {pk[0], pk[1], pk[2], pk[3]};
-    return __builtin_bit_cast(half8, bu);
-}
-
-// keys >= T hold stale cache rows: their P^T entries are 0, and their V entries
-// are zeroed so that nothing but finite values meets the MFMA
-template <int NDT>
-__device__ __forceinline__ void zero_stale_v(uintx4 (&v)[NDT], int kk, int T, int g) {
-    if (kk + 32 <= T) return;
-    uint32_t keep[4];
-#pragma unroll
-    for (int w = 0; w < 4; w++)
-        keep[w] = (kk + slot_key(g, 2 * w) < T ? 0x0000ffffu : 0u) | (kk + slot_key(g, 2 * w + 1) < T ? 0xffff0000u : 0u);
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        v[dt].x &= keep[0];
-        v[dt].y &= keep[1];
-        v[dt].z &= keep[2];
-        v[dt].w &= keep[3];
-    }
-}
-
-// O^T += V^T P^T for the live tiles, after the rescale the step asked for
-template <int HD, int QT>
-__device__ __forceinline__ void step_pv(AttnState<HD, QT> &S, const uintx4 (&v)[HD / 16], const half8 (&bp)[QT],
-                                        const float (&alpha)[QT], bool moved, const bool (&tl)[QT]) {
-    constexpr int NDT = HD / 16;
-    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
-#pragma unroll
-        for (int t = 0; t < QT; t++)
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) S.o[t][dt] *= alpha[t];
-    }
-#pragma unroll
-    for (int t = 0; t < QT; t++) {
-        if (!tl[t]) continue;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            S.o[t][dt] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, v[dt]), bp[t], S.o[t][dt], 0, 0, 0);
-    }
-}
-
-// S^T = K Q^T for the live tiles
-template <int HD, int QT>
-__device__ __forceinline__ void step_scores(const AttnState<HD, QT> &S, const uintx4 (&k)[2][HD / 32], int t,
-                                            floatx4 (&st)[2]) {
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-        st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int dc = 0; dc < HD / 32; dc++)
-            st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, k[kt][dc]), S.qf[t][dc], st[kt],
-                                                            0, 0, 0);
-    }
-}
-
-// One 32-key step from registers for all query tiles: scores and softmax,
-// then the next step's V loads are issued (the current K is dead by then, so
-// the two register buffers never hold four operand sets at once), then PV.
-template <int HD, int QT>
-__device__ __forceinline__ void attn_step(AttnState<HD, QT> &S, KvStep<HD> &b, KvStep<HD> &nb, const KvSrc &src,
-                                          int kk, int k1, int P, int T, int g) {
-    half8 bp[QT];
-    float alpha[QT];
-    bool tl[QT];
-    bool moved = false;
-#pragma unroll
-    for (int t = 0; t < QT; t++) {
-        tl[t] = true;
-        floatx4 st[2];
-        step_scores<HD, QT>(S, b.k, t, st);
-        bp[t] = step_softmax<HD, QT>(S, t, st, kk, P, T, T, g, alpha[t], moved);
-    }
-    kv_load_v<HD>(nb, src, kk + 32 < k1 ? kk + 32 : -1);
-    zero_stale_v<HD / 16>(b.v, kk, T, g);
-    step_pv<HD, QT>(S, b.v, bp, alpha, moved, tl);
-}
-
-// Result of one query (lane (r16, g) holds d = dt*16 + 4g + i): with one
-// split the normalised row goes straight into the wo input (fp16, fragment
-// order); otherwise o / l as fp16 and (m, l) for the merge of the splits,
-// which weighs split s by l_s * exp2(m_s - max m).  DEV: the partials are
-// stored at device scope, for a merge inside the same launch.
-template <int HD, bool DEV = false>
-__device__ __forceinline__ void attn_emit(const AttnParams &p, int s, int head, int m, int g,
-                                          const floatx4 (&o)[HD / 16], float mq, float l) {
-    const float inv = 1.0f / l;
-    if (p.nsplit == 1) {
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int64_t k = (int64_t)head * HD + dt * 16 + 4 * g + i;
-                p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(o[dt][i] * inv);
-            }
-        return;
-    }
-    const int64_t pi = ((int64_t)s * p.n_heads + head) * p.M + m;
-    uint16_t *po = (uint16_t *)p.part_o + pi * HD;
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) {
-        const float w = l > 0.f ? inv : 0.f;  // a query that saw no key of this split has l = 0
-        const uintx2 v{(uint32_t)f2h(o[dt][0] * w) | ((uint32_t)f2h(o[dt][1] * w) << 16),
-                       (uint32_t)f2h(o[dt][2] * w) | ((uint32_t)f2h(o[dt][3] * w) << 16)};
-        if constexpr (DEV) st_dev64(po + dt * 16 + 4 * g, (uint64_t)v.x | ((uint64_t)v.y << 32));
-        else *(uintx2 *)(po + dt * 16 + 4 * g) = v;
-    }
-    if (g == 0) {
-        if constexpr (DEV) {
-            st_dev64(p.part_ml + 2 * pi, (uint64_t)__float_as_uint(mq) | ((uint64_t)__float_as_uint(l) << 32));
-        } else {
-            p.part_ml[2 * pi] = mq;
-            p.part_ml[2 * pi + 1] = l;
-        }
-    }
-}
-
-// Merge of the splits by the last workgroup of a (KV head h, query tile qg)
-// to finish: thread (r = tid / 16, c = tid % 16) owns query qg * 16 + r and
-// dims [c HD/16, +HD/16).  The arithmetic, and its order, is k_attn_combine's:
-// out = sum_s w_s o_s / sum_s w_s in split order, w_s = l_s exp2(m_s - max m).
-constexpr int kFusedMaxSplits = 64;
-// The merge when every split's (m, l) and pieces fit in registers at once
-// (ns <= NSM): one memory round trip; the same arithmetic and order as the
-// general path of attn_merge_tile.
-template <int HD, int NSM>
-__device__ __forceinline__ void attn_merge_regs(const AttnParams &p, int head, int m, int c, int ns, int64_t stride,
-                                                int64_t pi0) {
-    constexpr int DPT = HD / 16;
-    const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
-    uint64_t mlv[NSM], ov[NSM][DPT / 4];
-#pragma unroll
-    for (int j = 0; j < NSM; j++) {
-        mlv[j] = j < ns ? ld_dev64(p.part_ml + 2 * (pi0 + j * stride)) : 0ull;
-#pragma unroll
-        for (int k = 0; k < DPT / 4; k++) ov[j][k] = j < ns ? ld_dev64(po + j * stride * HD + 4 * k) : 0ull;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NSM; j++)
-        if (j < ns) mx = fmaxf(mx, __uint_as_float((uint32_t)mlv[j]));
-    float W = 0.f, acc[DPT];
-#pragma unroll
-    for (int i = 0; i < DPT; i++) acc[i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < NSM; j++) {
-        if (j < ns) {
-            const float ms = __uint_as_float((uint32_t)mlv[j]);
-            const float w = ms == -INFINITY ? 0.f : __uint_as_float((uint32_t)(mlv[j] >> 32)) * exp2f(ms - mx);
-            W += w;
-#pragma unroll
-            for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
-        }
-    }
-    // dims 4k .. 4k + 3 of this thread sit in fragment slots f, f + 2, f + 1, f + 3
-#pragma unroll
-    for (int k = 0; k < DPT / 4; k++) {
-        const int64_t e = (int64_t)head * HD + c * DPT + 4 * k;
-        *(uintx2 *)(p.out16 + (int64_t)m * p.out_ld + frag_index(e)) =
-            uintx2{(uint32_t)f2h(acc[4 * k] / W) | ((uint32_t)f2h(acc[4 * k + 2] / W) << 16),
-                   (uint32_t)f2h(acc[4 * k + 1] / W) | ((uint32_t)f2h(acc[4 * k + 3] / W) << 16)};
-    }
-}
-
-template <int HD> __device__ __forceinline__ void attn_merge_tile(const AttnParams &p, int h, int qg) {
-    constexpr int DPT = HD / 16;  // dims per thread, 4 or 8: one or two 8-byte loads per split
-    __shared__ float cml[16][kFusedMaxSplits][2];
-    const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
-    const int nq = p.M * p.n_rep, ns = p.nsplit;
-    const int q = qg * 16 + r;
-    const bool live = q < nq;
-    const int head = h * p.n_rep + (live ? q % p.n_rep : 0), m = live ? q / p.n_rep : 0;
-    const int64_t stride = (int64_t)p.n_heads * p.M;  // partial rows per split
-    const int64_t pi0 = (int64_t)head * p.M + m;
-    if (ns <= 16) {
-        if (!live) return;
-        if (ns <= 8) attn_merge_regs<HD, 8>(p, head, m, c, ns, stride, pi0);
-        else attn_merge_regs<HD, 16>(p, head, m, c, ns, stride, pi0);
-        return;
-    }
-    for (int s = c; s < ns; s += 16) {
-        const uint64_t v = live ? ld_dev64(p.part_ml + 2 * (pi0 + s * stride)) : 0ull;
-        cml[r][s][0] = __uint_as_float((uint32_t)v);
-        cml[r][s][1] = __uint_as_float((uint32_t)(v >> 32));
-    }
-    __syncthreads();
-    if (!live) return;
-    float mx = -INFINITY;
-    for (int s = 0; s < ns; s++) mx = fmaxf(mx, cml[r][s][0]);
-    const uint16_t *po = (const uint16_t *)p.part_o + pi0 * HD + c * DPT;
-    float W = 0.f, acc[DPT];
-#pragma unroll
-    for (int i = 0; i < DPT; i++) acc[i] = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-        // 8 splits' pieces requested at once
-        uint64_t ov[8][DPT / 4];
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-#pragma unroll
-            for (int k = 0; k < DPT / 4; k++) ov[j][k] = s0 + j < ns ? ld_dev64(po + (s0 + j) * stride * HD + 4 * k) : 0ull;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (s0 + j < ns) {
-                const float ms = cml[r][s0 + j][0];
-                const float w = ms == -INFINITY ? 0.f : cml[r][s0 + j][1] * exp2f(ms - mx);
-                W += w;
-#pragma unroll
-                for (int i = 0; i < DPT; i++) acc[i] += h2f((uint16_t)(ov[j][i >> 2] >> (16 * (i & 3)))) * w;
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < DPT; i++) {
-        const int64_t k = (int64_t)head * HD + c * DPT + i;
-        p.out16[(int64_t)m * p.out_ld + frag_index(k)] = f2h(acc[i] / W);
-    }
-}
-
-template <int HD, int QT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnParams p) {
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnParams) {
     warm_kernargs<sizeof(AttnParams)>();
-    constexpr int NDT = HD / 16;
-    const int h = blockIdx.x, s = blockIdx.y, qg = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r16 = lane & 15, g = lane >> 4;
-    const int nq = p.M * p.n_rep;
-    const int T = p.P + p.M;
-    const int k0 = (s * 4 + wave) * p.keys_per_wave;
-    const int k1 = min(k0 + p.keys_per_wave, T);
-    const uint32_t stream_bytes = (uint32_t)p.cap * HD * 2u;
-    KvSrc src;
-    src.k = make_rsrc(p.kc + (int64_t)h * p.cap * HD, stream_bytes);
-    src.v = make_rsrc(p.vc + (int64_t)h * p.cap * HD, stream_bytes);
-    src.lane = (uint32_t)(r16 * 32 + g * 8) * 2u;
-
-    // the queries first (just written by the Q/K/V launch), then the first
-    // 32 keys; two register buffers: the next 32 keys load while the current
-    // ones compute (K at the start of a step, V once the step's scores are done)
-    QueryRaw<HD> qr[QT];
-#pragma unroll
-    for (int t = 0; t < QT; t++) query_fetch<HD>(qr[t], p, h, (qg * QT + t) * 16 + r16, g);
-    KvStep<HD> b0, b1;
-    int kk = k0;
-    kv_load_k<HD>(b0, src, kk < k1 ? kk : -1);
-    kv_load_v<HD>(b0, src, kk < k1 ? kk : -1);
-
-    AttnState<HD, QT> S;
-    const float sl2 = p.scale * 1.4426950408889634f;  // scale * log2(e): softmax in base 2
-#pragma unroll
-    for (int t = 0; t < QT; t++) query_init<HD, QT>(S, t, qr[t], sl2);
-
-    while (kk < k1) {
-        kv_load_k<HD>(b1, src, kk + 32 < k1 ? kk + 32 : -1);
-        attn_step<HD, QT>(S, b0, b1, src, kk, k1, p.P, T, g);
-        kk += 32;
-        if (kk >= k1) break;
-        kv_load_k<HD>(b0, src, kk + 32 < k1 ? kk + 32 : -1);
-        attn_step<HD, QT>(S, b1, b0, src, kk, k1, p.P, T, g);
-        kk += 32;
-    }
-#pragma unroll
-    for (int t = 0; t < QT; t++) S.l[t] = xsum4(S.l[t]);  // the query's 4 partial sums
-
-    // ---- merge the 4 waves' states: rescale to the common max, then
-    // (o0 + o2) + (o1 + o3) through LDS ----
-    __shared__ float sml[4][QT][16][2];
-    __shared__ floatx4 sob[2][QT][NDT][64];
-    if (g == 0) {
-#pragma unroll
-        for (int t = 0; t < QT; t++) {
-            sml[wave][t][r16][0] = S.m[t];
-            sml[wave][t][r16][1] = S.l[t];
-        }
-    }
-    __syncthreads();
-    float Lt[QT], Mt[QT];
-#pragma unroll
-    for (int t = 0; t < QT; t++) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; w++) mx = fmaxf(mx, sml[w][t][r16][0]);
-        float L = 0.f, fme = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const float mw = sml[w][t][r16][0];
-            const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-            L += sml[w][t][r16][1] * f;
-            if (w == wave) fme = f;
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) S.o[t][dt] *= fme;
-        Lt[t] = L;
-        Mt[t] = mx;
-    }
-    if (wave >= 2) {
-#pragma unroll
-        for (int t = 0; t < QT; t++)
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) sob[wave - 2][t][dt][lane] = S.o[t][dt];
-    }
-    __syncthreads();
-    if (wave < 2) {
-#pragma unroll
-        for (int t = 0; t < QT; t++)
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) S.o[t][dt] += sob[wave][t][dt][lane];
-    }
-    __syncthreads();
-    if (wave == 1) {
-#pragma unroll
-        for (int t = 0; t < QT; t++)
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) sob[0][t][dt][lane] = S.o[t][dt];
-    }
-    __syncthreads();
-    const bool fused = p.fused_combine != 0;
-    if (wave == 0) {
-#pragma unroll
-        for (int t = 0; t < QT; t++) {
-            const int q = (qg * QT + t) * 16 + r16;
-            if (q >= nq) continue;
-            floatx4 y[NDT];
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) y[dt] = S.o[t][dt] + sob[0][t][dt][lane];
-            if (fused) attn_emit<HD, true>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
-            else attn_emit<HD>(p, s, h * p.n_rep + q % p.n_rep, q / p.n_rep, g, y, Mt[t], Lt[t]);
-        }
-    }
-    if (!fused) return;
-
-    // ---- the last of the tile's nsplit workgroups to arrive merges the splits ----
-    // Wave 0 wrote the partials (device scope) and waits for those stores to
-    // complete before it counts the arrival; the last arrival resets the count
-    // for the next launch and reads every split's partials at device scope.
-    __shared__ int s_last;
-    if (wave == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (lane == 0) {
-            int *cnt = p.split_cnt + (int64_t)h * gridDim.z + qg;
-            const int last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.nsplit - 1;
-            if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = last;
-        }
-    }
-    __syncthreads();
-    if (!s_last) return;
-    static_assert(QT == 1, "the merge covers one 16-query tile per workgroup");
-    attn_merge_tile<HD>(p, h, qg);
+    attn_wg<HD, false>(kernarg<AttnParams>(), blockIdx.x, blockIdx.y, blockIdx.z, AttnWait{});
 }
 
 // ---- many queries (tree verify): query tiles across waves, keys shared in LDS ----
@@ -924,12 +418,14 @@ void launch_rope_kv(const RopeKvParams &p, hipStream_t st) {
     hipLaunchKernelGGL(k_rope_kv, dim3(p.M, (units + 63) / 64), dim3(64), 0, st, p);
 }
 
-static int attn_target_splits(int n_kv) { return n_kv >= 64 ? 1 : 64 / n_kv; }
-
 // Up to 16 rows (a linear verify or a decode step) the key ranges are a
 // function of P alone, so each row's arithmetic is the same as in a one-row
-// call.  Above, the splits shrink as query blocks grow, towards one 8-wave
-// workgroup per CU (256).
+// call: a split is 8 waves x 3 steps of 32 keys below 1024 cached positions
+// (one split up to ~750), else 8 waves x as many steps as give about 64 / n_kv
+// splits; each wave's first two steps sit in its registers (requested while
+// the fused launch's matmul runs), later ones stream behind them.  Above 16
+// rows, the splits shrink as query blocks grow, towards one 8-wave workgroup
+// per CU (256).
 AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
     const int T = P + M;
     if (M > 16) {
@@ -942,19 +438,21 @@ AttnSplit attn_split(int P, int M, int n_kv, int n_rep) {
         kps = kps < 32 ? 32 : (kps + 31) / 32 * 32;
         return AttnSplit{kps / 4, (T + kps - 1) / kps};
     }
-    const int want = attn_target_splits(n_kv);
-    int kpw = (P + 1 + 4 * want - 1) / (4 * want);
-    kpw = kpw < 32 ? 32 : (kpw + 31) / 32 * 32;
-    return AttnSplit{kpw, (T + 4 * kpw - 1) / (4 * kpw)};
+    // steps per wave: 3 (one split) for short prefixes, else as few as give
+    // about 64 / n_kv splits (64 workgroups per query tile), at most 32
+    const int want = std::min(kTMaxSplits, n_kv >= 64 ? 1 : 64 / n_kv);
+    const int spw = P < 1024 ? 3 : std::max(1, (P + 1 + 8 * 32 * want - 1) / (8 * 32 * want));
+    const int kps = 8 * 32 * spw;                                            // keys per split
+    return AttnSplit{32 * spw, (T + kps - 1) / kps};
 }
 
-// split size >= (P + 1) / want and >= 32, so for M <= 128
-// nsplit = ceil((P + M) / size) <= want + 1 + 128 / 32
-int attn_max_splits(int n_kv) {
-    const int t = attn_target_splits(n_kv);
-    const int n = (t > kTMaxSplits ? t : kTMaxSplits) + 5;
-    return n < kCombMaxSplits ? n : kCombMaxSplits;
-}
+// above 16 rows the split size is >= (P + 1) / want and >= 32 with
+// want <= kTMaxSplits, so for M <= 128 nsplit = ceil((P + M) / size) <=
+// want + 1 + 128 / 32; up to 16 rows a split holds 768 keys below 1024
+// cached positions (nsplit <= 2) and >= (P + 1) / want above (nsplit <=
+// want + 1 <= kTMaxSplits + 1)
+static_assert(kTMaxSplits + 5 <= kCombMaxSplits && kTMaxSplits + 5 <= kFusedMaxSplits, "split bounds");
+int attn_max_splits(int) { return kTMaxSplits + 5; }
 
 // LDS beyond the 64 KiB default for the M > 16 kernel: a function attribute
 // set once per device (the caller's current device), under a lock, since
@@ -974,54 +472,72 @@ static void allow_attn_t_lds() {
     done[dev] = true;
 }
 
-void launch_attention(const AttnParams &p, hipStream_t st) {
-    // a split covers 4 * keys_per_wave keys: whole 32-key blocks, and whole
-    // 32-key steps of each of the 4 waves up to 16 rows
-    const int kps_unit = p.M > 16 ? 8 : 32;
+static void attn_check(const AttnParams &p) {
+    // a split covers waves x keys_per_wave keys: whole 32-key blocks (4 waves
+    // above 16 rows), and whole 32-key steps of each of the 8 waves up to 16
+    const int kps_unit = p.M > 16 ? 8 : 32, waves = p.M > 16 ? 4 : 8;
     if (p.keys_per_wave < kps_unit || p.keys_per_wave % kps_unit) throw BackendError("attention: keys_per_wave");
-    if ((int64_t)p.nsplit * 4 * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
-    if ((int64_t)(p.nsplit - 1) * 4 * p.keys_per_wave >= (int64_t)p.P + p.M) throw BackendError("attention: empty split");
+    if ((int64_t)p.nsplit * waves * p.keys_per_wave < (int64_t)p.P + p.M) throw BackendError("attention: splits too few");
+    if ((int64_t)(p.nsplit - 1) * waves * p.keys_per_wave >= (int64_t)p.P + p.M)
+        throw BackendError("attention: empty split");
     if (p.cap % 32 || (int64_t)p.P + p.M > p.cap) throw BackendError("attention: cache capacity");
     if (p.mask_words < 1 || p.mask_words > 2 || p.M > 64 * p.mask_words) throw BackendError("attention: mask words");
     if (p.hd != 128 && p.hd != 64) throw BackendError("attention: head_dim must be 64 or 128");
-    const int nq = p.M * p.n_rep, nqt = (nq + 15) / 16;
+}
+
+AttnParams attn_small_params(const AttnParams &p) {
+    attn_check(p);
+    if (p.M > 16) throw BackendError("attention: more than 16 rows");
+    const int nqt = (p.M * p.n_rep + 15) / 16;
+    AttnParams a = p;
+    a.fused_combine = 0;
+    if (p.nsplit > 1 && p.split_cnt) {
+        if ((int64_t)p.n_kv * nqt > p.split_cnt_len) throw BackendError("attention: split counters too few");
+        a.fused_combine = p.nsplit <= kFusedMaxSplits;
+    }
+    return a;
+}
+
+int attn_small_workgroups(const AttnParams &p) { return p.n_kv * p.nsplit * ((p.M * p.n_rep + 15) / 16); }
+
+void launch_attn_combine(const AttnParams &p, hipStream_t st) {
+    if (p.nsplit <= 1) return;
+    if (p.nsplit > kCombMaxSplits) throw BackendError("attention: too many splits to combine");
+    const int rows = kCombThreads / (p.hd / 8);
+    const int64_t nrows = (int64_t)p.n_heads * p.M;
+    if ((int64_t)p.nsplit * nrows * p.hd * 2 >= 0x80000000LL) throw BackendError("attention: partials too large");
+    const dim3 grid((unsigned)((nrows + rows - 1) / rows)), block(kCombThreads);
+    if (p.nsplit <= 8) hipLaunchKernelGGL(k_attn_combine<8>, grid, block, 0, st, p);
+    else if (p.nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p);
+    else if (p.nsplit <= 24) hipLaunchKernelGGL(k_attn_combine<24>, grid, block, 0, st, p);
+    else if (p.nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, grid, block, 0, st, p);
+    else if (p.nsplit <= 40) hipLaunchKernelGGL(k_attn_combine<40>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(k_attn_combine<kCombMaxSplits>, grid, block, 0, st, p);
+}
+
+void launch_attention(const AttnParams &p, hipStream_t st) {
     if (p.M > 16) {
+        attn_check(p);
         // query blocks of kTWaves waves x kTQW tiles sharing each key block through LDS
+        const int nqt = (p.M * p.n_rep + 15) / 16;
         const dim3 grid(p.n_kv, p.nsplit, (nqt + kTWaves * kTQW - 1) / (kTWaves * kTQW));
         allow_attn_t_lds();
         if (p.hd == 128) hipLaunchKernelGGL(k_attn_t<128>, grid, dim3(kTThreads), attn_t_lds<128>(), st, p);
         else hipLaunchKernelGGL(k_attn_t<64>, grid, dim3(kTThreads), attn_t_lds<64>(), st, p);
-    } else {
-        AttnParams a = p;
-        a.fused_combine = 0;
-        if (p.nsplit > 1 && p.split_cnt) {
-            if ((int64_t)p.n_kv * nqt > p.split_cnt_len) throw BackendError("attention: split counters too few");
-            a.fused_combine = p.nsplit <= kFusedMaxSplits;
-        }
-        // One query tile per wave keeps a wave within 256 registers (two
-        // double-buffered 32-key operand sets and its accumulators), so two
-        // waves share each SIMD.  Query tiles become workgroups along z; with the
-        // KV head as blockIdx.x and n_kv a multiple of the 8 XCDs, every
-        // workgroup of one head lands on the same XCD, so the query tiles re-read
-        // that head's keys from its L2.
-        const dim3 grid(p.n_kv, p.nsplit, nqt);
-        if (p.hd == 128) hipLaunchKernelGGL((k_attn<128, 1>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_attn<64, 1>), grid, dim3(256), 0, st, a);
-        if (a.fused_combine) return;
+        launch_attn_combine(p, st);
+        return;
     }
-    if (p.nsplit > 1) {
-        if (p.nsplit > kCombMaxSplits) throw BackendError("attention: too many splits to combine");
-        const int rows = kCombThreads / (p.hd / 8);
-        const int64_t nrows = (int64_t)p.n_heads * p.M;
-        if ((int64_t)p.nsplit * nrows * p.hd * 2 >= 0x80000000LL) throw BackendError("attention: partials too large");
-        const dim3 grid((unsigned)((nrows + rows - 1) / rows)), block(kCombThreads);
-        if (p.nsplit <= 8) hipLaunchKernelGGL(k_attn_combine<8>, grid, block, 0, st, p);
-        else if (p.nsplit <= 16) hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p);
-        else if (p.nsplit <= 24) hipLaunchKernelGGL(k_attn_combine<24>, grid, block, 0, st, p);
-        else if (p.nsplit <= 32) hipLaunchKernelGGL(k_attn_combine<32>, grid, block, 0, st, p);
-        else if (p.nsplit <= 40) hipLaunchKernelGGL(k_attn_combine<40>, grid, block, 0, st, p);
-        else hipLaunchKernelGGL(k_attn_combine<kCombMaxSplits>, grid, block, 0, st, p);
-    }
+    const AttnParams a = attn_small_params(p);
+    // One query tile per wave keeps a wave within 256 registers (two
+    // double-buffered 32-key operand sets and its accumulators), so two waves
+    // share each SIMD.  Query tiles become workgroups along z; with the KV head
+    // as blockIdx.x and n_kv a multiple of the 8 XCDs, every workgroup of one
+    // head lands on the same XCD, so the query tiles re-read that head's keys
+    // from its L2.
+    const dim3 grid(p.n_kv, p.nsplit, (p.M * p.n_rep + 15) / 16);
+    if (p.hd == 128) hipLaunchKernelGGL(k_attn<128>, grid, dim3(kAttnThreads), 0, st, a);
+    else hipLaunchKernelGGL(k_attn<64>, grid, dim3(kAttnThreads), 0, st, a);
+    if (!a.fused_combine) launch_attn_combine(a, st);
 }
 
 }  // namespace sd

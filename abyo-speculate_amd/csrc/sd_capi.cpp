@@ -553,7 +553,7 @@ sd_status sd_synchronize(sd_model *m) {
     return guard([&] {
         need(m);
         setdev(m);
-        SD_HIP_CHECK(hipStreamSynchronize(m->model->st));
+        m->model->sync();
     });
 }
 
@@ -573,7 +573,7 @@ sd_status sd_read_kv_rows(sd_model *m, int32_t layer, int32_t which, int32_t hea
         // rows out of the blocked layout (sd_common.hpp: kv_k_off / kv_v_off)
         const int64_t b0 = (int64_t)pos0 / 32, b1 = ((int64_t)(pos0 + n) + 31) / 32;
         std::vector<uint16_t> blk((size_t)(b1 - b0) * 32 * c.head_dim);
-        SD_HIP_CHECK(hipStreamSynchronize(m->model->st));
+        m->model->sync();
         if (!blk.empty())
             SD_HIP_CHECK(hipMemcpy(blk.data(), base + b0 * 32 * c.head_dim, blk.size() * 2, hipMemcpyDeviceToHost));
         const int64_t off0 = b0 * 32 * c.head_dim;

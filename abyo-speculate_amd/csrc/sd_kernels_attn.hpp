@@ -62,5 +62,31 @@ struct AttnParams {
 
 void launch_rope_kv(const RopeKvParams &p, hipStream_t st);
 void launch_attention(const AttnParams &p, hipStream_t st);
+// Up to 16 rows: the checked parameters of the attention workgroups
+// (fused_combine set), how many of them a launch has, and the combine launch
+// that follows them when they do not merge the splits themselves (nothing
+// with one split).
+AttnParams attn_small_params(const AttnParams &p);
+int attn_small_workgroups(const AttnParams &p);
+void launch_attn_combine(const AttnParams &p, hipStream_t st);
+
+// ---- sd_qgemm.hip: the fused Q/K/V + attention launch (M <= 16) ----
+// The Q/K/V matmul with RoPE and the KV append in its epilogue (GemmParams g,
+// as launch_qgemm takes it) and the attention over the result (AttnParams a,
+// as launch_attention takes it) in one launch.  flags: nflags words, one per
+// matmul workgroup, that a launch sets to epoch (non-zero, different from the
+// previous launch's on these flags); status: host-visible memory that a launch
+// sets to 1 if its attention gave up waiting for the matmul (its outputs are
+// then undefined and the split counters must be cleared).  Launches sharing
+// these words must not overlap.  cus: the device's CU count.
+struct QkvAttnSync {
+    unsigned *flags;
+    int nflags;
+    unsigned epoch;
+    int *status;
+};
+bool qkv_attention_fits(const GemmParams &g, const AttnParams &a, int cus);
+void launch_qkv_attention(const GemmParams &g, const AttnParams &a, const QkvAttnSync &sy, int cus, hipStream_t st,
+                          const LaunchTiming &tm = LaunchTiming{});
 
 }  // namespace sd

@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "sd_common.hpp"
@@ -79,8 +80,9 @@ Model::~Model() {
                     (void *)acc_m, (void *)acc_s, (void *)acc_q, (void *)acc_am, (void *)acc_tree,
                     (void *)acc_out, (void *)t2d_inv, (void *)qg_part, (void *)aux_h, (void *)aux_x, (void *)aux_y,
                     (void *)aux_ids, (void *)ssq, (void *)split_cnt, (void *)acc_part, (void *)acc_cnt,
-                    (void *)acc_prob, (void *)acc_lin})
+                    (void *)acc_prob, (void *)acc_lin, (void *)qa_flags})
         F(p);
+    if (qa_status) hipHostFree(qa_status);
     if (h_stage) hipHostFree(h_stage);
     if (acc_stage) hipHostFree(acc_stage);
     if (stage_ev) hipEventDestroy(stage_ev);
@@ -123,6 +125,13 @@ void Model::alloc_buffers() {
     part_o = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * c.head_dim);
     part_ml = dalloc<float>((size_t)nsplit_max * c.n_heads * Mx * 2);
     split_cnt = dalloc<int>(c.n_heads);  // n_kv x (query tiles <= n_rep up to 16 rows), zero
+    qa_flags = dalloc<unsigned>(kQaFlags);
+    SD_HIP_CHECK(hipHostMalloc((void **)&qa_status, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
+    *(volatile int *)qa_status = 0;
+    SD_HIP_CHECK(hipHostGetDevicePointer((void **)&qa_status_dev, qa_status, 0));
+    SD_HIP_CHECK(hipDeviceGetAttribute(&n_cus, hipDeviceAttributeMultiprocessorCount, c.device));
+    const char *unfused = std::getenv("SD_ATTN_UNFUSED");
+    fused_qkv_attn = !(unfused && unfused[0] == '1');
     logits = dalloc<float>((size_t)Mx * c.vocab);
     hidden_out = dalloc<float>((size_t)Mx * c.hidden);
     last_row = dalloc<float>((size_t)c.vocab);
@@ -163,6 +172,21 @@ void Model::alloc_buffers() {
 }
 
 void Model::stage_wait() { SD_HIP_CHECK(hipEventSynchronize(stage_ev)); }
+
+void Model::check_status() {
+    if (*(volatile int *)qa_status == 0) return;
+    // the launch's outputs are undefined and its counters may be left mid-count
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+    SD_HIP_CHECK(hipMemsetAsync(split_cnt, 0, (size_t)cfg.n_heads * sizeof(int), st));
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+    *(volatile int *)qa_status = 0;
+    throw BackendError("fused Q/K/V + attention launch: the attention gave up waiting for the matmul");
+}
+
+void Model::sync() {
+    SD_HIP_CHECK(hipStreamSynchronize(st));
+    check_status();
+}
 void Model::stage_done() { SD_HIP_CHECK(hipEventRecord(stage_ev, st)); }
 
 bool Model::weights_ready() const {
@@ -560,6 +584,7 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     if (P + M > c.ctx_len) throw ArgError("forward: KV capacity exceeded");
     if (mask_words < 1 || mask_words > 2) throw ArgError("forward: mask words");
     SD_HIP_CHECK(hipSetDevice(c.device));
+    check_status();  // a fused launch of an earlier forward that gave up
     // stage ids | pos | mask in pinned memory with the device block's layout,
     // then one H2D copy
     stage_wait();
@@ -594,6 +619,13 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     // the RoPE finaliser) scales by 1/rms
     const bool spread = !fused && M > 16 && M <= 64;
     const int sp_parts = resid_u_parts(H);
+    // K and V rows read once per layer by the attention: [0, P + M) of every KV head
+    const double kv_bytes = 2.0 * c.n_kv_heads * (double)(P + M) * c.head_dim * 2.0;
+    // up to 16 rows, with the epilogues fused, the attention's workgroups join
+    // the Q/K/V launch where its shape allows (qkv_attention_fits)
+    auto qa_fits = [&](const GemmParams &g, const AttnParams &at) {
+        return fused && fused_qkv_attn && qkv_attention_fits(g, at, n_cus);
+    };
     for (int l = 0; l < c.n_layers; l++) {
         auto &L = lw[l];
         if (spread)
@@ -601,6 +633,29 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
         else if (!fused)
             launch_rmsnorm(h, (const float *)L[K_ATTN_NORM].d, M, H, c.rms_eps, xp, xp_ld, nullptr, st, qg_part, pend);
         int nks_qkv;
+        bool qa_launched = false;
+        AttnParams a{};
+        a.q16 = q16;
+        a.kc = kc(l);
+        a.vc = vc(l);
+        a.cap = cap;
+        a.mask = d_mask;
+        a.mask_words = mask_words;
+        a.P = P;
+        a.M = M;
+        a.n_heads = c.n_heads;
+        a.n_kv = c.n_kv_heads;
+        a.n_rep = c.n_heads / c.n_kv_heads;
+        a.hd = c.head_dim;
+        a.keys_per_wave = split.keys_per_wave;
+        a.nsplit = split.nsplit;
+        a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+        a.part_o = part_o;
+        a.part_ml = part_ml;
+        a.split_cnt = split_cnt;
+        a.split_cnt_len = c.n_heads;
+        a.out16 = ap;
+        a.out_ld = ap_ld;
         {
             GemmParams p{};
             gemm_workspace(p);
@@ -642,8 +697,25 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 R.hd = c.head_dim;
                 R.interleaved = c.arch == 0;
             }
-            run_gemm(p, PC_QKV, wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]));
-            nks_qkv = qgemm_slices(p);
+            const double wqkv = wbytes(L[K_ATTN_Q]) + wbytes(L[K_ATTN_K]) + wbytes(L[K_ATTN_V]);
+            if (qa_fits(p, a)) {
+                // the attention's workgroups ride in the Q/K/V launch
+                nks_qkv = 1;
+                qa_launched = true;
+                // a launch number per launch, never 0 (the flags' initial value)
+                if (++qa_epoch == 0) ++qa_epoch;
+                const QkvAttnSync sy{qa_flags, kQaFlags, qa_epoch, qa_status_dev};
+                if (prof_on) {
+                    const int ev = prof_events();
+                    launch_qkv_attention(p, a, sy, n_cus, st, LaunchTiming{ev_pool[ev], ev_pool[ev + 1]});
+                    prof.push_back(ProfEntry{PC_QKV_ATTN, gemm_bytes(p, wqkv) + kv_bytes, ev});
+                } else {
+                    launch_qkv_attention(p, a, sy, n_cus, st);
+                }
+            } else {
+                run_gemm(p, PC_QKV, wqkv);
+                nks_qkv = qgemm_slices(p);
+            }
         }
         {
             RopeKvParams r{};
@@ -676,36 +748,14 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 r.norm_eps = c.rms_eps;
             }
             if (!fused) launch_rope_kv(r, st);
-            AttnParams a{};
-            a.q16 = q16;
-            a.kc = kc(l);
-            a.vc = vc(l);
-            a.cap = cap;
-            a.mask = d_mask;
-            a.mask_words = mask_words;
-            a.P = P;
-            a.M = M;
-            a.n_heads = c.n_heads;
-            a.n_kv = c.n_kv_heads;
-            a.n_rep = c.n_heads / c.n_kv_heads;
-            a.hd = c.head_dim;
-            a.keys_per_wave = split.keys_per_wave;
-            a.nsplit = split.nsplit;
-            a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
-            a.part_o = part_o;
-            a.part_ml = part_ml;
-            a.split_cnt = split_cnt;
-            a.split_cnt_len = c.n_heads;
-            a.out16 = ap;
-            a.out_ld = ap_ld;
-            if (prof_on) {
-                // K and V rows read once per layer: [0, P + M) of every KV head
-                const double kvb = 2.0 * c.n_kv_heads * (double)(P + M) * c.head_dim * 2.0;
-                const int ev = prof_begin();
-                launch_attention(a, st);
-                prof_end(ev, PC_ATTN, kvb);
-            } else {
-                launch_attention(a, st);
+            if (!qa_launched) {
+                if (prof_on) {
+                    const int ev = prof_begin();
+                    launch_attention(a, st);
+                    prof_end(ev, PC_ATTN, kv_bytes);
+                } else {
+                    launch_attention(a, st);
+                }
             }
         }
         {
@@ -851,7 +901,7 @@ void Model::lm_head_rows(const float *hidden_host, int rows, float *out_host) {
         launch_qgemm(p, st);
         SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.vocab, aux_y, (size_t)n * c.vocab * 4,
                                     hipMemcpyDeviceToHost, st));
-        SD_HIP_CHECK(hipStreamSynchronize(st));
+        sync();
     }
 }
 
@@ -880,7 +930,7 @@ void Model::embed_rows(const int *ids, int n, float *out_host) {
         launch_embed(gw[K_TOK_EMBD].fmt, embed_table(), c.hidden, aux_ids, k, aux_h, st);
         SD_HIP_CHECK(hipMemcpyAsync(out_host + (size_t)r0 * c.hidden, aux_h, (size_t)k * c.hidden * 4,
                                     hipMemcpyDeviceToHost, st));
-        SD_HIP_CHECK(hipStreamSynchronize(st));
+        sync();
     }
 }
 
@@ -1030,7 +1080,7 @@ void Decoder::observe(const uint32_t *ids, size_t n) {
         collect_hist = history.size();
         collect_fwd = model->fwd_count;
     }
-    SD_HIP_CHECK(hipStreamSynchronize(model->st));
+    model->sync();
 }
 
 void Decoder::next_logits(float *out) {
@@ -1042,7 +1092,7 @@ void Decoder::next_logits(float *out) {
         forward_advance(&last, 1, false);
     }
     if (out) SD_HIP_CHECK(hipMemcpyAsync(out, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
 }
 
 void Decoder::batched_logits(const uint32_t *drafts, size_t k, float *out) {
@@ -1067,7 +1117,7 @@ void Decoder::batched_logits(const uint32_t *drafts, size_t k, float *out) {
     history.insert(history.end(), drafts, drafts + k);
     if (out) {
         SD_HIP_CHECK(hipMemcpyAsync(out, m.logits, (k + 1) * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
-        SD_HIP_CHECK(hipStreamSynchronize(m.st));
+        m.sync();
     }
     // without `out` the rows stay on the device for the caller's own kernels,
     // queued behind the forward on the same stream (the device-acceptance
@@ -1118,7 +1168,7 @@ void Decoder::tree_logits_keep_kv(const uint32_t *tokens, const uint32_t *parent
     if (out_hidden)
         SD_HIP_CHECK(
             hipMemcpyAsync(out_hidden, m.hidden_out, n * (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
 }
 
 void Decoder::tree_logits(const uint32_t *tokens, const uint32_t *parents, size_t n, float *out_logits) {
@@ -1129,14 +1179,14 @@ void Decoder::tree_logits(const uint32_t *tokens, const uint32_t *parents, size_
     tree_forward(tokens, parents, n, false, prefix);
     if (out_logits)
         SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.logits, n * (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
     truncate(prefix);
     forward_advance(&last, 1, false);  // restores the cache and the cached next-token row
     // Llama replaces row 0 by the one-token pass's row (quantized_llama.rs:306-322); Qwen2 discards that
     // row and keeps the tree pass's row 0 (quantized_qwen2.rs:227-234).
     if (out_logits && m.cfg.arch == 0)
         SD_HIP_CHECK(hipMemcpyAsync(out_logits, m.last_row, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
 }
 
 void Decoder::commit_tree_path(const uint32_t *tokens, const uint32_t *parents, size_t n, const uint32_t *acc,
@@ -1160,7 +1210,7 @@ void Decoder::commit_tree_path(const uint32_t *tokens, const uint32_t *parents, 
         cache_len = prefix + (int)n_acc;
     }
     for (size_t j = 1; j < n_acc; j++) history.push_back(t.tokens[acc[j]]);
-    SD_HIP_CHECK(hipStreamSynchronize(model->st));
+    model->sync();
 }
 
 void Decoder::last_hidden_state(float *out) {
@@ -1173,7 +1223,7 @@ void Decoder::last_hidden_state(float *out) {
     m.forward(&id, &pos, &mk, 1, 1, cache_len, 0, true, {}, nullptr);
     cache_len += 1;
     if (out) SD_HIP_CHECK(hipMemcpyAsync(out, m.hidden_out, (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
 }
 
 void Decoder::observe_returning_last_hidden(const uint32_t *ids, size_t n, float *out) {
@@ -1202,7 +1252,7 @@ void Decoder::observe_returning_last_hidden(const uint32_t *ids, size_t n, float
     if (out)
         SD_HIP_CHECK(hipMemcpyAsync(out, m.hidden_out + (size_t)(lastM - 1) * m.cfg.hidden, (size_t)m.cfg.hidden * 4,
                                     hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
 }
 
 void Decoder::last_hidden_states_multi(const uint32_t *layers, size_t nl, float *out_final, float *out_layers) {
@@ -1228,7 +1278,7 @@ void Decoder::last_hidden_states_multi(const uint32_t *layers, size_t nl, float 
     collect_fwd = m.fwd_count;
     if (out_final)
         SD_HIP_CHECK(hipMemcpyAsync(out_final, m.hidden_out, (size_t)m.cfg.hidden * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
     if (out_layers) std::memcpy(out_layers, tmp.data(), tmp.size() * 4);
 }
 
@@ -1272,7 +1322,7 @@ void Decoder::argmax_rows(int32_t *out, size_t n) {
     // staging buffer first)
     int *pin = m.acc_stage + (size_t)kAccTreeInts * m.cfg.max_batch;
     SD_HIP_CHECK(hipMemcpyAsync(pin, m.argmax, n * 4, hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
     std::memcpy(out, pin, n * 4);
 }
 
@@ -1313,7 +1363,7 @@ void Decoder::verify_greedy_tree(const uint32_t *tokens, const uint32_t *parents
         launch_argmax_rows(m.last_row, m.cfg.vocab, m.cfg.vocab, 1, m.argmax, m.st);
         int *pin = m.acc_stage + (size_t)kAccTreeInts * m.cfg.max_batch;  // pinned (see argmax_rows)
         SD_HIP_CHECK(hipMemcpyAsync(pin, m.argmax, 4, hipMemcpyDeviceToHost, m.st));
-        SD_HIP_CHECK(hipStreamSynchronize(m.st));
+        m.sync();
         root_am = pin[0];
     }
     tree_logits_keep_kv(tokens, parents, n, nullptr, nullptr);
@@ -1385,7 +1435,7 @@ void Decoder::set_d2t(const int64_t *d2t, size_t n) {
     SD_HIP_CHECK(hipSetDevice(m.cfg.device));
     if (!m.t2d_inv) SD_HIP_CHECK(hipMalloc((void **)&m.t2d_inv, (size_t)m.cfg.vocab * sizeof(int) + 256));
     SD_HIP_CHECK(hipMemcpyAsync(m.t2d_inv, inv.data(), inv.size() * sizeof(int), hipMemcpyHostToDevice, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
     d2t_host.assign(d2t, d2t + n);
     t2d_host = std::move(inv);
     m.d2t_draft_vocab = (int)n;
@@ -1525,7 +1575,7 @@ void Decoder::accept_walk(const int *parents, const int *tokens, int n, const fl
     launch_accept_walk(a, m.st);
     int *out = m.acc_stage + (size_t)kAccTreeInts * c.max_batch;
     SD_HIP_CHECK(hipMemcpyAsync(out, m.acc_out, ((size_t)n + 4) * sizeof(int), hipMemcpyDeviceToHost, m.st));
-    SD_HIP_CHECK(hipStreamSynchronize(m.st));
+    m.sync();
     const int status = out[3];
     if (status == ACC_ERR_SOFTMAX) throw SamplingError("softmax produced a non-positive or non-finite sum");
     if (status == ACC_ERR_ADJUSTED) throw SamplingError("adjusted distribution has non-positive mass");

@@ -70,8 +70,11 @@ struct DevTensor {
 
 // Per-kernel-class timing collected with HIP events on the model's stream.
 // Classes: 0 qkv, 1 wo, 2 gate_up, 3 down, 4 lm_head (the dequant-matmul
-// launches) and 5 attn (split attention + combine of one layer).
-enum ProfClass : int { PC_QKV = 0, PC_WO = 1, PC_GATE_UP = 2, PC_DOWN = 3, PC_LM_HEAD = 4, PC_ATTN = 5 };
+// launches), 5 attn (split attention + combine of one layer) and 6 qkv_attn
+// (the fused Q/K/V + attention launch of one layer, M <= 16).
+enum ProfClass : int {
+    PC_QKV = 0, PC_WO = 1, PC_GATE_UP = 2, PC_DOWN = 3, PC_LM_HEAD = 4, PC_ATTN = 5, PC_QKV_ATTN = 6
+};
 struct ProfEntry {
     int cls;
     double bytes;  // algorithmic bytes of the launch
@@ -143,6 +146,22 @@ class Model {
     int collect_cap = 0;     // rows of collect_buf
     uint64_t fwd_count = 0;  // forwards, weight and cache writes so far (the collected rows' validity stamp)
     int *split_cnt = nullptr;  // attention's per-tile split arrival counts (zero between launches)
+    // The fused Q/K/V + attention launch (M <= 16, where it fits): a flag per
+    // matmul workgroup, the number of the last launch (the value its flags
+    // were set to) and the pinned, device-mapped word a launch sets when its
+    // attention gave up waiting for the matmul.  fused_qkv_attn: take the
+    // fused launch where it fits (the environment variable SD_ATTN_UNFUSED=1
+    // at creation turns it off, for comparisons).
+    static constexpr int kQaFlags = 4096;
+    unsigned *qa_flags = nullptr;
+    unsigned qa_epoch = 0;
+    int *qa_status = nullptr, *qa_status_dev = nullptr;
+    int n_cus = 0;
+    bool fused_qkv_attn = true;
+    // waits for the stream, then fails (clearing the synchronisation words) if
+    // a fused launch gave up
+    void sync();
+    void check_status();
     int *amax_i = nullptr, *argmax = nullptr, *d_ids = nullptr, *d_pos = nullptr, *d_src = nullptr;
     uint64_t *d_mask = nullptr;
     // split-K partial sums of the M > 16 matmul (see GemmParams::allow_split)

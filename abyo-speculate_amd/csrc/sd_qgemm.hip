@@ -33,9 +33,11 @@
 // m16) where s16 = fp16(d * sc) and m16 = fp16(dmin * m).
 #include <hip/hip_ext.h>
 
+#include "sd_attn_dev.hpp"
 #include "sd_buffer.hpp"
 #include "sd_common.hpp"
 #include "sd_kernels.hpp"
+#include "sd_kernels_attn.hpp"
 #include "sd_qcodes.hpp"
 
 namespace sd {
@@ -309,8 +311,11 @@ __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)
 // writes the tiles' argmax partial of every token (first max wins) to `slot`.
 // --------------------------------------------------------------------------
 // four fp16 values to one 8-byte store
-__device__ __forceinline__ void st4h(uint16_t *dst, float a, float b, float c, float d) {
-    *(uintx2 *)dst = uintx2{(uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16), (uint32_t)f2h(c) | ((uint32_t)f2h(d) << 16)};
+// DEV: a device-scope store (read by other workgroups of the same launch)
+template <bool DEV = false> __device__ __forceinline__ void st4h(uint16_t *dst, float a, float b, float c, float d) {
+    const uintx2 v{(uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16), (uint32_t)f2h(c) | ((uint32_t)f2h(d) << 16)};
+    if constexpr (DEV) st_dev64(dst, (uint64_t)v.x | ((uint64_t)v.y << 32));
+    else *(uintx2 *)dst = v;
 }
 
 // Operands the epilogue reads besides the accumulators, requested when the
@@ -382,7 +387,8 @@ __device__ __forceinline__ void epi_prefetch_rope(const GemmParams &p, const Gem
 // LayerWeights::rope_at_positions (quantized_llama_local.rs:94-105,
 // quantized_qwen2_local.rs:98-109): (x0 c - x1 s, x0 s + x1 c) on the pairs
 // (2i, 2i+1) inside a tile (rope_i) or (i, i + hd/2) across the two (rope).
-template <int RT>
+// DEV: device-scope stores, for the attention workgroups of the same launch.
+template <int RT, bool DEV>
 __device__ __forceinline__ void rope_epilogue(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
                                               const floatx4 (&v)[RT], const EpiPre<RT> &e, int m, int g) {
     if constexpr (RT == 2) {
@@ -422,24 +428,28 @@ __device__ __forceinline__ void rope_epilogue(const GemmParams &p, const GemmSeg
                 const int dd = L.d + rt * half;
                 uint16_t *dst = L.which == 0 ? R.q16 + ((int64_t)L.head * p.M + m) * hd + dd
                                              : R.kc + (int64_t)L.head * R.cap * hd + kv_k_off(t, dd, hd);
-                st4h(dst, y[rt][0], y[rt][1], y[rt][2], y[rt][3]);
+                st4h<DEV>(dst, y[rt][0], y[rt][1], y[rt][2], y[rt][3]);
             }
         } else {
             uint16_t *vs = R.vc + (int64_t)L.head * R.cap * hd;
 #pragma unroll
             for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) vs[kv_v_off(t, L.d + rt * half + i, hd)] = f2h(x[rt][i]);
+                for (int i = 0; i < 4; i++) {
+                    uint16_t *dst = vs + kv_v_off(t, L.d + rt * half + i, hd);
+                    if constexpr (DEV) st_dev16(dst, f2h(x[rt][i]));
+                    else *dst = f2h(x[rt][i]);
+                }
         }
     }
 }
 
-template <int RT>
+template <int RT, bool DEV = false>
 __device__ __forceinline__ void epilogue(const GemmParams &p, const GemmSeg (&S)[RT], const int (&rloc)[RT],
                                          const floatx4 (&v)[RT], const EpiPre<RT> &e, int m, int g, int slot) {
     const bool live = m < p.M;
     if (p.rope.q16) {
-        if (live) rope_epilogue<RT>(p, S, rloc, v, e, m, g);
+        if (live) rope_epilogue<RT, DEV>(p, S, rloc, v, e, m, g);
         return;
     }
     if (p.mode == GM_SWIGLU) {
@@ -757,16 +767,18 @@ __device__ __forceinline__ void qmm_body(const GemmParams &p, const WRow (&row)[
     int_drain<RT>(cy, acc);
 }
 
-template <int RT, int KW, int XL>
-__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
-    warm_kernargs<sizeof(GemmParams)>();
+// One workgroup (index wg) of the M <= 16 launch.  DONE (the fused Q/K/V +
+// attention launch): the epilogue's stores are made at device scope and, once
+// they are complete, the workgroup writes epoch to flags[wg].
+template <int RT, int KW, int XL, bool DONE = false>
+__device__ __forceinline__ void qmm_wg(const GemmParams &p, int wg, unsigned *flags = nullptr, unsigned epoch = 0) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     GemmSeg S[RT];
     int rloc[RT];
     if (p.mode == GM_SWIGLU) {
         // feature tiles f0 .. f0 + RT/2 - 1: their gate tiles, then their up tiles
-        const int f0 = (int)blockIdx.x * (RT / 2);
+        const int f0 = wg * (RT / 2);
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             S[rt] = rt < RT / 2 ? p.seg[0] : p.seg[1];
@@ -777,10 +789,10 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
         // RT).  With RoPE in the epilogue (RT == 2) the pair is instead tiles j
         // and j + hd/32 of one head, so the lane holding element d of a head
         // also holds d + hd/2, the partner of the half rotation.
-        int t0 = (int)blockIdx.x * RT, tstep = 1;
+        int t0 = wg * RT, tstep = 1;
         if (RT == 2 && p.rope.q16) {
             const int half = p.rope.hd / 32;
-            t0 = ((int)blockIdx.x / half) * 2 * half + (int)blockIdx.x % half;
+            t0 = (wg / half) * 2 * half + wg % half;
             tstep = half;
         }
         const GemmSeg s = seg_of_tile(p, t0);
@@ -856,7 +868,53 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) v[rt] *= inv;
     }
-    epilogue<RT>(p, S, rloc, v, e, r16, g, (int)blockIdx.x);
+    if constexpr (!DONE) {
+        epilogue<RT>(p, S, rloc, v, e, r16, g, wg);
+        return;
+    }
+    epilogue<RT, true>(p, S, rloc, v, e, r16, g, wg);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_store(flags + wg, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int RT, int KW, int XL>
+__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(2))) void k_qmm(GemmParams p) {
+    warm_kernargs<sizeof(GemmParams)>();
+    qmm_wg<RT, KW, XL>(kernarg<GemmParams>(), blockIdx.x);
+}
+
+// ---- the fused Q/K/V + attention launch (M <= 16) ----
+// Workgroups [0, nprod) are the Q/K/V matmul's (k_qmm<2, 8, XL>, RoPE and the
+// KV append in the epilogue, stored at device scope), the rest the
+// attention's (attn_wg): those request their first cached keys at once, wait
+// until the Q/K/V workgroups of their KV head's rows have flagged them stored
+// (attn_wait), then read the queries and the new rows.  The attention's
+// launch, argument fetch and first cache reads so overlap the matmul instead
+// of following it.  Progress: a workgroup of either kind fills a CU (two waves
+// per SIMD), the launch has no more workgroups than CUs (qkv_attention_fits),
+// and the Q/K/V workgroups never wait.
+struct QkvAttnArgs {
+    GemmParams g;
+    AttnWait w;
+    int nprod;
+    AttnParams a;
+};
+
+template <int HD, int XL>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_attn(QkvAttnArgs) {
+    warm_kernargs<sizeof(QkvAttnArgs)>();
+    const GemmParams &g = kernarg<GemmParams, offsetof(QkvAttnArgs, g)>();
+    const AttnWait &w = kernarg<AttnWait, offsetof(QkvAttnArgs, w)>();
+    const int nprod = kernarg<int, offsetof(QkvAttnArgs, nprod)>();
+    const AttnParams &a = kernarg<AttnParams, offsetof(QkvAttnArgs, a)>();
+    if ((int)blockIdx.x < nprod) {
+        qmm_wg<2, 8, XL, true>(g, blockIdx.x, w.flags, w.epoch);
+        return;
+    }
+    // KV head fastest: with n_kv a multiple of the 8 XCDs every workgroup of a
+    // head shares one XCD's L2
+    const int i = (int)blockIdx.x - nprod, h = i % a.n_kv, r = i / a.n_kv;
+    attn_wg<HD, true>(a, h, r % a.nsplit, r / a.nsplit, w);
 }
 
 // ==========================================================================
@@ -1194,7 +1252,7 @@ static bool launch_kw(const GemmParams &p, int kw, int nwg, hipStream_t st, cons
     }
 }
 
-int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
+static void qgemm_check(const GemmParams &p) {
     if (p.M < 1 || p.M > 128) throw BackendError("qgemm: M out of range");
     if (p.K % 256) throw BackendError("qgemm: K must be a multiple of 256");
     if (p.mode == GM_SWIGLU && (p.nseg != 2 || p.seg[0].rows != p.seg[1].rows || p.seg[0].fmt != p.seg[1].fmt))
@@ -1221,6 +1279,47 @@ int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
             throw BackendError("qgemm: RoPE column layout");
         if (R.cap % 32 || (int64_t)R.P + p.M > R.cap) throw BackendError("qgemm: RoPE cache capacity");
     }
+}
+
+bool qkv_attention_fits(const GemmParams &g, const AttnParams &a, int cus) {
+    if (g.M > 16 || !g.rope.q16 || g.mode != GM_STORE || qgemm_rt(g) != 2 || qgemm_kw(g) != 8) return false;
+    if (a.M != g.M || (a.hd != 64 && a.hd != 128)) return false;
+    // the producer of head j's columns is workgroup range [j hd/32, (j+1) hd/32)
+    if (qgemm_workgroups(g) * 32 != (a.n_heads + 2 * a.n_kv) * a.hd) return false;
+    const bool merged = a.nsplit == 1 || (a.split_cnt && a.nsplit <= kFusedMaxSplits);
+    // every workgroup of the launch on a CU of its own: attention workgroups
+    // that wait on CUs the matmul would use made the Qwen2.5-7B-shaped M = 9
+    // step slower than the two launches (measured 2700 against 2656 us)
+    return merged && qgemm_workgroups(g) + attn_small_workgroups(a) <= cus;
+}
+
+void launch_qkv_attention(const GemmParams &g, const AttnParams &a, const QkvAttnSync &sy, int cus, hipStream_t st,
+                          const LaunchTiming &tm) {
+    qgemm_check(g);
+    if (!qkv_attention_fits(g, a, cus)) throw BackendError("qkv_attention: shape does not fit the fused launch");
+    if (!sy.flags || !sy.status || sy.epoch == 0) throw BackendError("qkv_attention: synchronisation words missing");
+    QkvAttnArgs p;
+    p.g = g;
+    p.a = attn_small_params(a);
+    p.nprod = qgemm_workgroups(g);
+    if (p.nprod > sy.nflags) throw BackendError("qkv_attention: too few producer flags");
+    p.w.flags = sy.flags;
+    p.w.epoch = sy.epoch;
+    p.w.status = sy.status;
+    const dim3 grid(p.nprod + attn_small_workgroups(p.a)), block(kAttnThreads);
+    if (a.hd == 128) {
+        if (g.M <= 4) launch_timed(k_qkv_attn<128, 2>, grid, block, 0, st, tm, p);
+        else if (g.M <= 8) launch_timed(k_qkv_attn<128, 4>, grid, block, 0, st, tm, p);
+        else launch_timed(k_qkv_attn<128, 8>, grid, block, 0, st, tm, p);
+    } else {
+        if (g.M <= 4) launch_timed(k_qkv_attn<64, 2>, grid, block, 0, st, tm, p);
+        else if (g.M <= 8) launch_timed(k_qkv_attn<64, 4>, grid, block, 0, st, tm, p);
+        else launch_timed(k_qkv_attn<64, 8>, grid, block, 0, st, tm, p);
+    }
+}
+
+int launch_qgemm(const GemmParams &p, hipStream_t st, const LaunchTiming &tm) {
+    qgemm_check(p);
     const int ct = token_tiles(p.M);
     if (ct > 1) {
         if (qgemm_slices(p) > 1 && !p.part) throw BackendError("qgemm: split-K workspace missing");

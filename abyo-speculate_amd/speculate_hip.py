@@ -32,7 +32,7 @@ F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
  ATTN_NORM, FFN_NORM, ATTN_Q_BIAS, ATTN_K_BIAS, ATTN_V_BIAS) = range(15)
 ARCH_LLAMA, ARCH_QWEN2 = 0, 1
 MIX_Q4_K, MIX_Q4_K_M, MIX_Q5K_Q80, MIX_Q6_K, MIX_Q5_K, MIX_Q8_0 = range(6)
-PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head", "attn")
+PROFILE_CLASSES = ("qkv", "wo", "gate_up", "down", "lm_head", "attn", "qkv_attn")
 BENCH_QKV, BENCH_GATE_UP, BENCH_ALL_LAYERS = 100, 101, -2
 
 

@@ -150,7 +150,7 @@ def leg_summary(t, prof, tokens_per_step, extra):
 
 def summarize(prof):
     out = {}
-    for cls in ("qkv", "wo", "gate_up", "down", "lm_head", "attn"):
+    for cls in ("qkv", "wo", "gate_up", "down", "lm_head", "attn", "qkv_attn"):
         es = [e for e in prof if e[0] == cls]
         if not es:
             continue
@@ -260,7 +260,10 @@ def main():
     per_launch_bytes = gb / len(gem)
     avg_launch_s = gt / len(gem)
     achieved = per_launch_bytes / avg_launch_s / 1e9
-    step_bytes = gb / args.steps + sum(e[1] for e in prof if e[0] == "attn") / args.steps
+    # every profiled launch: the K1 matmuls, and the attention alone or fused
+    # with the Q/K/V matmul (qkv_attn: its weights, activations, outputs and
+    # cache rows)
+    step_bytes = sum(e[1] for e in prof) / args.steps
     log(f"K1 dequant-matmul: {achieved:.0f} GB/s over {len(gem)} launches")
     traffic, traffic_src = measured_traffic("m5")
 
@@ -279,7 +282,9 @@ def main():
         "step_algorithmic_bytes": int(step_bytes),
         "kernels": summarize(prof),
         "roofline": {"bound": "hbm",
-                     "kernel": "k_qmm (K1 fused dequant-matmul for M<=16, all 129 launches of a step)",
+                     "kernel": f"k_qmm (K1 fused dequant-matmul for M<=16: the {len(gem) // args.steps} matmul-only "
+                               "launches of a step; the Q/K/V matmul runs inside the fused Q/K/V + attention "
+                               "launch, kernels.qkv_attn)",
                      "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
