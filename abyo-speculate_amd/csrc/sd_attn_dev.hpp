@@ -569,8 +569,7 @@ __device__ __forceinline__ void attn_wg(const AttnParams &p, int h, int s, int q
     S.l[0] = xsum4(S.l[0]);  // the query's 4 partial sums
 
     // ---- merge the 8 waves: rescale to the common max, then
-    // ((o0 + o4) + (o2 + o6)) + ((o1 + o5) + (o3 + o7)) through LDS (the
-    // staged blocks' last reads precede the first barrier) ----
+    // ((o0 + o4) + (o2 + o6)) + ((o1 + o5) + (o3 + o7)) through LDS ----
     if (g == 0) {
         sml[wave][r16][0] = S.m[0];
         sml[wave][r16][1] = S.l[0];
@@ -589,18 +588,24 @@ __device__ __forceinline__ void attn_wg(const AttnParams &p, int h, int s, int q
     }
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) S.o[0][dt] *= fme;
+    // s_w = o_w + o_(w+4) on waves 0..3 (a wave reads, then rewrites, only its
+    // own slot), then wave 0 forms (s0 + s2) + (s1 + s3)
+    if (wave >= 4) {
 #pragma unroll
-    for (int lvl = 4; lvl >= 1; lvl >>= 1) {
-        if (wave >= lvl && wave < 2 * lvl) {
+        for (int dt = 0; dt < NDT; dt++) sob[wave - 4][dt][lane] = S.o[0][dt];
+    }
+    __syncthreads();
+    if (wave < 4) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) sob[wave - lvl][dt][lane] = S.o[0][dt];
+        for (int dt = 0; dt < NDT; dt++) {
+            S.o[0][dt] += sob[wave][dt][lane];
+            if (wave > 0) sob[wave][dt][lane] = S.o[0][dt];
         }
-        __syncthreads();
-        if (wave < lvl) {
+    }
+    __syncthreads();
+    if (wave == 0) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) S.o[0][dt] += sob[wave][dt][lane];
-        }
-        if (lvl > 1) __syncthreads();
+        for (int dt = 0; dt < NDT; dt++) S.o[0][dt] = (S.o[0][dt] + sob[2][dt][lane]) + (sob[1][dt][lane] + sob[3][dt][lane]);
     }
     const bool fused = p.fused_combine != 0;
     const int q = qg * 16 + r16;
