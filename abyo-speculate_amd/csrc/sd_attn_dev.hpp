@@ -446,14 +446,16 @@ constexpr int kAttnThreads = 512;
 // waits for the producers of its rows only: q heads h n_rep .. (h + 1) n_rep - 1,
 // k head h and v head h.  A flag per producer (distinct words, plain stores)
 // instead of one shared counter: device-scope atomics on one word from a few
-// hundred workgroups queue for microseconds.  A wait that exceeds kWaitPolls
-// device-scope reads (about a second) gives up: the workgroup writes nothing
-// and sets *status (host-visible memory), which the host checks after the
-// step.
+// hundred workgroups queue for microseconds.  A wait that exceeds `polls`
+// device-scope reads (kWaitPolls: about a second) gives up: the workgroup
+// writes nothing and sets *status (host-visible memory), which the host
+// checks after the step.  The attention waits for `want`, which is epoch
+// except under fault injection (a number no producer writes).
 struct AttnWait {
     unsigned *flags;
-    unsigned epoch;
+    unsigned epoch, want;
     int *status;
+    int polls;
 };
 constexpr int kWaitPolls = 1 << 21;
 
@@ -466,13 +468,13 @@ __device__ __forceinline__ bool attn_wait(const AttnWait &w, const AttnParams &p
         constexpr int WPH = HD / 32;  // producer workgroups per head
         const int lane = threadIdx.x, nqw = WPH * p.n_rep, cnt = WPH * (p.n_rep + 2);
         bool ok = false;
-        for (int it = 0; it < kWaitPolls; it++) {
+        for (int it = 0; it < w.polls; it++) {
             bool all = true;
             for (int i = lane; i < cnt; i += 64) {
                 const int j = i < nqw ? WPH * h * p.n_rep + i
                             : i < nqw + WPH ? WPH * (p.n_heads + h) + (i - nqw)
                                             : WPH * (p.n_heads + p.n_kv + h) + (i - nqw - WPH);
-                all = all && __hip_atomic_load(w.flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == w.epoch;
+                all = all && __hip_atomic_load(w.flags + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == w.want;
             }
             if (__builtin_amdgcn_ballot_w64(!all) == 0) {
                 ok = true;

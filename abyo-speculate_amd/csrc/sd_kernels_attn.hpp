@@ -78,12 +78,16 @@ void launch_attn_combine(const AttnParams &p, hipStream_t st);
 // previous launch's on these flags); status: host-visible memory that a launch
 // sets to 1 if its attention gave up waiting for the matmul (its outputs are
 // then undefined and the split counters must be cleared).  Launches sharing
-// these words must not overlap.  cus: the device's CU count.
+// these words must not overlap.  cus: the device's CU count.  fault_polls:
+// 0, or fault injection for tests: the attention waits for a number no
+// producer writes and gives up after fault_polls reads (every workgroup still
+// ends normally, and the launch reports through status).
 struct QkvAttnSync {
     unsigned *flags;
     int nflags;
     unsigned epoch;
     int *status;
+    int fault_polls;
 };
 bool qkv_attention_fits(const GemmParams &g, const AttnParams &a, int cus);
 void launch_qkv_attention(const GemmParams &g, const AttnParams &a, const QkvAttnSync &sy, int cus, hipStream_t st,

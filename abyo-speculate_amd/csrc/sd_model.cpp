@@ -585,6 +585,11 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
     if (mask_words < 1 || mask_words > 2) throw ArgError("forward: mask words");
     SD_HIP_CHECK(hipSetDevice(c.device));
     check_status();  // a fused launch of an earlier forward that gave up
+    // fault injection for tests (SD_ATTN_WAIT_TEST=<reads>): the fused
+    // launch's attention waits for a number no producer writes, gives up
+    // after that many reads, and the step ends in BackendError
+    const char *wtest = std::getenv("SD_ATTN_WAIT_TEST");
+    const int fault_polls = wtest ? std::max(1, std::atoi(wtest)) : 0;
     // stage ids | pos | mask in pinned memory with the device block's layout,
     // then one H2D copy
     stage_wait();
@@ -703,8 +708,8 @@ void Model::forward(const int *ids, const int *pos, const uint64_t *mask, int ma
                 nks_qkv = 1;
                 qa_launched = true;
                 // a launch number per launch, never 0 (the flags' initial value)
-                if (++qa_epoch == 0) ++qa_epoch;
-                const QkvAttnSync sy{qa_flags, kQaFlags, qa_epoch, qa_status_dev};
+                if (++qa_epoch >= 0x80000000u) qa_epoch = 1;
+                const QkvAttnSync sy{qa_flags, kQaFlags, qa_epoch, qa_status_dev, fault_polls};
                 if (prof_on) {
                     const int ev = prof_events();
                     launch_qkv_attention(p, a, sy, n_cus, st, LaunchTiming{ev_pool[ev], ev_pool[ev + 1]});

@@ -1306,6 +1306,9 @@ void launch_qkv_attention(const GemmParams &g, const AttnParams &a, const QkvAtt
     p.w.flags = sy.flags;
     p.w.epoch = sy.epoch;
     p.w.status = sy.status;
+    if (sy.fault_polls < 0 || sy.epoch >= 0x80000000u) throw BackendError("qkv_attention: bad synchronisation words");
+    p.w.want = sy.fault_polls ? sy.epoch | 0x80000000u : sy.epoch;
+    p.w.polls = sy.fault_polls ? sy.fault_polls : kWaitPolls;
     const dim3 grid(p.nprod + attn_small_workgroups(p.a)), block(kAttnThreads);
     if (a.hd == 128) {
         if (g.M <= 4) launch_timed(k_qkv_attn<128, 2>, grid, block, 0, st, tm, p);
