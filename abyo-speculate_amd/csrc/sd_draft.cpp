@@ -173,6 +173,7 @@ void Draft3::set_tensor(int kind, const void *host, size_t bytes) {
     if (bytes != tensor_bytes(kind)) throw ArgError("draft tensor: byte size does not match the config");
     if (!host) throw ArgError("draft tensor: null data");
     SD_D3_CHECK(hipSetDevice(cfg.device));
+    SD_D3_CHECK(hipStreamSynchronize(own));  // kernels still reading the old tensor
     if (kind == D3_D2T) {
         const int64_t *src = (const int64_t *)host;
         std::vector<int32_t> t(len[kind]);
@@ -193,6 +194,7 @@ void Draft3::get_tensor(int kind, void *host, size_t bytes) const {
     if (bytes != tensor_bytes(kind)) throw ArgError("draft tensor: byte size does not match the config");
     if (!have[kind]) throw ArgError("draft tensor not set");
     SD_D3_CHECK(hipSetDevice(cfg.device));
+    SD_D3_CHECK(hipStreamSynchronize(own));
     if (kind == D3_D2T) std::memcpy(host, d2t_host.data(), bytes);
     else SD_D3_CHECK(hipMemcpy(host, w + off[kind], bytes, hipMemcpyDeviceToHost));
 }
@@ -203,6 +205,9 @@ void Draft3::synthesize(uint64_t seed, float std_) {
         synth_f16(w + off[k], len[k], seed * 1315423911ull + (uint64_t)k * 977ull, std_, own);
         have[k] = true;
     }
+    // the draft's stream does not order with the synchronous copies of
+    // get_tensor / set_tensor: the tensors are complete when this returns
+    SD_D3_CHECK(hipStreamSynchronize(own));
     // norms 1 + N(0, 0.1) and d2t = distinct target ids, from a host generator
     std::mt19937_64 rng(seed ^ 0x9E3779B97F4A7C15ull);
     std::normal_distribution<float> nd(0.f, 0.1f);
@@ -481,6 +486,7 @@ void Draft2::set_tensor(int kind, const void *host, size_t bytes) {
     if (bytes != tensor_bytes(kind)) throw ArgError("draft tensor: byte size does not match the config");
     if (!host) throw ArgError("draft tensor: null data");
     SD_D3_CHECK(hipSetDevice(cfg.device));
+    SD_D3_CHECK(hipStreamSynchronize(own));  // kernels still reading the old tensor
     SD_D3_CHECK(hipMemcpy(w + off[kind], host, bytes, hipMemcpyHostToDevice));
     have[kind] = true;
 }
@@ -489,6 +495,7 @@ void Draft2::get_tensor(int kind, void *host, size_t bytes) const {
     if (bytes != tensor_bytes(kind)) throw ArgError("draft tensor: byte size does not match the config");
     if (!have[kind]) throw ArgError("draft tensor not set");
     SD_D3_CHECK(hipSetDevice(cfg.device));
+    SD_D3_CHECK(hipStreamSynchronize(own));
     SD_D3_CHECK(hipMemcpy(host, w + off[kind], bytes, hipMemcpyDeviceToHost));
 }
 
@@ -498,6 +505,9 @@ void Draft2::synthesize(uint64_t seed, float std_) {
         synth_f16(w + off[k], len[k], seed * 2654435761ull + (uint64_t)k * 7919ull, std_, own);
         have[k] = true;
     }
+    // the draft's stream does not order with the synchronous copies of
+    // get_tensor / set_tensor: the tensors are complete when this returns
+    SD_D3_CHECK(hipStreamSynchronize(own));
     std::mt19937_64 rng(seed ^ 0xC2B2AE3D27D4EB4Full);
     std::normal_distribution<float> nd(0.f, 0.1f);
     std::vector<uint16_t> nw(cfg.hidden);

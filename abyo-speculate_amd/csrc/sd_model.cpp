@@ -274,6 +274,7 @@ void Model::get_tensor(int layer, int kind, void *host, size_t bytes) {
     if (bytes != g) throw ArgError("buffer size does not match the tensor");
     SD_HIP_CHECK(hipSetDevice(cfg.device));
     if (t.fmt == F32) {
+        SD_HIP_CHECK(hipStreamSynchronize(st));  // the model's stream does not order with this copy
         SD_HIP_CHECK(hipMemcpy(host, t.d, g, hipMemcpyDeviceToHost));
     } else {
         uint8_t *tmp = dalloc<uint8_t>(g);
@@ -290,6 +291,7 @@ void Model::dequant_tensor(int layer, int kind, float *host) {
     SD_HIP_CHECK(hipSetDevice(cfg.device));
     const size_t n = (size_t)t.rows * t.K;
     if (t.fmt == F32) {
+        SD_HIP_CHECK(hipStreamSynchronize(st));  // the model's stream does not order with this copy
         SD_HIP_CHECK(hipMemcpy(host, t.d, n * 4, hipMemcpyDeviceToHost));
         return;
     }
