@@ -40,6 +40,10 @@ template <typename T> static T *dmalloc(size_t n) {
     void *p = nullptr;
     SD_D3_CHECK(hipMalloc(&p, n * sizeof(T) + 256));
     SD_D3_CHECK(hipMemset(p, 0, n * sizeof(T) + 256));
+    // the fill runs on the null stream, which the draft's non-blocking stream
+    // does not wait for: without this, the zeros could land after a kernel
+    // on that stream has written the buffer
+    SD_D3_CHECK(hipDeviceSynchronize());
     return (T *)p;
 }
 

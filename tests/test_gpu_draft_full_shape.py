@@ -81,11 +81,7 @@ def test_eagle3_reference_config_chain(hip):
                 ties += _gap_ties(lg_o, E3.top_k_indices(lg_d, 8), 8, float(np.max(np.abs(lg_d - lg_o))))
                 h_dev, h_or = out_d, out_o
         print(f"eagle3 near ties {ties}", flush=True)
-        # every mismatch was checked to be a near tie above; a swapped pair
-        # counts twice, and how many pairs fall inside the tie window depends
-        # on both sides' rounding (the oracle's f32 BLAS order varies with the
-        # host CPU), so the bound is one swapped pair per step
-        assert ties <= 2 * 5
+        assert ties <= 2
     finally:
         d.close()
 
